@@ -1,0 +1,161 @@
+/*
+ * smoe.h — C ABI of the MI355X (gfx950) SimpleMoE expert-layer hot path.
+ *
+ * The reference (xmpeng-dev/system-lab) ships no callable code for this path;
+ * its notes quote the call shapes of the external operators it drove on
+ * MI355X.  Each entry point below names the reference interface it replaces
+ * (file:line under the reference tree).
+ *
+ * Conventions shared by every entry point:
+ *   - returns 0 on success, a negative SMOE_EINVAL_* code on a rejected
+ *     argument (checked on the host before anything touches the GPU), or a
+ *     positive hipError_t value when a HIP launch fails;
+ *   - takes the HIP stream (hipStream_t passed as void*) last, enqueues work on
+ *     it and never synchronises, so routing counts stay on the device;
+ *   - the caller owns every buffer; the library allocates no device memory;
+ *   - bf16 tensors are passed as uint16_t (raw bf16 bits), fp8 tensors as
+ *     uint8_t holding OCP float8_e4m3fn bytes (max 448, 0x7f/0xff = NaN);
+ *   - every pointer must be 16-byte aligned; H, I, N and the GEMM K dimension
+ *     must be multiples of 128; E <= SMOE_MAX_EXPERTS.
+ *
+ * Semantics (binding for the kernels and the CPU oracle alike):
+ *   pair p = t*K + k; rows are sorted stably by expert id, ties by ascending p;
+ *   row_map[r] = p, inv_map[p] = r, offsets = exclusive scan of counts.
+ *   1x128 activation quantisation per row and 128-column group g:
+ *     amax = max|x|, s = amax/448 (fp32 RN; s = 1 when amax == 0),
+ *     q = e4m3_rne(clamp(x/s, -448, 448)); the stored scale is s.
+ *   128x128 weight quantisation applies the same rule over each block.
+ */
+#ifndef SMOE_H_
+#define SMOE_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SMOE_MAX_EXPERTS 1024
+
+enum {
+  SMOE_OK = 0,
+  SMOE_EINVAL_NULL = -1,      /* a required pointer is NULL                 */
+  SMOE_EINVAL_DIM = -2,       /* a dimension is <= 0 or out of range         */
+  SMOE_EINVAL_ALIGN128 = -3,  /* H / I / N / Kdim not a multiple of 128      */
+  SMOE_EINVAL_EXPERTS = -4,   /* E <= 0 or E > SMOE_MAX_EXPERTS              */
+  SMOE_EINVAL_WORKSPACE = -5, /* workspace NULL or smaller than required     */
+  SMOE_EINVAL_PTRALIGN = -6,  /* a pointer is not 16-byte aligned            */
+  SMOE_EINVAL_TOPK = -7,      /* K <= 0, K > E or K > 32                     */
+};
+
+/* Human-readable text for a status code (never NULL). */
+const char* smoe_strerror(int status);
+
+/* Library version string, e.g. "smoe 0.1 gfx950". */
+const char* smoe_version(void);
+
+/*
+ * Router: softmax over fp32 logits, optional per-expert selection bias,
+ * top-K by (score desc, expert id asc), weights renormalised over the K
+ * picks.  logits [T,E] f32, bias [E] f32 or NULL -> topk_idx [T,K] i32,
+ * topk_w [T,K] f32.
+ * Replaces the router "gating linear -> softmax -> top-k -> renorm"
+ * (moe/MoE_detailed_computation_dataflow.md:53-66) and the aux-loss-free
+ * selection bias (moe/MegatronCore_MoE_reading_notes.md:688-697).
+ */
+int smoe_router_topk(const float* logits, const float* bias, int T, int E, int K,
+                     int32_t* topk_idx, float* topk_w, void* stream);
+
+/*
+ * Expert sort: stable counting sort of the T*K (token, slot) pairs by expert.
+ * topk_idx [T,K] i32 -> row_map [T*K], inv_map [T*K], counts [E],
+ * offsets [E+1] (all i32).  ws must hold smoe_route_sort_workspace_size().
+ * Replaces the pack sort phase that yields pack_perm "sorted pair index ->
+ * original pair index" (notes/2026-04/2026-04-10_monolithmoe_layout_c_pack_optimization.md:56,80)
+ * and Megatron's tokens_per_expert computation in Dispatcher.permute
+ * (moe/MegatronCore_MoE_reading_notes.md:94-99), without the host .tolist()
+ * sync (summary/fp8_expert_gemm_optimization.md:190).
+ */
+size_t smoe_route_sort_workspace_size(int T, int K, int E);
+int smoe_route_sort(const int32_t* topk_idx, int T, int K, int E, int32_t* row_map,
+                    int32_t* inv_map, int32_t* counts, int32_t* offsets, void* ws,
+                    size_t ws_bytes, void* stream);
+
+/*
+ * Fused permute + 1x128 fp8 quantisation.  Each token row of x [T,H] bf16 is
+ * read once, quantised once and its fp8 bytes and scales written to the K
+ * sorted rows inv_map[t*K+k]: xq [T*K,H] u8, xs [T*K,H/128] f32.
+ * Replaces Dispatcher.permute(x, routing_map) followed by the separate
+ * quantize_fp8 launches (notes/2026-04/2026-04-21_gptoss_10_moe_fp8_grouped_gemm_diagnosis.md:38-46)
+ * with the blockwise 1x128 activation recipe
+ * (moe/MegatronCore_MoE_reading_notes.md:498-501).
+ */
+int smoe_permute_quant(const uint16_t* x, const int32_t* inv_map, int T, int H, int K,
+                       uint8_t* xq, float* xs, void* stream);
+
+/*
+ * Dispatch convenience: smoe_route_sort followed by smoe_permute_quant on one
+ * stream (no host sync).  ws as for smoe_route_sort.
+ */
+int smoe_dispatch_quant(const uint16_t* x, const int32_t* topk_idx, int T, int H, int K,
+                        int E, int32_t* row_map, int32_t* inv_map, int32_t* counts,
+                        int32_t* offsets, uint8_t* xq, float* xs, void* ws,
+                        size_t ws_bytes, void* stream);
+
+/*
+ * 128x128 blockwise fp8 weight quantisation.  w [E,N,Kdim] bf16 (Kdim
+ * contiguous, "NK" layout) -> wq [E,N,Kdim] u8, ws [E,N/128,Kdim/128] f32.
+ * Replaces the weight-cache refresh (summary/fp8_expert_gemm_optimization.md:135-143)
+ * under the 128x128 weight-block recipe (moe/MegatronCore_MoE_reading_notes.md:498-501).
+ */
+int smoe_quantize_weight_blockwise(const uint16_t* w, int E, int N, int Kdim, uint8_t* wq,
+                                   float* ws, void* stream);
+
+/*
+ * Dropless fp8 grouped GEMM with blockwise scales.  For each expert e and each
+ * row r in [offsets[e], offsets[e+1]):
+ *   c[r,n] = bf16( sum_kb as[r,kb]*bs[e,n/128,kb] * sum_{k in kb} a[r,k]*b[e,n,k] )
+ * a [R,Kdim] u8, as [R,Kdim/128] f32, b [E,N,Kdim] u8, bs [E,N/128,Kdim/128] f32,
+ * offsets [E+1] i32 on the device -> c [R,N] bf16.  Zero-token experts
+ * produce no tiles.  ws may be NULL (smoe_grouped_gemm_fp8_workspace_size
+ * returns 0).
+ * Replaces pt.ops.grouped_gemm_fp8(permuted, w1, tokens_per_expert, ...)
+ * (notes/2026-04/2026-04-21_gptoss_10_moe_fp8_grouped_gemm_diagnosis.md:39) and
+ * _fp8_fused_grouped_fwd(A_fp8, A_si, B_fp8, B_si, tpe)
+ * (summary/fp8_expert_gemm_optimization.md:121-131), with blockwise instead
+ * of per-tensor scales.
+ */
+size_t smoe_grouped_gemm_fp8_workspace_size(int E, int R, int N, int Kdim);
+int smoe_grouped_gemm_fp8(const uint8_t* a, const float* as, const uint8_t* b,
+                          const float* bs, const int32_t* offsets, int E, int R, int N,
+                          int Kdim, uint16_t* c, void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * SwiGLU + 1x128 requantisation.  c1 [R,2I] bf16 with gate columns [0,I) and
+ * up columns [I,2I): h = silu(g)*u in fp32 -> hq [R,I] u8, hs [R,I/128] f32.
+ * silu(g) = g / (1 + exp(-g)) with exp evaluated by the library's own
+ * fp32 routine (Cody-Waite reduction + degree-7 Taylor polynomial).
+ * Replaces activation_func_with_probs / the SwiGLU elementwise kernel
+ * (notes/2026-04/2026-04-21_gptoss_10_moe_fp8_grouped_gemm_diagnosis.md:46;
+ * moe/MoE_detailed_computation_dataflow.md:172-174) plus the fc2 input quant.
+ */
+int smoe_swiglu_quant(const uint16_t* c1, int R, int I, uint8_t* hq, float* hs,
+                      void* stream);
+
+/*
+ * Weighted unpermute/combine: out[t] = bf16( sum_k w[t,k] * y[inv_map[t*K+k]] )
+ * accumulated in fp32 in k order (each product and sum rounded separately).
+ * y [T*K,H] bf16, inv_map [T*K] i32, w [T,K] f32 -> out [T,H] bf16.
+ * Replaces Dispatcher.unpermute(expert_out, probs) / _unpermute_kernel
+ * (notes/2026-04/2026-04-24_gptoss_16_tier1_elementwise_tax_audit.md:69;
+ * moe/MoE_detailed_computation_dataflow.md:195).
+ */
+int smoe_unpermute_combine(const uint16_t* y, const int32_t* inv_map, const float* w,
+                           int T, int K, int H, uint16_t* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SMOE_H_ */

@@ -1,0 +1,366 @@
+"""CPU oracle for the SimpleMoE expert-layer hot path — TEST INFRASTRUCTURE ONLY.
+
+This module restates, in numpy, the semantics the MI355X kernels must match.
+It is the checker: only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import it.  The product path
+(``smoe``) never imports or calls anything here.
+
+The reference (xmpeng-dev/system-lab) holds no code for this path, only
+engineering notes describing it; every function below cites the note it
+restates.  Where the notes leave a choice open the convention is fixed here
+and is binding for the kernels too:
+
+  C1 router: probs = softmax(fp32 logits); score = probs + bias; top-K by
+     (score desc, expert id asc); w = probs[sel] / sum(probs[sel]).
+  C2 sort:   pair p = t*K + k; stable counting sort by expert id.
+  C3 quant:  per 1x128 group: amax = max|x|, s = amax/448 (s = 1 if amax == 0),
+     q = e4m3_rne(clamp(x/s, +-448)); s is stored.
+  C4 weights: C3 over each 128x128 block of W[e] stored [N, K].
+  C5 GEMM:   c[r,n] = sum_kb as[r,kb]*bs[e,n/128,kb]*sum_k a[r,k]*b[e,n,k].
+  C6 SwiGLU: h = silu(g)*u in fp32, g = c1[:, :I], u = c1[:, I:]; C3 on h.
+  C7 combine: out[t] = bf16(sum_k w[t,k]*y[inv_map[t*K+k]]), fp32, k order,
+     each product and sum rounded separately.
+
+Floating-point evaluation order is part of the contract where a kernel is
+bit-exact (router softmax reduction tree, exp routine, combine order): the
+oracle evaluates those in exactly the order the kernels do, in float32.
+
+Pinning (what checks each function; tests/test_oracle.py):
+  e4m3_encode      torch.float8_e4m3fn cast (library RNE) after clamp, over
+                   every bf16 pattern and every e4m3 rounding midpoint +-1 ulp.
+  expf32           numpy float64 exp (error bound <= 2 ulp), special values.
+  router_topk      brute-force python sort on tiny inputs; closed-form softmax.
+  route_sort       the reference's worked 16-token routing example
+                   (moe/MoE_detailed_computation_dataflow.md:74-122, counts
+                   [5,4,5,4,3,4,4,3]); permutation/stability invariants;
+                   brute-force python counting sort.
+  quant_1x128      closed forms (one-hot, constant, amax==0, +-448 saturation).
+  grouped_gemm     one-hot rows, identity blocks, single non-zero K block,
+                   zero-token experts, float64 dense matmul of the dequantised
+                   operands computed per expert independently.
+  swiglu_quant     float64 silu; silu(0)=0; silu(x)->x for large x.
+  unpermute_combine K=1, w=1 is an exact inverse permutation (bytes equal);
+                   python float32 scalar loop on tiny inputs.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+F32 = np.float32
+E4M3_MAX = F32(448.0)
+GROUP = 128
+
+# ---------------------------------------------------------------------------
+# bit-level helpers
+# ---------------------------------------------------------------------------
+
+
+def bf16_to_f32(u16: np.ndarray) -> np.ndarray:
+    """bf16 bits (uint16) -> float32 (exact)."""
+    return (np.asarray(u16, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16(x: np.ndarray) -> np.ndarray:
+    """float32 -> bf16 bits with round-to-nearest-even (NaN kept quiet)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    rounded = ((u + np.uint32(0x7FFF) + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    return np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), rounded)
+
+
+def e4m3_encode(v: np.ndarray) -> np.ndarray:
+    """float32 with |v| <= 448 -> OCP e4m3fn byte, round to nearest even.
+
+    Subnormal range (|v| < 2^-6): the code is rint(|v| * 2^9) (exact scaling,
+    RNE), which also yields 0x08 when rounding up to the smallest normal.
+    Normal range: RNE on the fp32 bit pattern to 3 mantissa bits, then rebias
+    the exponent from 127 to 7 (120 << 3 in the combined field).
+    Recipe: E4M3 activations/weights (moe/MegatronCore_MoE_reading_notes.md:498-501),
+    OCP e4m3fn with max 448 on gfx950 (summary/fp8_expert_gemm_optimization.md:202-208).
+    """
+    u = np.ascontiguousarray(v, dtype=np.float32).view(np.uint32)
+    sign = ((u >> 24) & 0x80).astype(np.uint32)
+    a = u & np.uint32(0x7FFFFFFF)
+    af = a.view(np.float32)
+    sub = af < F32(2.0 ** -6)
+    q_sub = np.rint(af * F32(512.0)).astype(np.uint32)
+    rnd = (a + np.uint32(0x7FFFF) + ((a >> 20) & 1)) >> 20
+    q_norm = rnd - np.uint32(120 << 3)
+    q = np.where(sub, q_sub, q_norm)
+    return (q | sign).astype(np.uint8)
+
+
+def e4m3_decode(q: np.ndarray) -> np.ndarray:
+    """OCP e4m3fn byte -> float32 (0x7f / 0xff -> NaN)."""
+    q = np.asarray(q, dtype=np.uint8).astype(np.int32)
+    s = np.where(q & 0x80, -1.0, 1.0)
+    e = (q >> 3) & 0xF
+    m = q & 7
+    mag = np.where(e == 0, m * 2.0 ** -9, (1.0 + m / 8.0) * np.exp2(e - 7.0))
+    out = (s * mag).astype(np.float32)
+    out[(q & 0x7F) == 0x7F] = np.nan
+    return out
+
+
+def quant_rule(x: np.ndarray, s: np.ndarray) -> np.ndarray:
+    """q = e4m3_rne(clamp(x / s, -448, 448)) in float32 (C3)."""
+    y = np.asarray(x, np.float32) / np.asarray(s, np.float32)
+    return e4m3_encode(np.clip(y, -E4M3_MAX, E4M3_MAX))
+
+
+def group_scale(amax: np.ndarray) -> np.ndarray:
+    """s = amax / 448 (fp32 RN), or 1 when amax == 0 (C3)."""
+    amax = np.asarray(amax, np.float32)
+    s = amax / E4M3_MAX
+    return np.where(amax == 0, F32(1.0), s).astype(np.float32)
+
+
+# ---------------------------------------------------------------------------
+# fp32 exp shared by the router softmax and SwiGLU
+# ---------------------------------------------------------------------------
+
+_LOG2E = F32(1.4426950408889634)
+_LN2_HI = np.uint32(0x3F317200).view(np.float32)  # 0.693145751953125, 16 significant bits
+_LN2_LO = np.uint32(0x35BFBE8E).view(np.float32)  # ln2 - LN2_HI
+_EXP_HI = F32(88.0)
+_EXP_LO = F32(-87.0)
+_TAYLOR = [F32(1.0 / 5040.0), F32(1.0 / 720.0), F32(1.0 / 120.0), F32(1.0 / 24.0),
+           F32(1.0 / 6.0), F32(0.5), F32(1.0), F32(1.0)]
+
+
+def expf32(x: np.ndarray) -> np.ndarray:
+    """exp in float32 by Cody-Waite range reduction and a degree-7 Taylor
+    polynomial (Horner), every operation a separately rounded fp32 op:
+      n = rint(x*log2e); r = (x - n*LN2_HI) - n*LN2_LO; p(r); p * 2^n.
+    x > 88 -> +inf, x < -87 -> 0.  Max error about 2 ulp over [-87, 88].
+    The HIP kernels evaluate the identical sequence (compiled with
+    -ffp-contract=off), so results are bit-identical.
+    """
+    x = np.asarray(x, np.float32)
+    xc = np.clip(x, _EXP_LO, _EXP_HI)
+    n = np.rint(xc * _LOG2E).astype(np.float32)
+    r = (xc - n * _LN2_HI).astype(np.float32)
+    r = (r - n * _LN2_LO).astype(np.float32)
+    p = _TAYLOR[0]
+    for c in _TAYLOR[1:]:
+        p = (p * r + c).astype(np.float32)
+    ni = n.astype(np.int32)
+    two_n = ((ni + 127).astype(np.uint32) << 23).view(np.float32)
+    out = (p * two_n).astype(np.float32)
+    out = np.where(x > _EXP_HI, F32(np.inf), out)
+    out = np.where(x < _EXP_LO, F32(0.0), out)
+    return out.astype(np.float32)
+
+
+# ---------------------------------------------------------------------------
+# R: router
+# ---------------------------------------------------------------------------
+
+WAVE = 64
+
+
+def _wave_tree_sum(vals: np.ndarray) -> np.ndarray:
+    """Sum over the last axis in the kernel's order: lane j accumulates
+    elements j, j+64, j+128, ... in ascending order, then an xor-butterfly
+    over lanes with offsets 32, 16, 8, 4, 2, 1 (all lanes end equal)."""
+    T, E = vals.shape
+    nchunk = (E + WAVE - 1) // WAVE
+    pad = np.zeros((T, nchunk * WAVE), np.float32)
+    pad[:, :E] = vals
+    lanes = np.zeros((T, WAVE), np.float32)
+    for c in range(nchunk):
+        lanes = (lanes + pad[:, c * WAVE:(c + 1) * WAVE]).astype(np.float32)
+    idx = np.arange(WAVE)
+    for off in (32, 16, 8, 4, 2, 1):
+        lanes = (lanes + lanes[:, idx ^ off]).astype(np.float32)
+    return lanes[:, 0]
+
+
+def softmax_f32(logits: np.ndarray) -> np.ndarray:
+    """probs = exp(l - max) / sum, fp32, sum in the wave-tree order (C1;
+    moe/MoE_detailed_computation_dataflow.md:56-58)."""
+    logits = np.asarray(logits, np.float32)
+    m = logits.max(axis=1, keepdims=True)
+    e = expf32((logits - m).astype(np.float32))
+    s = _wave_tree_sum(e)
+    return (e / s[:, None]).astype(np.float32)
+
+
+def router_topk(logits: np.ndarray, K: int, bias: np.ndarray | None = None):
+    """C1 router: softmax, optional selection bias, top-K with ties toward the
+    lower expert id, renormalised weights (sequential fp32 sum in pick order).
+    moe/MoE_detailed_computation_dataflow.md:53-66 (gate -> softmax -> top-k,
+    renorm); moe/MegatronCore_MoE_reading_notes.md:688-697 (aux-loss-free
+    bias used only for selection)."""
+    probs = softmax_f32(logits)
+    score = probs if bias is None else (probs + np.asarray(bias, np.float32)[None, :]).astype(np.float32)
+    order = np.argsort(-score, axis=1, kind="stable")[:, :K]
+    picked = np.take_along_axis(probs, order, axis=1)
+    ssum = np.zeros(picked.shape[0], np.float32)
+    for k in range(K):
+        ssum = (ssum + picked[:, k]).astype(np.float32)
+    w = (picked / ssum[:, None]).astype(np.float32)
+    return order.astype(np.int32), w
+
+
+# ---------------------------------------------------------------------------
+# K0: expert sort
+# ---------------------------------------------------------------------------
+
+
+def route_sort(topk_idx: np.ndarray, E: int):
+    """C2: stable sort of pairs p = t*K + k by expert id.
+    row_map[r] = p ("pack_perm: sorted pair index -> original pair index",
+    notes/2026-04/2026-04-10_monolithmoe_layout_c_pack_optimization.md:56,80,120),
+    inv_map[p] = r, counts[e], offsets = exclusive scan (E+1 entries)."""
+    flat = np.asarray(topk_idx, np.int32).reshape(-1)
+    row_map = np.argsort(flat, kind="stable").astype(np.int32)
+    inv_map = np.empty_like(row_map)
+    inv_map[row_map] = np.arange(flat.size, dtype=np.int32)
+    counts = np.bincount(flat, minlength=E).astype(np.int32)
+    offsets = np.zeros(E + 1, np.int32)
+    offsets[1:] = np.cumsum(counts)
+    return row_map, inv_map, counts, offsets
+
+
+# ---------------------------------------------------------------------------
+# K1 / W: quantisation
+# ---------------------------------------------------------------------------
+
+
+def quant_1x128(x: np.ndarray):
+    """C3 on rows of x [M, H] float32 (H % 128 == 0) -> q [M,H] u8, s [M,H/128] f32.
+    1x128 activation tiles: moe/MegatronCore_MoE_reading_notes.md:498-501."""
+    x = np.asarray(x, np.float32)
+    M, H = x.shape
+    g = x.reshape(M, H // GROUP, GROUP)
+    amax = np.abs(g).max(axis=2)
+    s = group_scale(amax)
+    q = quant_rule(g, s[:, :, None]).reshape(M, H)
+    return q, s
+
+
+def permute_quant(x_bf16: np.ndarray, inv_map: np.ndarray, K: int):
+    """K1: quantise each token row once (C3) and place it at the K sorted rows
+    inv_map[t*K+k].  x_bf16 [T,H] uint16 -> xq [T*K,H] u8, xs [T*K,H/128] f32."""
+    x = bf16_to_f32(x_bf16)
+    T, H = x.shape
+    q, s = quant_1x128(x)
+    R = T * K
+    xq = np.empty((R, H), np.uint8)
+    xs = np.empty((R, H // GROUP), np.float32)
+    dst = np.asarray(inv_map, np.int64).reshape(T, K)
+    for k in range(K):
+        xq[dst[:, k]] = q
+        xs[dst[:, k]] = s
+    return xq, xs
+
+
+def quantize_weight_blockwise(w_bf16: np.ndarray):
+    """C4: 128x128 blocks of W[e] in [N, K] layout (summary/fp8_expert_gemm_optimization.md:137)
+    -> wq [E,N,K] u8, ws [E,N/128,K/128] f32."""
+    w = bf16_to_f32(w_bf16)
+    E, N, Kd = w.shape
+    b = w.reshape(E, N // GROUP, GROUP, Kd // GROUP, GROUP)
+    amax = np.abs(b).max(axis=(2, 4))
+    s = group_scale(amax)
+    q = quant_rule(b, s[:, :, None, :, None]).reshape(E, N, Kd)
+    return q, s
+
+
+# ---------------------------------------------------------------------------
+# K2: grouped GEMM
+# ---------------------------------------------------------------------------
+
+
+def dequant_rows(q: np.ndarray, s: np.ndarray) -> np.ndarray:
+    """[M,K] fp8 with [M,K/128] scales -> float64."""
+    M, Kd = q.shape
+    v = e4m3_decode(q).astype(np.float64).reshape(M, Kd // GROUP, GROUP)
+    return (v * s.astype(np.float64)[:, :, None]).reshape(M, Kd)
+
+
+def dequant_weight(q: np.ndarray, s: np.ndarray) -> np.ndarray:
+    """[N,K] fp8 with [N/128,K/128] scales -> float64."""
+    N, Kd = q.shape
+    v = e4m3_decode(q).astype(np.float64).reshape(N // GROUP, GROUP, Kd // GROUP, GROUP)
+    return (v * s.astype(np.float64)[:, None, :, None]).reshape(N, Kd)
+
+
+def grouped_gemm_fp8(a, a_s, b, b_s, offsets) -> np.ndarray:
+    """C5 in float64: per expert e, rows [offsets[e], offsets[e+1]) times
+    dequantised W[e]^T.  "fp8 dot -> fp32 acc -> dequant -> bf16"
+    (summary/fp8_expert_gemm_optimization.md:89-95) applied per 128-K block;
+    dropless, zero-token experts produce nothing
+    (moe/MegatronCore_MoE_reading_notes.md:695).  Returns float64 [R, N]."""
+    R = a.shape[0]
+    E, N, _ = b.shape
+    out = np.zeros((R, N), np.float64)
+    for e in range(E):
+        lo, hi = int(offsets[e]), int(offsets[e + 1])
+        if hi <= lo:
+            continue
+        out[lo:hi] = dequant_rows(a[lo:hi], a_s[lo:hi]) @ dequant_weight(b[e], b_s[e]).T
+    return out
+
+
+# ---------------------------------------------------------------------------
+# K3: SwiGLU + requant
+# ---------------------------------------------------------------------------
+
+
+def silu_f32(g: np.ndarray) -> np.ndarray:
+    """silu(g) = g / (1 + exp(-g)) in fp32 with expf32."""
+    g = np.asarray(g, np.float32)
+    return (g / (F32(1.0) + expf32(-g)).astype(np.float32)).astype(np.float32)
+
+
+def swiglu_quant(c1_bf16: np.ndarray):
+    """C6: h = silu(g) * u in fp32 (g = columns [0,I), u = [I,2I);
+    moe/MoE_detailed_computation_dataflow.md:172-174), then C3 per 1x128."""
+    c1 = bf16_to_f32(c1_bf16)
+    I = c1.shape[1] // 2
+    h = (silu_f32(c1[:, :I]) * c1[:, I:]).astype(np.float32)
+    return quant_1x128(h)
+
+
+# ---------------------------------------------------------------------------
+# K5: combine
+# ---------------------------------------------------------------------------
+
+
+def unpermute_combine(y_bf16: np.ndarray, inv_map: np.ndarray, w: np.ndarray, K: int):
+    """C7: out[t] = bf16(sum_k w[t,k] * y[inv_map[t*K+k]]), fp32, k order
+    (moe/MoE_detailed_computation_dataflow.md:195; fp32 accumulator per
+    notes/2026-04/2026-04-10_monolithmoe_layout_c_pack_optimization.md:67)."""
+    y = bf16_to_f32(y_bf16)
+    R, H = y.shape
+    T = R // K
+    dst = np.asarray(inv_map, np.int64).reshape(T, K)
+    w = np.asarray(w, np.float32).reshape(T, K)
+    acc = np.zeros((T, H), np.float32)
+    for k in range(K):
+        acc = (acc + (w[:, k:k + 1] * y[dst[:, k]]).astype(np.float32)).astype(np.float32)
+    return f32_to_bf16(acc)
+
+
+# ---------------------------------------------------------------------------
+# M: the whole layer
+# ---------------------------------------------------------------------------
+
+
+def moe_forward(x_bf16, logits, w1q, w1s, w2q, w2s, K, bias=None):
+    """R -> K0 -> K1 -> K2(fc1) -> K3 -> K2(fc2) -> K5
+    (moe/MoE_detailed_computation_dataflow.md:295-317).  GEMM outputs are
+    rounded to bf16 between stages as the kernels do.  Returns a dict of every
+    intermediate so tests can check stage by stage."""
+    E = w1q.shape[0]
+    idx, w = router_topk(logits, K, bias)
+    row_map, inv_map, counts, offsets = route_sort(idx, E)
+    xq, xs = permute_quant(x_bf16, inv_map, K)
+    c1 = f32_to_bf16(grouped_gemm_fp8(xq, xs, w1q, w1s, offsets).astype(np.float32))
+    hq, hs = swiglu_quant(c1)
+    y = f32_to_bf16(grouped_gemm_fp8(hq, hs, w2q, w2s, offsets).astype(np.float32))
+    out = unpermute_combine(y, inv_map, w, K)
+    return dict(topk_idx=idx, topk_w=w, row_map=row_map, inv_map=inv_map, counts=counts,
+                offsets=offsets, xq=xq, xs=xs, c1=c1, hq=hq, hs=hs, y=y, out=out)

@@ -1,0 +1,126 @@
+// smoe_common.h — device helpers shared by the smoe HIP kernels (gfx950).
+//
+// Everything here is evaluated with separately rounded fp32 operations: the
+// library is compiled with -ffp-contract=off so that no multiply/add pair is
+// fused behind the source's back, and fp32 division stays IEEE correctly
+// rounded (-fhip-fp32-correctly-rounded-divide-sqrt).  This is what makes the
+// quantised bytes bit-identical to the CPU restatement of the same rules.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/smoe.h"
+
+namespace smoe {
+
+constexpr int kWave = 64;
+constexpr int kGroup = 128;  // quantisation group / weight block edge
+constexpr float kE4M3Max = 448.0f;
+
+// ---------------------------------------------------------------- bf16 ----
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 bits; NaN stays a quiet NaN.
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+// ---------------------------------------------------------------- e4m3 ----
+// OCP e4m3fn encode of |v| <= 448 with round-to-nearest-even.
+// Subnormal range |v| < 2^-6: code = rint(|v| * 2^9) (the product is exact;
+// a result of 8 is the smallest normal, 0x08, which is the correct code).
+// Normal range: RNE to 3 mantissa bits on the fp32 pattern, then rebias the
+// exponent 127 -> 7 (subtract 120 << 3 from the combined exponent|mantissa).
+__device__ __forceinline__ uint32_t e4m3_encode(float v) {
+  uint32_t u = __float_as_uint(v);
+  uint32_t sign = (u >> 24) & 0x80u;
+  uint32_t a = u & 0x7fffffffu;
+  float af = __uint_as_float(a);
+  uint32_t q;
+  if (af < 0.015625f) {
+    q = (uint32_t)__builtin_rintf(af * 512.0f);
+  } else {
+    q = ((a + 0x7ffffu + ((a >> 20) & 1u)) >> 20) - (120u << 3);
+  }
+  return q | sign;
+}
+
+// q = e4m3(clamp(x / s, +-448)).  x / s is an IEEE fp32 division.
+__device__ __forceinline__ uint32_t quant_one(float x, float s) {
+  float y = x / s;
+  y = fminf(fmaxf(y, -kE4M3Max), kE4M3Max);
+  return e4m3_encode(y);
+}
+
+// s = amax / 448 (fp32 RN), 1 when amax == 0.
+__device__ __forceinline__ float group_scale(float amax) {
+  return amax == 0.0f ? 1.0f : amax / kE4M3Max;
+}
+
+// ---------------------------------------------------------------- exp -----
+// exp in fp32: Cody-Waite reduction n = rint(x*log2e),
+// r = (x - n*LN2_HI) - n*LN2_LO with LN2_HI holding 16 significant bits (so
+// n*LN2_HI is exact), degree-7 Taylor polynomial by Horner, times 2^n built
+// from the exponent field.  x > 88 -> +inf, x < -87 -> 0.  About 1.2 ulp.
+__device__ __forceinline__ float expf32(float x) {
+  const float kLog2e = 1.4426950408889634f;
+  const float kLn2Hi = __uint_as_float(0x3f317200u);
+  const float kLn2Lo = __uint_as_float(0x35bfbe8eu);
+  if (x > 88.0f) return __builtin_inff();
+  if (x < -87.0f) return 0.0f;
+  float n = __builtin_rintf(x * kLog2e);
+  float r = x - n * kLn2Hi;
+  r = r - n * kLn2Lo;
+  float p = (float)(1.0 / 5040.0);
+  p = p * r + (float)(1.0 / 720.0);
+  p = p * r + (float)(1.0 / 120.0);
+  p = p * r + (float)(1.0 / 24.0);
+  p = p * r + (float)(1.0 / 6.0);
+  p = p * r + 0.5f;
+  p = p * r + 1.0f;
+  p = p * r + 1.0f;
+  float two_n = __uint_as_float((uint32_t)((int)n + 127) << 23);
+  return p * two_n;
+}
+
+__device__ __forceinline__ float silu32(float g) { return g / (1.0f + expf32(-g)); }
+
+// --------------------------------------------------------------- waves ----
+template <int kWidth>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+  for (int o = kWidth / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWidth));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum_tree(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = v + __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+}  // namespace smoe
+
+// ------------------------------------------------------ host validation ----
+#define SMOE_CHECK_PTR(p)                                   \
+  do {                                                      \
+    if ((p) == nullptr) return SMOE_EINVAL_NULL;            \
+    if (((uintptr_t)(p)) & 15u) return SMOE_EINVAL_PTRALIGN; \
+  } while (0)
+
+#define SMOE_RETURN_LAUNCH()                          \
+  do {                                                \
+    hipError_t err__ = hipGetLastError();             \
+    return err__ == hipSuccess ? SMOE_OK : (int)err__; \
+  } while (0)

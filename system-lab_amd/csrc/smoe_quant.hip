@@ -1,0 +1,270 @@
+// smoe_quant.hip — fused permute + 1x128 fp8 quantisation, SwiGLU + requant,
+// and 128x128 blockwise weight quantisation (gfx950).
+//
+// Row kernels (permute_quant, swiglu_quant) give one wave to one row.  A lane
+// owns 16 consecutive elements, so 8 lanes cover one 128-element group and
+// the group amax is a 3-step xor reduction inside those 8 lanes.  A wave
+// walks the row 8 groups (1024 elements) at a time; up to kUnroll such chunks
+// are loaded with 128-bit loads before any arithmetic so that every lane has
+// kUnroll*32 bytes in flight.  Each lane writes its 16 fp8 bytes as one
+// 128-bit store, and the first lane of each group writes the group's scale.
+//
+// permute_quant reads a token row once and writes the same bytes to the K
+// sorted rows inv_map[t*K + k]: the algorithmic minimum of one read of x and
+// K writes of the fp8 row.
+#include "smoe_common.h"
+
+namespace smoe {
+
+struct Q16 {
+  uint4 q;      // 16 fp8 bytes
+  float scale;  // group scale (identical in the 8 lanes of a group)
+};
+
+// Quantise 16 fp32 values owned by this lane whose group spans 8 lanes.
+__device__ __forceinline__ Q16 quant16(const float (&f)[16]) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(f[i]));
+  amax = group_max<8>(amax);
+  const float s = group_scale(amax);
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    w[i] = quant_one(f[4 * i], s) | (quant_one(f[4 * i + 1], s) << 8) |
+           (quant_one(f[4 * i + 2], s) << 16) | (quant_one(f[4 * i + 3], s) << 24);
+  }
+  Q16 r;
+  r.q = make_uint4(w[0], w[1], w[2], w[3]);
+  r.scale = s;
+  return r;
+}
+
+__device__ __forceinline__ void unpack_bf16x8(const uint4& v, float* f) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __uint_as_float(w[i] << 16);
+    f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+
+// ---------------------------------------------------------- permute_quant
+template <int kUnroll>
+__global__ __launch_bounds__(256) void permute_quant_kernel(
+    const uint16_t* __restrict__ x, const int32_t* __restrict__ inv_map, int T, int H, int K,
+    uint8_t* __restrict__ xq, float* __restrict__ xs) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const int G = H / kGroup;
+  const int R = T * K;
+  const int sub = lane & 7, gl = lane >> 3;
+  // destination rows: lane k holds inv_map[t*K + k]
+  const int my_r = lane < K ? inv_map[(size_t)t * K + lane] : 0;
+  const uint16_t* xrow = x + (size_t)t * H;
+  for (int c0 = 0; c0 * 8 < G; c0 += kUnroll) {
+    uint4 v[kUnroll][2];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int g = (c0 + u) * 8 + gl;
+      if (g < G) {
+        const uint4* src = (const uint4*)(xrow + g * kGroup + sub * 16);
+        v[u][0] = src[0];
+        v[u][1] = src[1];
+      } else {
+        v[u][0] = v[u][1] = make_uint4(0, 0, 0, 0);
+      }
+    }
+    Q16 q[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      float f[16];
+      unpack_bf16x8(v[u][0], f);
+      unpack_bf16x8(v[u][1], f + 8);
+      q[u] = quant16(f);
+    }
+    for (int k = 0; k < K; ++k) {
+      const int r = __shfl(my_r, k, kWave);
+      if ((unsigned)r >= (unsigned)R) continue;  // malformed map: never write out of range
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int g = (c0 + u) * 8 + gl;
+        if (g < G) {
+          *(uint4*)(xq + (size_t)r * H + g * kGroup + sub * 16) = q[u].q;
+          if (sub == 0) xs[(size_t)r * G + g] = q[u].scale;
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------ swiglu_quant
+template <int kUnroll>
+__global__ __launch_bounds__(256) void swiglu_quant_kernel(const uint16_t* __restrict__ c1,
+                                                           int R, int I,
+                                                           uint8_t* __restrict__ hq,
+                                                           float* __restrict__ hs) {
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= R) return;
+  const int G = I / kGroup;
+  const int sub = lane & 7, gl = lane >> 3;
+  const uint16_t* gate = c1 + (size_t)r * 2 * I;
+  const uint16_t* up = gate + I;
+  for (int c0 = 0; c0 * 8 < G; c0 += kUnroll) {
+    uint4 vg[kUnroll][2], vu[kUnroll][2];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int g = (c0 + u) * 8 + gl;
+      if (g < G) {
+        const int col = g * kGroup + sub * 16;
+        vg[u][0] = *(const uint4*)(gate + col);
+        vg[u][1] = *(const uint4*)(gate + col + 8);
+        vu[u][0] = *(const uint4*)(up + col);
+        vu[u][1] = *(const uint4*)(up + col + 8);
+      } else {
+        vg[u][0] = vg[u][1] = vu[u][0] = vu[u][1] = make_uint4(0, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      float fg[16], fu[16], h[16];
+      unpack_bf16x8(vg[u][0], fg);
+      unpack_bf16x8(vg[u][1], fg + 8);
+      unpack_bf16x8(vu[u][0], fu);
+      unpack_bf16x8(vu[u][1], fu + 8);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) h[i] = silu32(fg[i]) * fu[i];
+      const Q16 q = quant16(h);
+      const int g = (c0 + u) * 8 + gl;
+      if (g < G) {
+        *(uint4*)(hq + (size_t)r * I + g * kGroup + sub * 16) = q.q;
+        if (sub == 0) hs[(size_t)r * G + g] = q.scale;
+      }
+    }
+  }
+}
+
+// ------------------------------------------------- weight 128x128 blocks
+// One 256-thread workgroup per 128x128 block.  Thread t owns 8 chunks of 8
+// bf16 (chunk j*256+t -> block row chunk/16, column (chunk%16)*8).
+__global__ __launch_bounds__(256) void quant_weight_kernel(const uint16_t* __restrict__ w,
+                                                           int N, int Kd,
+                                                           uint8_t* __restrict__ wq,
+                                                           float* __restrict__ ws) {
+  __shared__ float wmax[4];
+  const int nb = N / kGroup, kb = Kd / kGroup;
+  const int blk = blockIdx.x;
+  const int e = blk / (nb * kb);
+  const int rem = blk - e * nb * kb;
+  const int bn = rem / kb, bk = rem - bn * kb;
+  const size_t base = ((size_t)e * N + (size_t)bn * kGroup) * Kd + (size_t)bk * kGroup;
+  float f[8][8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int ch = j * 256 + threadIdx.x;
+    const int row = ch >> 4, col = (ch & 15) * 8;
+    uint4 v = *(const uint4*)(w + base + (size_t)row * Kd + col);
+    unpack_bf16x8(v, f[j]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(f[j][i]));
+  }
+  amax = wave_max(amax);
+  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  const float s = group_scale(amax);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int ch = j * 256 + threadIdx.x;
+    const int row = ch >> 4, col = (ch & 15) * 8;
+    uint32_t lo = quant_one(f[j][0], s) | (quant_one(f[j][1], s) << 8) |
+                  (quant_one(f[j][2], s) << 16) | (quant_one(f[j][3], s) << 24);
+    uint32_t hi = quant_one(f[j][4], s) | (quant_one(f[j][5], s) << 8) |
+                  (quant_one(f[j][6], s) << 16) | (quant_one(f[j][7], s) << 24);
+    *(uint2*)(wq + base + (size_t)row * Kd + col) = make_uint2(lo, hi);
+  }
+  if (threadIdx.x == 0) ws[((size_t)e * nb + bn) * kb + bk] = s;
+}
+
+}  // namespace smoe
+
+using namespace smoe;
+
+extern "C" int smoe_permute_quant(const uint16_t* x, const int32_t* inv_map, int T, int H, int K,
+                                  uint8_t* xq, float* xs, void* stream) {
+  if (T <= 0 || H <= 0) return SMOE_EINVAL_DIM;
+  if (H % kGroup) return SMOE_EINVAL_ALIGN128;
+  if (K <= 0 || K > 32) return SMOE_EINVAL_TOPK;
+  if ((long long)T * K > 0x7fffffffLL) return SMOE_EINVAL_DIM;
+  SMOE_CHECK_PTR(x);
+  SMOE_CHECK_PTR(inv_map);
+  SMOE_CHECK_PTR(xq);
+  SMOE_CHECK_PTR(xs);
+  const int chunks = (H / kGroup + 7) / 8;
+  const dim3 grid((T + 3) / 4), block(256);
+  hipStream_t s = (hipStream_t)stream;
+#define SMOE_PQ(U) permute_quant_kernel<U><<<grid, block, 0, s>>>(x, inv_map, T, H, K, xq, xs)
+  switch (chunks) {
+    case 1: SMOE_PQ(1); break;
+    case 2: SMOE_PQ(2); break;
+    case 3: SMOE_PQ(3); break;
+    case 4: SMOE_PQ(4); break;
+    case 5: SMOE_PQ(5); break;
+    case 6: SMOE_PQ(6); break;
+    case 7: SMOE_PQ(7); break;
+    default: SMOE_PQ(8); break;
+  }
+#undef SMOE_PQ
+  SMOE_RETURN_LAUNCH();
+}
+
+extern "C" int smoe_dispatch_quant(const uint16_t* x, const int32_t* topk_idx, int T, int H,
+                                   int K, int E, int32_t* row_map, int32_t* inv_map,
+                                   int32_t* counts, int32_t* offsets, uint8_t* xq, float* xs,
+                                   void* ws, size_t ws_bytes, void* stream) {
+  if (T <= 0 || H <= 0) return SMOE_EINVAL_DIM;
+  if (H % kGroup) return SMOE_EINVAL_ALIGN128;
+  SMOE_CHECK_PTR(x);
+  SMOE_CHECK_PTR(xq);
+  SMOE_CHECK_PTR(xs);
+  int st = smoe_route_sort(topk_idx, T, K, E, row_map, inv_map, counts, offsets, ws, ws_bytes,
+                           stream);
+  if (st) return st;
+  return smoe_permute_quant(x, inv_map, T, H, K, xq, xs, stream);
+}
+
+extern "C" int smoe_swiglu_quant(const uint16_t* c1, int R, int I, uint8_t* hq, float* hs,
+                                 void* stream) {
+  if (R <= 0 || I <= 0) return SMOE_EINVAL_DIM;
+  if (I % kGroup) return SMOE_EINVAL_ALIGN128;
+  SMOE_CHECK_PTR(c1);
+  SMOE_CHECK_PTR(hq);
+  SMOE_CHECK_PTR(hs);
+  const int chunks = (I / kGroup + 7) / 8;
+  const dim3 grid((R + 3) / 4), block(256);
+  hipStream_t s = (hipStream_t)stream;
+#define SMOE_SW(U) swiglu_quant_kernel<U><<<grid, block, 0, s>>>(c1, R, I, hq, hs)
+  if (chunks <= 1) SMOE_SW(1);
+  else if (chunks <= 2) SMOE_SW(2);
+  else SMOE_SW(4);
+#undef SMOE_SW
+  SMOE_RETURN_LAUNCH();
+}
+
+extern "C" int smoe_quantize_weight_blockwise(const uint16_t* w, int E, int N, int Kdim,
+                                              uint8_t* wq, float* ws, void* stream) {
+  if (N <= 0 || Kdim <= 0) return SMOE_EINVAL_DIM;
+  if (E <= 0 || E > SMOE_MAX_EXPERTS) return SMOE_EINVAL_EXPERTS;
+  if (N % kGroup || Kdim % kGroup) return SMOE_EINVAL_ALIGN128;
+  SMOE_CHECK_PTR(w);
+  SMOE_CHECK_PTR(wq);
+  SMOE_CHECK_PTR(ws);
+  const long long blocks = (long long)E * (N / kGroup) * (Kdim / kGroup);
+  if (blocks > 0x7fffffffLL) return SMOE_EINVAL_DIM;
+  quant_weight_kernel<<<dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream>>>(w, N, Kdim,
+                                                                                      wq, ws);
+  SMOE_RETURN_LAUNCH();
+}

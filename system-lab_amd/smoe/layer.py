@@ -1,0 +1,76 @@
+"""SimpleMoE: the expert layer forward built from the smoe ops.
+
+    Route -> Dispatch (permute + 1x128 quant) -> grouped fc1 -> SwiGLU+requant
+          -> grouped fc2 -> weighted combine
+(moe/MoE_detailed_computation_dataflow.md:295-317; Megatron MoELayer stages,
+moe/MegatronCore_MoE_reading_notes.md:84-116).  EP degree 1: every expert is
+local, so dispatch is a local permute and there is no all-to-all.  The whole
+forward is stream-ordered with no host synchronisation.
+"""
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from . import ops
+
+
+class SimpleMoE(nn.Module):
+    """Dropless top-k MoE FFN with SwiGLU experts in blockwise fp8.
+
+    Parameters follow the notes' naming: ``w1`` [E, 2I, H] holds the gate
+    rows [0, I) and up rows [I, 2I) of fc1 in [N, K] layout; ``w2`` [E, H, I]
+    is fc2.  ``w_gate`` [H, E] is the router's gating linear.
+    Weights are quantised to fp8 with 128x128 block scales on first use and
+    cached (``refresh_fp8_cache`` re-quantises after an update).
+    """
+
+    def __init__(self, hidden: int, intermediate: int, num_experts: int, top_k: int,
+                 device=None, dtype=torch.bfloat16, router_bias: bool = False):
+        super().__init__()
+        self.hidden, self.intermediate = hidden, intermediate
+        self.num_experts, self.top_k = num_experts, top_k
+        kw = dict(device=device, dtype=dtype)
+        self.w_gate = nn.Parameter(torch.empty(hidden, num_experts, device=device, dtype=torch.float32))
+        self.w1 = nn.Parameter(torch.empty(num_experts, 2 * intermediate, hidden, **kw))
+        self.w2 = nn.Parameter(torch.empty(num_experts, hidden, intermediate, **kw))
+        self.register_buffer("router_bias", torch.zeros(num_experts, device=device) if router_bias else None)
+        self._fp8 = None
+
+    @torch.no_grad()
+    def reset_parameters(self, generator: torch.Generator | None = None, std: float = 0.02):
+        for p in (self.w_gate, self.w1, self.w2):
+            p.copy_(torch.randn(p.shape, generator=generator, dtype=torch.float32,
+                                device=generator.device if generator is not None else p.device).to(p) * std)
+        self._fp8 = None
+
+    @torch.no_grad()
+    def refresh_fp8_cache(self):
+        w1q, w1s = ops.quantize_weight_blockwise(self.w1.detach().contiguous())
+        w2q, w2s = ops.quantize_weight_blockwise(self.w2.detach().contiguous())
+        self._fp8 = (w1q, w1s, w2q, w2s)
+        return self._fp8
+
+    def fp8_weights(self):
+        return self._fp8 if self._fp8 is not None else self.refresh_fp8_cache()
+
+    @torch.no_grad()
+    def forward(self, x: torch.Tensor, logits: torch.Tensor | None = None,
+                return_intermediates: bool = False):
+        """x [T, H] bf16 -> y [T, H] bf16.  ``logits`` [T, E] f32 may be given
+        directly (the benchmark configs specify router logits); otherwise
+        they are x @ w_gate in fp32."""
+        if logits is None:
+            logits = x.float() @ self.w_gate
+        w1q, w1s, w2q, w2s = self.fp8_weights()
+        idx, w = ops.router_topk(logits.contiguous(), self.top_k, self.router_bias)
+        xq, xs, row_map, inv_map, counts, offsets = ops.permute_quant(x, idx, self.num_experts)
+        c1 = ops.grouped_gemm_fp8(xq, xs, w1q, w1s, offsets)
+        hq, hs = ops.swiglu_quant(c1)
+        y = ops.grouped_gemm_fp8(hq, hs, w2q, w2s, offsets)
+        out = ops.unpermute_combine(y, inv_map, w)
+        if return_intermediates:
+            return out, dict(topk_idx=idx, topk_w=w, row_map=row_map, inv_map=inv_map,
+                             counts=counts, offsets=offsets, xq=xq, xs=xs, c1=c1, hq=hq,
+                             hs=hs, y=y)
+        return out

@@ -1,0 +1,204 @@
+"""Torch-facing ops of the SimpleMoE expert-layer hot path.
+
+Each op validates its tensors, allocates outputs through torch's caching
+allocator, and enqueues HIP kernels from libsmoe.so on the current stream.
+No op synchronises with the host: routing counts and offsets stay on the
+device.  There is no CPU or PyTorch fallback — a missing library raises.
+
+Call shapes mirror the operators the reference's notes drive on MI355X:
+``grouped_gemm_fp8(permuted, w, tokens_per_expert)``
+(notes/2026-04/2026-04-21_gptoss_10_moe_fp8_grouped_gemm_diagnosis.md:39),
+``Dispatcher.permute`` / ``unpermute`` (moe/MegatronCore_MoE_reading_notes.md:94-116),
+with device-side ``offsets`` in place of a host ``tokens_per_expert`` list.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _C
+
+FP8 = torch.float8_e4m3fn
+GROUP = 128
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _check(t: torch.Tensor, name: str, dtypes, ndim: int | None = None) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be a GPU tensor (got {t.device}); the HIP kernels are the only path")
+    if t.dtype not in dtypes:
+        raise TypeError(f"{name} has dtype {t.dtype}, expected one of {dtypes}")
+    if ndim is not None and t.dim() != ndim:
+        raise ValueError(f"{name} must be {ndim}-D, got shape {tuple(t.shape)}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def _bytes(t: torch.Tensor) -> torch.Tensor:
+    """fp8 tensors are accepted as float8_e4m3fn or raw uint8."""
+    return t if t.dtype == torch.uint8 else t.view(torch.uint8)
+
+
+# ------------------------------------------------------------------ router
+def router_topk(logits: torch.Tensor, top_k: int, bias: torch.Tensor | None = None):
+    """softmax(fp32 logits) [+ bias for selection] -> top-k ids (score desc,
+    id asc) and renormalised weights.  logits [T,E] f32 -> (idx [T,K] i32,
+    w [T,K] f32).  (moe/MoE_detailed_computation_dataflow.md:53-66)"""
+    _check(logits, "logits", (torch.float32,), 2)
+    T, E = logits.shape
+    if bias is not None:
+        _check(bias, "bias", (torch.float32,), 1)
+        if bias.numel() != E:
+            raise ValueError("bias must have E entries")
+    idx = torch.empty((T, top_k), dtype=torch.int32, device=logits.device)
+    w = torch.empty((T, top_k), dtype=torch.float32, device=logits.device)
+    _C.call("smoe_router_topk", _ptr(logits), _ptr(bias), T, E, top_k, _ptr(idx), _ptr(w),
+            _stream())
+    return idx, w
+
+
+# -------------------------------------------------------------------- sort
+def route_sort(topk_idx: torch.Tensor, num_experts: int):
+    """Stable expert sort of the T*K pairs.  -> (row_map [R], inv_map [R],
+    counts [E], offsets [E+1]), all int32 on the device."""
+    _check(topk_idx, "topk_idx", (torch.int32,), 2)
+    T, K = topk_idx.shape
+    dev = topk_idx.device
+    R = T * K
+    row_map = torch.empty(R, dtype=torch.int32, device=dev)
+    inv_map = torch.empty(R, dtype=torch.int32, device=dev)
+    counts = torch.empty(num_experts, dtype=torch.int32, device=dev)
+    offsets = torch.empty(num_experts + 1, dtype=torch.int32, device=dev)
+    nbytes = _C.lib().smoe_route_sort_workspace_size(T, K, num_experts)
+    ws = torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=dev)
+    _C.call("smoe_route_sort", _ptr(topk_idx), T, K, num_experts, _ptr(row_map), _ptr(inv_map),
+            _ptr(counts), _ptr(offsets), _ptr(ws), ws.numel(), _stream())
+    return row_map, inv_map, counts, offsets
+
+
+# ---------------------------------------------------------------- dispatch
+def permute_quant_rows(x: torch.Tensor, inv_map: torch.Tensor, top_k: int):
+    """Quantise each token row of x [T,H] bf16 once (1x128 groups) and write it
+    to the rows inv_map[t*K+k].  -> (xq [T*K,H] fp8, xs [T*K,H/128] f32)."""
+    _check(x, "x", (torch.bfloat16,), 2)
+    _check(inv_map, "inv_map", (torch.int32,))
+    T, H = x.shape
+    if inv_map.numel() != T * top_k:
+        raise ValueError("inv_map must have T*K entries")
+    R = T * top_k
+    xq = torch.empty((R, H), dtype=FP8, device=x.device)
+    xs = torch.empty((R, H // GROUP), dtype=torch.float32, device=x.device)
+    _C.call("smoe_permute_quant", _ptr(x), _ptr(inv_map), T, H, top_k, _ptr(xq), _ptr(xs),
+            _stream())
+    return xq, xs
+
+
+def permute_quant(x: torch.Tensor, topk_idx: torch.Tensor, num_experts: int):
+    """Dispatcher.permute fused with 1x128 fp8 quantisation
+    (moe/MegatronCore_MoE_reading_notes.md:94-99, 498-501).
+    -> (xq, xs, row_map, inv_map, counts, offsets)."""
+    _check(x, "x", (torch.bfloat16,), 2)
+    _check(topk_idx, "topk_idx", (torch.int32,), 2)
+    T, H = x.shape
+    if topk_idx.shape[0] != T:
+        raise ValueError("topk_idx must have T rows")
+    K = topk_idx.shape[1]
+    dev = x.device
+    R = T * K
+    row_map = torch.empty(R, dtype=torch.int32, device=dev)
+    inv_map = torch.empty(R, dtype=torch.int32, device=dev)
+    counts = torch.empty(num_experts, dtype=torch.int32, device=dev)
+    offsets = torch.empty(num_experts + 1, dtype=torch.int32, device=dev)
+    xq = torch.empty((R, H), dtype=FP8, device=dev)
+    xs = torch.empty((R, H // GROUP), dtype=torch.float32, device=dev)
+    nbytes = _C.lib().smoe_route_sort_workspace_size(T, K, num_experts)
+    ws = torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=dev)
+    _C.call("smoe_dispatch_quant", _ptr(x), _ptr(topk_idx), T, H, K, num_experts,
+            _ptr(row_map), _ptr(inv_map), _ptr(counts), _ptr(offsets), _ptr(xq), _ptr(xs),
+            _ptr(ws), ws.numel(), _stream())
+    return xq, xs, row_map, inv_map, counts, offsets
+
+
+# ----------------------------------------------------------------- weights
+def quantize_weight_blockwise(w: torch.Tensor):
+    """128x128 blockwise fp8 weights.  w [E,N,K] bf16 ("NK" layout,
+    summary/fp8_expert_gemm_optimization.md:137) -> (wq [E,N,K] fp8,
+    ws [E,N/128,K/128] f32)."""
+    _check(w, "w", (torch.bfloat16,), 3)
+    E, N, Kd = w.shape
+    wq = torch.empty((E, N, Kd), dtype=FP8, device=w.device)
+    ws = torch.empty((E, N // GROUP, Kd // GROUP), dtype=torch.float32, device=w.device)
+    _C.call("smoe_quantize_weight_blockwise", _ptr(w), E, N, Kd, _ptr(wq), _ptr(ws), _stream())
+    return wq, ws
+
+
+# -------------------------------------------------------------------- GEMM
+def grouped_gemm_fp8(xq: torch.Tensor, xs: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor,
+                     offsets: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Dropless fp8 grouped GEMM: rows [offsets[e], offsets[e+1]) of xq times
+    W[e]^T with 1x128 / 128x128 scales -> bf16 [R, N].  Rows outside
+    [offsets[0], offsets[E]) are not written."""
+    for t, n in ((xq, "xq"), (wq, "wq")):
+        _check(t, n, (FP8, torch.uint8))
+    _check(xs, "xs", (torch.float32,), 2)
+    _check(ws, "ws", (torch.float32,), 3)
+    _check(offsets, "offsets", (torch.int32,), 1)
+    R, Kd = xq.shape
+    E, N, Kw = wq.shape
+    if Kw != Kd:
+        raise ValueError(f"K mismatch: xq has {Kd}, wq has {Kw}")
+    if offsets.numel() != E + 1:
+        raise ValueError("offsets must have E+1 entries")
+    if xs.shape != (R, Kd // GROUP) or ws.shape != (E, N // GROUP, Kd // GROUP):
+        raise ValueError("scale shapes do not match the operands")
+    if out is None:
+        out = torch.empty((R, N), dtype=torch.bfloat16, device=xq.device)
+    else:
+        _check(out, "out", (torch.bfloat16,), 2)
+        if out.shape != (R, N):
+            raise ValueError("out must be [R, N]")
+    _C.call("smoe_grouped_gemm_fp8", _ptr(_bytes(xq)), _ptr(xs), _ptr(_bytes(wq)), _ptr(ws),
+            _ptr(offsets), E, R, N, Kd, _ptr(out), None, 0, _stream())
+    return out
+
+
+# ------------------------------------------------------------------ SwiGLU
+def swiglu_quant(c1: torch.Tensor):
+    """h = silu(gate)*up (gate = columns [0,I), up = [I,2I)) requantised 1x128.
+    c1 [R,2I] bf16 -> (hq [R,I] fp8, hs [R,I/128] f32)."""
+    _check(c1, "c1", (torch.bfloat16,), 2)
+    R, I2 = c1.shape
+    if I2 % 2:
+        raise ValueError("c1 must have an even number of columns (gate | up)")
+    I = I2 // 2
+    hq = torch.empty((R, I), dtype=FP8, device=c1.device)
+    hs = torch.empty((R, I // GROUP), dtype=torch.float32, device=c1.device)
+    _C.call("smoe_swiglu_quant", _ptr(c1), R, I, _ptr(hq), _ptr(hs), _stream())
+    return hq, hs
+
+
+# ----------------------------------------------------------------- combine
+def unpermute_combine(y: torch.Tensor, inv_map: torch.Tensor, topk_w: torch.Tensor,
+                      out: torch.Tensor | None = None) -> torch.Tensor:
+    """out[t] = sum_k w[t,k] * y[inv_map[t*K+k]] in fp32 -> bf16 [T, H]
+    (moe/MoE_detailed_computation_dataflow.md:195)."""
+    _check(y, "y", (torch.bfloat16,), 2)
+    _check(inv_map, "inv_map", (torch.int32,))
+    _check(topk_w, "topk_w", (torch.float32,), 2)
+    T, K = topk_w.shape
+    R, H = y.shape
+    if R != T * K or inv_map.numel() != R:
+        raise ValueError("y / inv_map must have T*K rows")
+    if out is None:
+        out = torch.empty((T, H), dtype=torch.bfloat16, device=y.device)
+    _C.call("smoe_unpermute_combine", _ptr(y), _ptr(inv_map), _ptr(topk_w), T, K, H, _ptr(out),
+            _stream())
+    return out

@@ -1,0 +1,90 @@
+"""The C-ABI library loads, exports every entry point include/smoe.h
+declares, and rejects bad arguments on the host (no GPU needed: every case
+here returns before any HIP call)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from smoe import _C
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "smoe.h")
+
+
+def declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[\w\s\*]+?\b(smoe_\w+)\s*\(", text, re.M)))
+
+
+def test_header_and_binding_agree():
+    names = declared()
+    assert len(names) >= 12
+    assert sorted(_C.SIGNATURES) == names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _C.lib()
+    for n in declared():
+        assert hasattr(lib, n), n
+    assert lib.smoe_version().decode().startswith("smoe")
+
+
+def test_strerror_covers_codes():
+    lib = _C.lib()
+    for code in range(0, -8, -1):
+        assert lib.smoe_strerror(code)
+    assert b"unknown" in lib.smoe_strerror(-99)
+
+
+FAKE = 0x100000  # aligned, never dereferenced: validation fails first
+MIS = FAKE + 4
+
+
+@pytest.mark.parametrize("args,code", [
+    ((None, FAKE, 4, 256, 2, FAKE, FAKE, None), -1),      # x NULL
+    ((FAKE, FAKE, 4, 200, 2, FAKE, FAKE, None), -3),      # H % 128
+    ((FAKE, FAKE, 0, 256, 2, FAKE, FAKE, None), -2),      # T == 0
+    ((FAKE, FAKE, 4, 256, 0, FAKE, FAKE, None), -7),      # K == 0
+    ((MIS, FAKE, 4, 256, 2, FAKE, FAKE, None), -6),       # misaligned x
+])
+def test_permute_quant_rejects(args, code):
+    assert _C.lib().smoe_permute_quant(*args) == code
+
+
+def test_route_sort_rejects():
+    lib = _C.lib()
+    need = lib.smoe_route_sort_workspace_size(16, 2, 8)
+    assert need > 0
+    ok = (FAKE, 16, 2, 8, FAKE, FAKE, FAKE, FAKE)
+    assert lib.smoe_route_sort(*ok, FAKE, need - 1, None) == -5
+    assert lib.smoe_route_sort(*ok, None, need, None) == -5
+    assert lib.smoe_route_sort(FAKE, 16, 9, 8, FAKE, FAKE, FAKE, FAKE, FAKE, 1 << 20, None) == -7
+    assert lib.smoe_route_sort(FAKE, 16, 2, 0, FAKE, FAKE, FAKE, FAKE, FAKE, 1 << 20, None) == -4
+    assert lib.smoe_route_sort(FAKE, 16, 2, 2000, FAKE, FAKE, FAKE, FAKE, FAKE, 1 << 20, None) == -4
+    assert lib.smoe_route_sort(None, 16, 2, 8, FAKE, FAKE, FAKE, FAKE, FAKE, 1 << 20, None) == -1
+
+
+def test_gemm_swiglu_combine_router_reject():
+    lib = _C.lib()
+    g = lib.smoe_grouped_gemm_fp8
+    assert g(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 100, 256, 100, FAKE, None, 0, None) == -3
+    assert g(FAKE, FAKE, FAKE, FAKE, FAKE, 0, 100, 256, 256, FAKE, None, 0, None) == -4
+    assert g(FAKE, FAKE, FAKE, FAKE, None, 4, 100, 256, 256, FAKE, None, 0, None) == -1
+    assert g(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 0, 256, 256, FAKE, None, 0, None) == -2
+    assert lib.smoe_swiglu_quant(FAKE, 10, 100, FAKE, FAKE, None) == -3
+    assert lib.smoe_swiglu_quant(FAKE, 10, 128, None, FAKE, None) == -1
+    assert lib.smoe_unpermute_combine(FAKE, FAKE, FAKE, 4, 2, 130, FAKE, None) == -3
+    assert lib.smoe_unpermute_combine(FAKE, FAKE, FAKE, 4, 33, 128, FAKE, None) == -7
+    assert lib.smoe_router_topk(FAKE, None, 4, 8, 9, FAKE, FAKE, None) == -7
+    assert lib.smoe_router_topk(FAKE, None, 4, 1025, 2, FAKE, FAKE, None) == -4
+    assert lib.smoe_quantize_weight_blockwise(FAKE, 2, 128, 100, FAKE, FAKE, None) == -3
+    assert lib.smoe_grouped_gemm_fp8_workspace_size(4, 100, 256, 256) == 0
+
+
+def test_ops_refuse_cpu_tensors():
+    import torch
+    from smoe import ops
+    with pytest.raises(ValueError, match="GPU tensor"):
+        ops.router_topk(torch.zeros(4, 8), 2)

@@ -1,0 +1,289 @@
+"""Pins for the CPU oracle (no GPU).  Each check is independent of the
+oracle's own formula: a library routine, a closed form, brute force, or the
+reference's worked example."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import smoe_oracle as O
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+# ------------------------------------------------------------------ e4m3
+def _torch_e4m3(v):
+    return torch.from_numpy(np.ascontiguousarray(v, np.float32)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+
+
+def test_e4m3_encode_all_bf16_patterns_match_torch():
+    # every finite bf16 value with |v| <= 448 (torch's cast is RNE; it does
+    # not saturate, so only in-range values are compared)
+    u = np.arange(1 << 16, dtype=np.uint32)
+    v = (u << 16).view(np.float32)
+    v = v[np.isfinite(v) & (np.abs(v) <= 448)]
+    assert np.array_equal(O.e4m3_encode(v), _torch_e4m3(v))
+
+
+def test_e4m3_encode_rounding_midpoints_match_torch():
+    # midpoints between consecutive e4m3 magnitudes, and one fp32 ulp either side
+    mags = np.sort(np.unique(np.abs(O.e4m3_decode(np.arange(0x7F, dtype=np.uint8)))))
+    mid = ((mags[:-1].astype(np.float64) + mags[1:]) / 2).astype(np.float32)
+    probe = np.concatenate([mid, np.nextafter(mid, np.float32(0)), np.nextafter(mid, np.float32(1e9)), mags])
+    probe = np.concatenate([probe, -probe])
+    assert np.array_equal(O.e4m3_encode(probe), _torch_e4m3(probe))
+
+
+def test_e4m3_encode_dense_fp32_sweep_matches_torch():
+    # every 61st fp32 pattern in [0, 448] (an exhaustive sweep of all 1.1e9
+    # patterns also matches; it takes about a minute so the suite samples)
+    hi = int(np.float32(448).view(np.uint32))
+    u = np.arange(0, hi + 1, 61, dtype=np.uint32)
+    v = u.view(np.float32)
+    assert np.array_equal(O.e4m3_encode(v), _torch_e4m3(v))
+    assert np.array_equal(O.e4m3_encode(-v), _torch_e4m3(-v))
+
+
+def test_e4m3_decode_matches_torch():
+    q = np.arange(256, dtype=np.uint8)
+    ref = torch.from_numpy(q).view(torch.float8_e4m3fn).float().numpy()
+    got = O.e4m3_decode(q)
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    ok = ~np.isnan(ref)
+    assert np.array_equal(got[ok], ref[ok])
+    assert O.e4m3_decode(np.array([0x7E], np.uint8))[0] == 448.0
+
+
+def test_quant_rule_saturates():
+    s = np.float32(1.0)
+    assert O.quant_rule(np.float32(1000.0), s) == 0x7E
+    assert O.quant_rule(np.float32(-1000.0), s) == 0xFE
+    assert O.quant_rule(np.float32(449.0), s) == 0x7E
+
+
+# ---------------------------------------------------------------- bf16
+def test_bf16_roundtrip_matches_torch():
+    rng = np.random.default_rng(0)
+    x = (rng.standard_normal(100000) * 10).astype(np.float32)
+    ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(O.f32_to_bf16(x), ref)
+    assert np.array_equal(O.bf16_to_f32(ref), torch.from_numpy(x).to(torch.bfloat16).float().numpy())
+
+
+# ------------------------------------------------------------------ exp
+def test_expf32_within_2ulp_of_float64():
+    x = np.linspace(-87, 88, 400001).astype(np.float32)
+    got = O.expf32(x).astype(np.float64)
+    ref = np.exp(x.astype(np.float64))
+    ulp = np.spacing(ref.astype(np.float32)).astype(np.float64)
+    assert (np.abs(got - ref) / ulp).max() <= 2.0
+
+
+def test_expf32_special_values():
+    v = O.expf32(np.array([0.0, -0.0, 100.0, -100.0, 1.0], np.float32))
+    assert v[0] == 1.0 and v[1] == 1.0
+    assert np.isinf(v[2]) and v[3] == 0.0
+    assert abs(v[4] - np.e) < 1e-6
+
+
+# --------------------------------------------------------------- router
+def test_softmax_close_to_float64_and_tree_order():
+    rng = np.random.default_rng(1)
+    lg = rng.standard_normal((50, 256)).astype(np.float32)
+    p = O.softmax_f32(lg)
+    l64 = lg.astype(np.float64)
+    ref = np.exp(l64 - l64.max(1, keepdims=True))
+    ref /= ref.sum(1, keepdims=True)
+    assert np.abs(p - ref).max() < 1e-6
+    # the reduction tree for E <= 64 with one element per lane: brute force
+    vals = rng.random((3, 64)).astype(np.float32)
+    lanes = [list(r) for r in vals]
+    for off in (32, 16, 8, 4, 2, 1):
+        lanes = [[np.float32(r[i] + r[i ^ off]) for i in range(64)] for r in lanes]
+    assert np.array_equal(O._wave_tree_sum(vals), np.array([r[0] for r in lanes], np.float32))
+
+
+def test_router_topk_brute_force_with_ties():
+    rng = np.random.default_rng(2)
+    T, E, K = 40, 16, 4
+    lg = rng.integers(-2, 3, (T, E)).astype(np.float32)  # many exact ties
+    bias = rng.integers(-1, 2, E).astype(np.float32) * 0.0625
+    idx, w = O.router_topk(lg, K, bias)
+    p = O.softmax_f32(lg)
+    for t in range(T):
+        sc = [(float(np.float32(p[t, e] + bias[e])), e) for e in range(E)]
+        want = [e for _, e in sorted(sc, key=lambda z: (-z[0], z[1]))[:K]]
+        assert list(idx[t]) == want
+        picked = p[t, want].astype(np.float64)
+        assert np.allclose(w[t], picked / picked.sum(), rtol=1e-6)
+    assert np.allclose(w.sum(1), 1.0, atol=1e-6)
+
+
+# ----------------------------------------------------------------- sort
+def test_route_sort_reference_worked_example():
+    g = np.load(os.path.join(GOLDEN, "worked_example.npz"))
+    row_map, inv_map, counts, offsets = O.route_sort(g["topk_idx"], 8)
+    assert counts.tolist() == g["counts"].tolist() == [5, 4, 5, 4, 3, 4, 4, 3]
+    assert offsets.tolist() == [0, 5, 9, 14, 18, 21, 25, 29, 32]
+    # E0 holds t0 t2 t4 t9 t14 in token order (dataflow.md:103)
+    assert (row_map[:5] // 2).tolist() == [0, 2, 4, 9, 14]
+    # E2: t3 t4 t8 t13 t15
+    assert (row_map[9:14] // 2).tolist() == [3, 4, 8, 13, 15]
+
+
+def test_route_sort_brute_force_and_invariants():
+    rng = np.random.default_rng(3)
+    T, K, E = 300, 4, 37
+    idx = rng.integers(0, E, (T, K)).astype(np.int32)
+    idx[:, 1] = 5  # a hot expert
+    row_map, inv_map, counts, offsets = O.route_sort(idx, E)
+    brute = [p for e in range(E) for p in range(T * K) if idx.reshape(-1)[p] == e]
+    assert row_map.tolist() == brute
+    assert np.array_equal(inv_map[row_map], np.arange(T * K))
+    assert offsets[-1] == T * K and np.array_equal(np.diff(offsets), counts)
+
+
+# ---------------------------------------------------------------- quant
+def test_quant_1x128_closed_forms():
+    x = np.zeros((4, 256), np.float32)
+    x[0, 3] = -7.5                       # one-hot: -> -448, others 0
+    x[1, :128] = 0.25                    # constant group -> all 448
+    x[2, 128:] = np.linspace(-1, 1, 128)  # amax 1 -> s = 1/448
+    q, s = O.quant_1x128(x)
+    assert s[0, 0] == np.float32(7.5) / np.float32(448) and q[0, 3] == 0xFE
+    assert (q[0, np.arange(256) != 3] == 0).all() and s[0, 1] == 1.0
+    assert (q[1, :128] == 0x7E).all() and s[1, 0] == np.float32(0.25 / 448)
+    assert (q[3] == 0).all() and (s[3] == 1.0).all()  # amax == 0 -> s = 1, q = 0
+    assert q[2, 255] == 0x7E and q[2, 128] == 0xFE
+    # dequantised error within half an e4m3 ulp of the scaled value
+    rng = np.random.default_rng(4)
+    y = rng.standard_normal((64, 512)).astype(np.float32)
+    q, s = O.quant_1x128(y)
+    deq = O.dequant_rows(q, s)
+    rel = np.abs(deq - y) / np.repeat(s, 128, axis=1)
+    scaled = np.abs(y) / np.repeat(s, 128, axis=1)
+    half_ulp = np.where(scaled < 2 ** -6, 2.0 ** -10, 2.0 ** (np.floor(np.log2(np.maximum(scaled, 1e-30))) - 4))
+    assert (rel <= half_ulp * (1 + 1e-5)).all()
+
+
+def test_weight_quant_blocks_equal_flattened_groups():
+    g = np.load(os.path.join(GOLDEN, "weight_quant.npz"))
+    wq, ws = O.quantize_weight_blockwise(g["w"])
+    assert np.array_equal(wq, g["wq"]) and np.array_equal(ws, g["ws"])
+    # a 128x128 block is one group: its amax sets one scale for all 16384 values
+    w = O.bf16_to_f32(g["w"])
+    blk = w[1, 0:128, 128:256].reshape(1, -1)
+    amax = np.abs(blk).max()
+    s = np.float32(amax) / np.float32(448)
+    assert ws[1, 0, 1] == s
+    assert np.array_equal(wq[1, 0:128, 128:256].reshape(-1), O.quant_rule(blk.reshape(-1), s))
+
+
+# ----------------------------------------------------------------- GEMM
+def _rand_fp8(rng, shape):
+    q = rng.integers(0, 256, shape).astype(np.uint8)
+    q[(q & 0x7F) == 0x7F] = 0x3C  # no NaN codes
+    return q
+
+
+def test_grouped_gemm_brute_force_blocks():
+    rng = np.random.default_rng(5)
+    E, N, Kd = 3, 256, 384
+    counts = [5, 0, 9]
+    off = np.array([0, 5, 5, 14], np.int32)
+    R = 14
+    a, b = _rand_fp8(rng, (R, Kd)), _rand_fp8(rng, (E, N, Kd))
+    a_s = rng.random((R, Kd // 128)).astype(np.float32)
+    b_s = rng.random((E, N // 128, Kd // 128)).astype(np.float32)
+    got = O.grouped_gemm_fp8(a, a_s, b, b_s, off)
+    av, bv = O.e4m3_decode(a).astype(np.float64), O.e4m3_decode(b).astype(np.float64)
+    for r in range(R):
+        e = int(np.searchsorted(off, r, side="right") - 1)
+        for n in (0, 17, 128, 255):
+            ref = 0.0
+            for kb in range(Kd // 128):
+                part = float(np.dot(av[r, kb * 128:(kb + 1) * 128], bv[e, n, kb * 128:(kb + 1) * 128]))
+                ref += float(a_s[r, kb]) * float(b_s[e, n // 128, kb]) * part
+            assert abs(got[r, n] - ref) <= 1e-9 * max(1.0, abs(ref))
+    assert counts[1] == 0  # expert 1 owns no rows and nothing breaks
+
+
+def test_grouped_gemm_one_hot_and_single_block():
+    E, N, Kd = 2, 128, 256
+    a = np.zeros((4, Kd), np.uint8)
+    a[0, 5] = 0x38      # 1.0 at k=5 (block 0)
+    a[1, 200] = 0x40    # 2.0 at k=200 (block 1)
+    a_s = np.array([[1, 1], [1, 3], [2, 2], [1, 1]], np.float32)
+    b = np.zeros((E, N, Kd), np.uint8)
+    b[0, :, 5] = 0x38
+    b[1, 7, 200] = 0x48  # 4.0
+    b_s = np.ones((E, 1, 2), np.float32)
+    b_s[1, 0, 1] = 0.5
+    off = np.array([0, 1, 4], np.int32)
+    out = O.grouped_gemm_fp8(a, a_s, b, b_s, off)
+    assert (out[0] == 1.0).all()                    # row 0 -> expert 0, one-hot
+    assert out[1, 7] == 2.0 * 4.0 * 3.0 * 0.5       # scales of block 1 only
+    assert np.count_nonzero(out[1]) == 1 and not out[2:].any()
+
+
+# --------------------------------------------------------------- SwiGLU
+def test_silu_and_swiglu():
+    g = np.array([0.0, 30.0, -30.0, 1.0, -1.0], np.float32)
+    s = O.silu_f32(g)
+    assert s[0] == 0 and s[1] == 30.0 and abs(s[2]) < 1e-11
+    ref = g.astype(np.float64) / (1 + np.exp(-g.astype(np.float64)))
+    assert np.allclose(s, ref, rtol=1e-6)
+    rng = np.random.default_rng(6)
+    c1 = O.f32_to_bf16(rng.standard_normal((8, 512)).astype(np.float32) * 3)
+    hq, hs = O.swiglu_quant(c1)
+    c = O.bf16_to_f32(c1).astype(np.float64)
+    h = c[:, :256] / (1 + np.exp(-c[:, :256])) * c[:, 256:]
+    deq = O.dequant_rows(hq, hs)
+    assert np.abs(deq - h).max() <= np.abs(h).max() * 2 ** -4
+
+
+# -------------------------------------------------------------- combine
+def test_combine_identity_and_scalar_loop():
+    rng = np.random.default_rng(7)
+    T, K, H = 6, 3, 128
+    y = O.f32_to_bf16(rng.standard_normal((T * K, H)).astype(np.float32))
+    inv = rng.permutation(T * K).astype(np.int32)
+    w = rng.random((T, K)).astype(np.float32)
+    out = O.unpermute_combine(y, inv, w, K)
+    yf = O.bf16_to_f32(y)
+    for t in range(T):
+        for h in (0, 64, 127):
+            acc = np.float32(0)
+            for k in range(K):
+                acc = np.float32(acc + np.float32(w[t, k] * yf[inv[t * K + k], h]))
+            assert out[t, h] == O.f32_to_bf16(np.array([acc], np.float32))[0]
+    # K=1, w=1: exact inverse permutation
+    one = O.unpermute_combine(y, inv, np.ones((T * K, 1), np.float32), 1)
+    assert np.array_equal(one, y[inv])
+
+
+# ----------------------------------------------------------- whole layer
+def test_oracle_tiny_fixture_regression():
+    g = np.load(os.path.join(GOLDEN, "oracle_tiny.npz"))
+    res = O.moe_forward(g["x"], g["logits"], g["w1q"], g["w1s"], g["w2q"], g["w2s"], int(g["K"]))
+    for k, v in res.items():
+        assert np.array_equal(v, g[k]), k
+    # end-to-end against a float64 dense MoE on the dequantised weights
+    E = g["w1q"].shape[0]
+    x = O.bf16_to_f32(g["x"]).astype(np.float64)
+    ref = np.zeros_like(x)
+    for t in range(x.shape[0]):
+        for k in range(int(g["K"])):
+            e = g["topk_idx"][t, k]
+            w1 = O.dequant_weight(g["w1q"][e], g["w1s"][e])
+            w2 = O.dequant_weight(g["w2q"][e], g["w2s"][e])
+            c = w1 @ x[t]
+            I = c.size // 2
+            h = c[:I] / (1 + np.exp(-c[:I])) * c[I:]
+            ref[t] += g["topk_w"][t, k] * (w2 @ h)
+    out = O.bf16_to_f32(g["out"]).astype(np.float64)
+    # fp8 activations on both GEMM inputs: a few percent of the output scale
+    assert np.abs(out - ref).max() <= 0.1 * np.abs(ref).max()
+    assert np.abs(out - ref).mean() <= 0.05 * np.abs(ref).mean()
+    assert E == 4
