@@ -50,7 +50,20 @@ __device__ __forceinline__ void unpack_bf16x8(const uint4& v, float* f) {
 }
 
 // ---------------------------------------------------------- permute_quant
-template <int kUnroll>
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+
+// 128-bit store; kNT marks it non-temporal (streamed past the caches)
+template <bool kNT>
+__device__ __forceinline__ void store16(uint8_t* p, const uint4& q) {
+  if constexpr (kNT) {
+    v4u v = {q.x, q.y, q.z, q.w};
+    __builtin_nontemporal_store(v, (v4u*)p);
+  } else {
+    *(uint4*)p = q;
+  }
+}
+
+template <int kUnroll, bool kNT>
 __global__ __launch_bounds__(256) void permute_quant_kernel(
     const uint16_t* __restrict__ x, const int32_t* __restrict__ inv_map, int T, int H, int K,
     uint8_t* __restrict__ xq, float* __restrict__ xs) {
@@ -91,7 +104,7 @@ __global__ __launch_bounds__(256) void permute_quant_kernel(
       for (int u = 0; u < kUnroll; ++u) {
         const int g = (c0 + u) * 8 + gl;
         if (g < G) {
-          *(uint4*)(xq + (size_t)r * H + g * kGroup + sub * 16) = q[u].q;
+          store16<kNT>(xq + (size_t)r * H + g * kGroup + sub * 16, q[u].q);
           if (sub == 0) xs[(size_t)r * G + g] = q[u].scale;
         }
       }
@@ -206,7 +219,7 @@ extern "C" int smoe_permute_quant(const uint16_t* x, const int32_t* inv_map, int
   const int chunks = (H / kGroup + 7) / 8;
   const dim3 grid((T + 3) / 4), block(256);
   hipStream_t s = (hipStream_t)stream;
-#define SMOE_PQ(U) permute_quant_kernel<U><<<grid, block, 0, s>>>(x, inv_map, T, H, K, xq, xs)
+#define SMOE_PQ(U) permute_quant_kernel<U, false><<<grid, block, 0, s>>>(x, inv_map, T, H, K, xq, xs)
   switch (chunks) {
     case 1: SMOE_PQ(1); break;
     case 2: SMOE_PQ(2); break;

@@ -7,21 +7,21 @@
 //
 // Sort (C2): three small launches over the R = T*K (token, slot) pairs,
 // each wave owning one segment of kSeg consecutive pairs:
-//   1. route_hist  — per-segment expert histogram  hist[e][seg]
-//   2. route_scan  — exclusive scan of hist flattened expert-major, which is
-//                    exactly the first output row of (expert e, segment seg);
-//                    also writes counts and offsets
-//   3. route_rank  — each wave walks its segment in pair order, 64 pairs at a
-//                    time; lanes with equal expert ids are found by a ballot
-//                    per id bit, so the rank inside a chunk is a popcount of
-//                    lower matching lanes.  This keeps the order stable
-//                    without any global atomics.
+//   1. route_hist  — per-segment expert histogram hist[e][seg] (LDS atomics)
+//   2. route_rowscan — one wave per expert: exclusive scan of hist[e][:] in
+//                    place (the expert's rows that earlier segments own) and
+//                    counts[e]
+//   3. route_rank  — every workgroup scans counts into offsets in LDS; each
+//                    wave then walks its segment in pair order, 64 pairs at a
+//                    time (ids prefetched into registers); lanes with equal
+//                    expert ids are found with one ballot per id bit, so the
+//                    rank inside a chunk is a popcount of lower matching lanes.
+//                    Order is stable and no global atomics are used.
 #include "smoe_common.h"
 
 namespace smoe {
 
-constexpr int kSeg = 1024;           // pairs per segment (one wave)
-constexpr int kScanThreads = 1024;
+constexpr int kSeg = 512;  // pairs per segment (one wave)
 
 // ------------------------------------------------------------------ router
 template <int NC>
@@ -104,81 +104,112 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
 }
 
 // ------------------------------------------------------------------- sort
+constexpr int kPerLane = kSeg / kWave;
+
 __global__ __launch_bounds__(256) void route_hist_kernel(const int32_t* __restrict__ idx,
                                                          int R, int E, int nseg,
                                                          int32_t* __restrict__ hist) {
   extern __shared__ int32_t h_lds[];  // [4][E]
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int seg = blockIdx.x * 4 + w;
+  if (seg >= nseg) return;  // whole wave leaves; no workgroup barrier below
   int32_t* h = h_lds + w * E;
   for (int e = lane; e < E; e += kWave) h[e] = 0;
-  __builtin_amdgcn_wave_barrier();
-  const int seg = blockIdx.x * 4 + w;
-  if (seg < nseg) {
-    const int p0 = seg * kSeg;
-    const int p1 = min(p0 + kSeg, R);
-    for (int p = p0 + lane; p < p1; p += kWave) atomicAdd(&h[idx[p]], 1);
+  const int p0 = seg * kSeg;
+  int v[kPerLane];
+#pragma unroll
+  for (int i = 0; i < kPerLane; ++i) {
+    const int p = p0 + i * kWave + lane;
+    v[i] = p < R ? idx[p] : -1;
   }
   __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-  if (seg < nseg)
-    for (int e = lane; e < E; e += kWave) hist[(size_t)e * nseg + seg] = h[e];
+#pragma unroll
+  for (int i = 0; i < kPerLane; ++i)
+    if ((unsigned)v[i] < (unsigned)E) atomicAdd(&h[v[i]], 1);
+  __builtin_amdgcn_wave_barrier();
+  for (int e = lane; e < E; e += kWave) hist[(size_t)e * nseg + seg] = h[e];
 }
 
-__global__ __launch_bounds__(kScanThreads) void route_scan_kernel(int32_t* __restrict__ hist,
-                                                                  int E, int nseg, int R,
-                                                                  int32_t* __restrict__ counts,
-                                                                  int32_t* __restrict__ offsets) {
-  __shared__ int32_t part[kScanThreads];
-  const int n = E * nseg;
-  const int per = (n + kScanThreads - 1) / kScanThreads;
-  const int i0 = min(threadIdx.x * per, n), i1 = min(i0 + per, n);
-  int s = 0;
-  for (int i = i0; i < i1; ++i) s += hist[i];
-  part[threadIdx.x] = s;
-  __syncthreads();
-  // Hillis-Steele inclusive scan over the 1024 partial sums
-  for (int o = 1; o < kScanThreads; o <<= 1) {
-    int v = threadIdx.x >= o ? part[threadIdx.x - o] : 0;
-    __syncthreads();
-    part[threadIdx.x] += v;
-    __syncthreads();
+__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int u = __shfl_up(v, o, kWave);
+    if (lane >= o) v += u;
   }
-  int run = threadIdx.x ? part[threadIdx.x - 1] : 0;
-  for (int i = i0; i < i1; ++i) {
-    int v = hist[i];
-    hist[i] = run;
-    run += v;
+  return v;
+}
+
+__global__ __launch_bounds__(256) void route_rowscan_kernel(int32_t* __restrict__ hist, int E,
+                                                            int nseg,
+                                                            int32_t* __restrict__ counts) {
+  const int lane = threadIdx.x & 63;
+  const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (e >= E) return;
+  int32_t* row = hist + (size_t)e * nseg;
+  int carry = 0;
+  for (int s0 = 0; s0 < nseg; s0 += kWave) {
+    const int s = s0 + lane;
+    const int v = s < nseg ? row[s] : 0;
+    const int inc = wave_incl_scan(v, lane);
+    if (s < nseg) row[s] = carry + inc - v;
+    carry += __shfl(inc, kWave - 1, kWave);
   }
-  __syncthreads();
-  __threadfence_block();
-  for (int e = threadIdx.x; e < E; e += kScanThreads) {
-    int lo = hist[(size_t)e * nseg];
-    int hi = (e + 1 < E) ? hist[(size_t)(e + 1) * nseg] : R;
-    offsets[e] = lo;
-    counts[e] = hi - lo;
-  }
-  if (threadIdx.x == 0) offsets[E] = R;
+  if (lane == 0) counts[e] = carry;
 }
 
 __global__ __launch_bounds__(256) void route_rank_kernel(const int32_t* __restrict__ idx,
-                                                         const int32_t* __restrict__ base,
+                                                         const int32_t* __restrict__ rowpre,
+                                                         const int32_t* __restrict__ counts,
                                                          int R, int E, int nseg, int nbits,
+                                                         int32_t* __restrict__ offsets,
                                                          int32_t* __restrict__ row_map,
                                                          int32_t* __restrict__ inv_map) {
-  extern __shared__ int32_t c_lds[];  // [4][E]
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  extern __shared__ int32_t c_lds[];  // offs[E] then cur[4][E]
+  __shared__ int32_t wtot[4];
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  int32_t* offs = c_lds;
+  int32_t* cur = c_lds + E + w * E;
+  // offsets = exclusive scan of counts (each thread owns up to 4 experts)
+  const int per = (E + 255) / 256;
+  int loc[4], run = 0;
+  for (int i = 0; i < per; ++i) {
+    const int e = tid * per + i;
+    run += e < E ? counts[e] : 0;
+    loc[i] = run;
+  }
+  const int inc = wave_incl_scan(run, lane);
+  if (lane == kWave - 1) wtot[w] = inc;
+  __syncthreads();
+  int base = inc - run;
+  for (int j = 0; j < w; ++j) base += wtot[j];
+  for (int i = 0; i < per; ++i) {
+    const int e = tid * per + i;
+    if (e < E) {
+      const int ex = base + (i ? loc[i - 1] : 0);
+      offs[e] = ex;
+      if (blockIdx.x == 0) offsets[e] = ex;
+    }
+  }
+  if (blockIdx.x == 0 && tid == 0) offsets[E] = wtot[0] + wtot[1] + wtot[2] + wtot[3];
+  __syncthreads();
+
   const int seg = blockIdx.x * 4 + w;
-  if (seg >= nseg) return;  // whole wave leaves together
-  int32_t* cur = c_lds + w * E;
-  for (int e = lane; e < E; e += kWave) cur[e] = base[(size_t)e * nseg + seg];
+  if (seg >= nseg) return;
+  const int p0 = seg * kSeg;
+  int v[kPerLane];
+#pragma unroll
+  for (int i = 0; i < kPerLane; ++i) {
+    const int p = p0 + i * kWave + lane;
+    v[i] = p < R ? idx[p] : E;  // E is a sentinel id no valid lane has
+  }
+  for (int e = lane; e < E; e += kWave) cur[e] = offs[e] + rowpre[(size_t)e * nseg + seg];
   __builtin_amdgcn_wave_barrier();
   const uint64_t lt = (1ull << lane) - 1ull;
-  const int p0 = seg * kSeg;
-  const int p1 = min(p0 + kSeg, R);
-  for (int c0 = p0; c0 < p1; c0 += kWave) {
-    const int p = c0 + lane;
-    const bool valid = p < p1;
-    const int e = valid ? idx[p] : E;  // E is a sentinel id no valid lane has
+#pragma unroll
+  for (int i = 0; i < kPerLane; ++i) {
+    const int p = p0 + i * kWave + lane;
+    const int e = v[i];
+    const bool valid = (unsigned)e < (unsigned)E;
     uint64_t m = ~0ull;
     for (int b = 0; b < nbits; ++b) {
       const bool bit = (e >> b) & 1;
@@ -250,10 +281,10 @@ extern "C" int smoe_route_sort(const int32_t* topk_idx, int T, int K, int E, int
   int32_t* hist = (int32_t*)ws;
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid((nseg + 3) / 4), block(256);
-  const size_t lds = (size_t)4 * E * sizeof(int32_t);
-  route_hist_kernel<<<grid, block, lds, s>>>(topk_idx, R, E, nseg, hist);
-  route_scan_kernel<<<1, kScanThreads, 0, s>>>(hist, E, nseg, R, counts, offsets);
-  route_rank_kernel<<<grid, block, lds, s>>>(topk_idx, hist, R, E, nseg, nbits, row_map,
-                                             inv_map);
+  route_hist_kernel<<<grid, block, (size_t)4 * E * sizeof(int32_t), s>>>(topk_idx, R, E, nseg,
+                                                                        hist);
+  route_rowscan_kernel<<<dim3((E + 3) / 4), block, 0, s>>>(hist, E, nseg, counts);
+  route_rank_kernel<<<grid, block, (size_t)5 * E * sizeof(int32_t), s>>>(
+      topk_idx, hist, counts, R, E, nseg, nbits, offsets, row_map, inv_map);
   SMOE_RETURN_LAUNCH();
 }
