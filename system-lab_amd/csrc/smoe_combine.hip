@@ -9,6 +9,8 @@
 
 namespace smoe {
 
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+
 template <int kMaxK>
 __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ y,
                                                       const int32_t* __restrict__ inv_map,
@@ -56,7 +58,8 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
     o.y = f32_to_bf16(acc[2]) | (f32_to_bf16(acc[3]) << 16);
     o.z = f32_to_bf16(acc[4]) | (f32_to_bf16(acc[5]) << 16);
     o.w = f32_to_bf16(acc[6]) | (f32_to_bf16(acc[7]) << 16);
-    *(uint4*)(out + (size_t)t * H + col) = o;
+    v4u ov = {o.x, o.y, o.z, o.w};
+    __builtin_nontemporal_store(ov, (v4u*)(out + (size_t)t * H + col));
   }
 }
 

@@ -3,50 +3,58 @@
 //
 //   c[r,n] = bf16( sum_kb as[r,kb] * bs[e,n/128,kb] * sum_{k in kb} a[r,k]*b[e,n,k] )
 //
-// Tiling.  A workgroup of 256 threads (4 waves, 2x2) owns a 128-row x 128-col
-// output tile of one expert; each wave owns 64 rows x 64 cols, i.e. 2x2
-// blocks of the 32x32 fp8 MFMA (v_mfma_f32_32x32x64_f8f6f4).  The K loop steps
-// one scale block (128) at a time: two MFMAs per 32x32 block produce the
-// block's partial sum in fp32, which is then scaled by as[r,kb]*bs[e,nb,kb]
-// and added to the fp32 accumulator.  Weight rows feed the MFMA's A operand
-// and activation rows its B operand, so an output lane holds one activation
-// row r (lane % 32): the activation scale is a per-lane value and the weight
-// scale is uniform across the tile.
+// Tiling.  A workgroup of 256 threads (4 waves) owns a 256-row x 128-column
+// output tile of one expert; wave w owns rows (w>>1)*128 .. +128 and columns
+// (w&1)*64 .. +64, i.e. 8 x 4 blocks of the 16x16 fp8 MFMA with K = 128
+// (v_mfma_f32_16x16x128_f8f6f4).  One MFMA covers a whole 128-wide scale
+// block, so each block's partial sum is scaled by as[r,kb]*bs[e,nb,kb] and
+// added to the fp32 accumulator right away (4 FMAs per MFMA).  Weight rows
+// feed the MFMA's A operand and activation rows its B operand: an output lane
+// holds one activation row (lane % 16), so the activation scale is per lane
+// and the weight scale (one 128-column block per tile) is wave-uniform.
 //
-// Data movement.  Each K step loads a 128x128-byte activation tile and a
-// 128x128-byte weight tile with 128-bit global loads, stores them to LDS with
-// the 16-byte chunk index XOR-swizzled by (row & 7) so the 128-bit fragment
-// reads of 8 consecutive rows hit distinct banks, and double-buffers LDS so
-// the next step's global loads overlap this step's MFMAs (one barrier per
-// step).
+// Data movement.  Each K step stages a 256x128-byte activation tile, a
+// 128x128-byte weight tile and the 256 activation scales in LDS with direct
+// global->LDS loads (global_load_lds_dwordx4 / _dword: no VGPR round trip).
+// A lane's 16-byte chunk c of row i lands at chunk position c ^ (i & 7), so
+// the 128-bit fragment reads of 8 consecutive rows hit distinct banks.  Two
+// LDS stages: the loads of step kb+1 are issued before the MFMAs of step kb
+// and drained at the step's single barrier.
 //
-// Scheduling.  The grid covers an upper bound of m-tiles (ceil(R/128) + E)
-// times the n-tiles; each workgroup derives the per-expert m-tile prefix sum
-// from offsets[] in LDS (no host sync, no workspace) and leaves when its tile
-// index is past the real total.  Zero-token experts own no tiles; rows past
-// an expert's end are clamped on load and masked on store.
+// Scheduling.  The grid covers an upper bound of m-tiles (ceil(R/256) + E)
+// times the n-tiles, remapped so each XCD (8 per device, blocks dealt round
+// robin) works on a contiguous range of tiles, ordered in groups of kGroupM
+// m-tiles that sweep the n-tiles together (weight reuse in L2).  Every
+// workgroup derives the per-expert m-tile prefix sum from offsets[] in LDS
+// (no host sync, no workspace) and leaves when its tile index is past the
+// real total.  Zero-token experts own no tiles; rows past an expert's end are
+// clamped on load and masked on store.
 #include "smoe_common.h"
 
 namespace smoe {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v8i __attribute__((ext_vector_type(8)));
-typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-constexpr int kBM = 128;  // activation rows per tile
+constexpr int kBM = 256;  // activation rows per tile
 constexpr int kBN = 128;  // output columns per tile
 constexpr int kBK = 128;  // K per step (= scale block)
 constexpr int kThreads = 256;
-constexpr int kGroupM = 4;  // m-tiles per scheduling group (L2 reuse of weights)
-constexpr int kTileBytes = kBK;                           // bytes per LDS row
-constexpr int kStageBytes = (kBM + kBN) * kTileBytes;     // 32 KiB
+constexpr int kGroupM = 4;                      // m-tiles per scheduling group
+constexpr int kRow = kBK;                       // bytes per LDS tile row
+constexpr int kABytes = kBM * kRow;             // 32 KiB
+constexpr int kBBytes = kBN * kRow;             // 16 KiB
+constexpr int kSBytes = kBM * 4;                // 1 KiB of activation scales
+constexpr int kStage = kABytes + kBBytes + kSBytes;
 
 __device__ __forceinline__ int swz(int row, int chunk) {
-  return row * kTileBytes + ((chunk ^ (row & 7)) << 4);
+  return row * kRow + ((chunk ^ (row & 7)) << 4);
 }
 
-__device__ __forceinline__ v16f mfma_f8(v8i a, v8i b, v16f c) {
-  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+__device__ __forceinline__ v4f mfma16(v8i a, v8i b, v4f c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
 }
 
 __device__ __forceinline__ v8i lds_frag(const uint8_t* base, int row, int c0) {
@@ -55,19 +63,18 @@ __device__ __forceinline__ v8i lds_frag(const uint8_t* base, int row, int c0) {
   return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
-__global__ __launch_bounds__(kThreads) void grouped_gemm_fp8_kernel(
+__global__ __launch_bounds__(kThreads, 1) void grouped_gemm_fp8_kernel(
     const uint8_t* __restrict__ a, const float* __restrict__ as, const uint8_t* __restrict__ b,
     const float* __restrict__ bs, const int32_t* __restrict__ offsets, int E, int N, int Kd,
     int mt_bound, uint16_t* __restrict__ c) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * kStageBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * kStage];
   __shared__ int mstart[SMOE_MAX_EXPERTS + 1];
   __shared__ int wsum[kThreads / kWave];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wid = tid >> 6;
 
-  // ---- per-expert m-tile prefix sum (inclusive, mstart[e+1]) ------------
-  // each thread owns experts [tid*per, tid*per+per)
+  // ---- per-expert m-tile prefix sum (mstart[e] = first m-tile of e) -----
   const int per = (E + kThreads - 1) / kThreads;
   int loc[4];
   int run = 0;
@@ -78,7 +85,6 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_fp8_kernel(
     run += t;
     loc[i] = run;
   }
-  // wave inclusive scan of per-thread totals
   int incl = run;
 #pragma unroll
   for (int o = 1; o < kWave; o <<= 1) {
@@ -109,8 +115,7 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_fp8_kernel(
   const int nt = in_g / kGroupM;
   if (mt >= total_mt || mt >= mt_bound) return;
 
-  // expert owning m-tile mt: largest e with mstart[e] <= mt (binary search)
-  int lo = 0, hi = E;  // mstart[lo] <= mt < mstart[hi]
+  int lo = 0, hi = E;  // largest e with mstart[e] <= mt
   while (hi - lo > 1) {
     const int mid = (lo + hi) >> 1;
     if (mstart[mid] <= mt) lo = mid;
@@ -122,117 +127,97 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_fp8_kernel(
   const int n0 = nt * kBN;
   const int ksb = Kd / kBK;
 
-  // ---- global -> register loaders ---------------------------------------
-  // thread t loads 4 chunks of each tile: row = i*32 + t/8, chunk = t%8
-  const int lrow = tid >> 3, lch = tid & 7;
-  const uint8_t* ga[4];
+  // ---- direct global->LDS loaders ---------------------------------------
+  // Wave w fills 1 KiB LDS segments: A segments w*8..w*8+7, B segments
+  // w*4..w*4+3 (8 rows each), and scale rows w*64..w*64+63.  Lane i of a
+  // segment writes LDS position i: row = seg*8 + i/8, chunk slot i%8, which
+  // holds global chunk (i%8) ^ (row & 7).
+  const uint8_t* ga[8];
   const uint8_t* gb[4];
+  {
+    const int slot = lane & 7;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = min(i * 32 + lrow, rows - 1);
-    ga[i] = a + (size_t)(row0 + r) * Kd + lch * 16;
-    gb[i] = b + ((size_t)e * N + n0 + i * 32 + lrow) * Kd + lch * 16;
-  }
-  // per-lane activation scale rows for this wave's two 32-row blocks
-  const int wr = wid >> 1, wn = wid & 1;
-  const float* sa_ptr[2];
+    for (int j = 0; j < 8; ++j) {
+      const int row = (wid * 8 + j) * 8 + (lane >> 3);
+      const int ch = slot ^ (row & 7);
+      ga[j] = a + (size_t)(row0 + min(row, rows - 1)) * Kd + ch * 16;
+    }
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    const int r = min(wr * 64 + rb * 32 + (lane & 31), rows - 1);
-    sa_ptr[rb] = as + (size_t)(row0 + r) * ksb;
+    for (int j = 0; j < 4; ++j) {
+      const int row = (wid * 4 + j) * 8 + (lane >> 3);
+      const int ch = slot ^ (row & 7);
+      gb[j] = b + ((size_t)e * N + n0 + row) * Kd + ch * 16;
+    }
   }
+  const float* gs = as + (size_t)(row0 + min(wid * 64 + lane, rows - 1)) * ksb;
   const float* sb_ptr = bs + ((size_t)e * (N / kGroup) + n0 / kGroup) * ksb;
 
-  uint4 ra[4], rb_[4];
-  float sa_n[2], sb_n;
-  auto gload = [&](int kb) {
+  auto issue = [&](int kb, int buf) {
+    uint8_t* st = smem + buf * kStage;
     const size_t ko = (size_t)kb * kBK;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      ra[i] = *(const uint4*)(ga[i] + ko);
-      rb_[i] = *(const uint4*)(gb[i] + ko);
-    }
-    sa_n[0] = sa_ptr[0][kb];
-    sa_n[1] = sa_ptr[1][kb];
-    sb_n = sb_ptr[kb];
-  };
-  auto lstore = [&](int buf) {
-    uint8_t* sA = smem + buf * kStageBytes;
-    uint8_t* sB = sA + kBM * kTileBytes;
+    for (int j = 0; j < 8; ++j)
+      __builtin_amdgcn_global_load_lds((const void*)(ga[j] + ko),
+                                       (lds_ptr_t)(st + (wid * 8 + j) * 1024), 16, 0, 0);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      *(uint4*)(sA + swz(i * 32 + lrow, lch)) = ra[i];
-      *(uint4*)(sB + swz(i * 32 + lrow, lch)) = rb_[i];
-    }
+    for (int j = 0; j < 4; ++j)
+      __builtin_amdgcn_global_load_lds((const void*)(gb[j] + ko),
+                                       (lds_ptr_t)(st + kABytes + (wid * 4 + j) * 1024), 16, 0,
+                                       0);
+    __builtin_amdgcn_global_load_lds((const void*)(gs + kb),
+                                     (lds_ptr_t)(st + kABytes + kBBytes + wid * 256), 4, 0, 0);
   };
 
-  v16f acc[2][2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+  const int wr = wid >> 1, wn = wid & 1;
+  const int frow = lane & 15;
+  const int fch = (lane >> 4) * 2;
 
-  gload(0);
-  lstore(0);
-  float sa_c[2] = {sa_n[0], sa_n[1]};
-  float sb_c = sb_n;
+  v4f acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+  issue(0, 0);
   __syncthreads();
 
-  const int frow = lane & 31;
-  const int fch = (lane >> 5) * 2;
   for (int kb = 0; kb < ksb; ++kb) {
     const int buf = kb & 1;
-    if (kb + 1 < ksb) gload(kb + 1);
-    const uint8_t* sA = smem + buf * kStageBytes;
-    const uint8_t* sB = sA + kBM * kTileBytes;
-    v8i fx[2][2], fw[2][2];
+    if (kb + 1 < ksb) issue(kb + 1, buf ^ 1);
+    const uint8_t* sA = smem + buf * kStage;
+    const uint8_t* sB = sA + kABytes;
+    const float* sS = (const float*)(sB + kBBytes);
+    const float sb = sb_ptr[kb];
+    v8i fw[4];
 #pragma unroll
-    for (int kh = 0; kh < 2; ++kh) {
+    for (int j = 0; j < 4; ++j) fw[j] = lds_frag(sB, wn * 64 + j * 16 + frow, fch);
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        fx[i][kh] = lds_frag(sA, wr * 64 + i * 32 + frow, kh * 4 + fch);
-        fw[i][kh] = lds_frag(sB, wn * 64 + i * 32 + frow, kh * 4 + fch);
+    for (int i = 0; i < 8; ++i) {
+      const int r = wr * 128 + i * 16 + frow;
+      const v8i fx = lds_frag(sA, r, fch);
+      const float sc = sS[r] * sb;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const v4f p = mfma16(fw[j], fx, v4f{0.0f, 0.0f, 0.0f, 0.0f});
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[i][j][v] = __builtin_fmaf(p[v], sc, acc[i][j][v]);
       }
-    }
-    const v16f zero = {};
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-#pragma unroll
-      for (int rb = 0; rb < 2; ++rb) {
-        v16f p = mfma_f8(fw[nb][0], fx[rb][0], zero);
-        p = mfma_f8(fw[nb][1], fx[rb][1], p);
-        const float sc = sa_c[rb] * sb_c;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) acc[nb][rb][v] = __builtin_fmaf(p[v], sc, acc[nb][rb][v]);
-      }
-    }
-    if (kb + 1 < ksb) {
-      lstore(buf ^ 1);
-      sa_c[0] = sa_n[0];
-      sa_c[1] = sa_n[1];
-      sb_c = sb_n;
     }
     __syncthreads();
   }
 
-  // ---- epilogue: lane holds row (lane%32); v -> col 8*(v/4) + 4*(lane/32) + v%4
+  // ---- epilogue: lane holds row (lane%16); v -> col (lane/16)*4 + v ------
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    const int rl = wr * 64 + rb * 32 + (lane & 31);
+  for (int i = 0; i < 8; ++i) {
+    const int rl = wr * 128 + i * 16 + frow;
     if (rl >= rows) continue;
-    uint16_t* crow = c + (size_t)(row0 + rl) * N + n0 + wn * 64 + (lane >> 5) * 4;
+    uint16_t* crow = c + (size_t)(row0 + rl) * N + n0 + wn * 64 + (lane >> 4) * 4;
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-#pragma unroll
-      for (int vg = 0; vg < 4; ++vg) {
-        const v16f& q = acc[nb][rb];
-        uint2 o;
-        o.x = f32_to_bf16(q[vg * 4 + 0]) | (f32_to_bf16(q[vg * 4 + 1]) << 16);
-        o.y = f32_to_bf16(q[vg * 4 + 2]) | (f32_to_bf16(q[vg * 4 + 3]) << 16);
-        *(uint2*)(crow + nb * 32 + vg * 8) = o;
-      }
+    for (int j = 0; j < 4; ++j) {
+      uint2 o;
+      o.x = f32_to_bf16(acc[i][j][0]) | (f32_to_bf16(acc[i][j][1]) << 16);
+      o.y = f32_to_bf16(acc[i][j][2]) | (f32_to_bf16(acc[i][j][3]) << 16);
+      *(uint2*)(crow + j * 16) = o;
     }
   }
 }

@@ -152,7 +152,7 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const uint16_t* __res
       const Q16 q = quant16(h);
       const int g = (c0 + u) * 8 + gl;
       if (g < G) {
-        *(uint4*)(hq + (size_t)r * I + g * kGroup + sub * 16) = q.q;
+        store16<true>(hq + (size_t)r * I + g * kGroup + sub * 16, q.q);
         if (sub == 0) hs[(size_t)r * G + g] = q.scale;
       }
     }
@@ -219,16 +219,15 @@ extern "C" int smoe_permute_quant(const uint16_t* x, const int32_t* inv_map, int
   const int chunks = (H / kGroup + 7) / 8;
   const dim3 grid((T + 3) / 4), block(256);
   hipStream_t s = (hipStream_t)stream;
-#define SMOE_PQ(U) permute_quant_kernel<U, false><<<grid, block, 0, s>>>(x, inv_map, T, H, K, xq, xs)
+  // Up to 4 chunks (128 B per lane) in flight keeps 2+ waves per SIMD; the
+  // fp8 rows are written once and read by a later kernel, so the stores are
+  // non-temporal (measured 1.4x faster than cached stores at config 2).
+#define SMOE_PQ(U) permute_quant_kernel<U, true><<<grid, block, 0, s>>>(x, inv_map, T, H, K, xq, xs)
   switch (chunks) {
     case 1: SMOE_PQ(1); break;
     case 2: SMOE_PQ(2); break;
     case 3: SMOE_PQ(3); break;
-    case 4: SMOE_PQ(4); break;
-    case 5: SMOE_PQ(5); break;
-    case 6: SMOE_PQ(6); break;
-    case 7: SMOE_PQ(7); break;
-    default: SMOE_PQ(8); break;
+    default: SMOE_PQ(4); break;
   }
 #undef SMOE_PQ
   SMOE_RETURN_LAUNCH();
