@@ -17,9 +17,9 @@
 // 128x128-byte weight tile and the 256 activation scales in LDS with direct
 // global->LDS loads (global_load_lds_dwordx4 / _dword: no VGPR round trip).
 // A lane's 16-byte chunk c of row i lands at chunk position c ^ (i & 7), so
-// the 128-bit fragment reads of 8 consecutive rows hit distinct banks.  Two
-// LDS stages: the loads of step kb+1 are issued before the MFMAs of step kb
-// and drained at the step's single barrier.
+// the 128-bit fragment reads of 8 consecutive rows hit distinct banks.  Three
+// LDS stages: the loads of step kb+2 are issued before the MFMAs of step kb;
+// the step's single barrier waits only for step kb+1's loads.
 //
 // Scheduling.  The grid covers an upper bound of m-tiles (ceil(R/256) + E)
 // times the n-tiles, remapped so each XCD (8 per device, blocks dealt round
@@ -48,6 +48,33 @@ constexpr int kABytes = kBM * kRow;             // 32 KiB
 constexpr int kBBytes = kBN * kRow;             // 16 KiB
 constexpr int kSBytes = kBM * 4;                // 1 KiB of activation scales
 constexpr int kStage = kABytes + kBBytes + kSBytes;
+constexpr int kStages = 3;                      // LDS ring depth (3 x 49 KiB)
+constexpr int kLoadsPerStage = 13;              // per wave: 8 A + 4 B + 1 scale
+
+// s_waitcnt with vmcnt = n (n < 16), expcnt and lgkmcnt not waited on except
+// lgkmcnt(0): the encoding is vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8].
+template <int n>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  static_assert(n >= 0 && n < 16, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt(n | (7 << 4));
+}
+
+// Direct global->LDS loads issued as inline asm: lane i's 16 (or 4) bytes at
+// base + voff land at LDS address m0 + i*16 (i*4).  The compiler does not see
+// these as LDS writes, so it inserts no vmcnt(0) before the fragment reads of
+// other stages; completion is tracked explicitly with s_waitcnt vmcnt(n)
+// followed by a workgroup barrier.  No compiler-visible global loads are
+// issued inside the K loop, so the counts are exact.
+__device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff),
+               "s"(base)
+               : "memory");
+}
+__device__ __forceinline__ void dma4(const void* base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds), "v"(voff),
+               "s"(base)
+               : "memory");
+}
 
 __device__ __forceinline__ int swz(int row, int chunk) {
   return row * kRow + ((chunk ^ (row & 7)) << 4);
@@ -67,7 +94,7 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_fp8_kernel(
     const uint8_t* __restrict__ a, const float* __restrict__ as, const uint8_t* __restrict__ b,
     const float* __restrict__ bs, const int32_t* __restrict__ offsets, int E, int N, int Kd,
     int mt_bound, uint16_t* __restrict__ c) {
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * kStage];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kStages * kStage];
   __shared__ int mstart[SMOE_MAX_EXPERTS + 1];
   __shared__ int wsum[kThreads / kWave];
 
@@ -132,40 +159,39 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_fp8_kernel(
   // w*4..w*4+3 (8 rows each), and scale rows w*64..w*64+63.  Lane i of a
   // segment writes LDS position i: row = seg*8 + i/8, chunk slot i%8, which
   // holds global chunk (i%8) ^ (row & 7).
-  const uint8_t* ga[8];
-  const uint8_t* gb[4];
+  // per-lane 32-bit byte offsets from wave-uniform (SGPR) base pointers
+  const uint8_t* a_base = a + (size_t)row0 * Kd;
+  const uint8_t* b_base = b + ((size_t)e * N + n0) * Kd;
+  const float* s_base = as + (size_t)row0 * ksb;
+  uint32_t oa[8], ob[4];
   {
     const int slot = lane & 7;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int row = (wid * 8 + j) * 8 + (lane >> 3);
-      const int ch = slot ^ (row & 7);
-      ga[j] = a + (size_t)(row0 + min(row, rows - 1)) * Kd + ch * 16;
+      oa[j] = (uint32_t)(min(row, rows - 1) * Kd + ((slot ^ (row & 7)) << 4));
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int row = (wid * 4 + j) * 8 + (lane >> 3);
-      const int ch = slot ^ (row & 7);
-      gb[j] = b + ((size_t)e * N + n0 + row) * Kd + ch * 16;
+      ob[j] = (uint32_t)(row * Kd + ((slot ^ (row & 7)) << 4));
     }
   }
-  const float* gs = as + (size_t)(row0 + min(wid * 64 + lane, rows - 1)) * ksb;
+  const uint32_t os = (uint32_t)(min(wid * 64 + lane, rows - 1) * ksb) * 4u;
   const float* sb_ptr = bs + ((size_t)e * (N / kGroup) + n0 / kGroup) * ksb;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_ptr_t)smem;
 
   auto issue = [&](int kb, int buf) {
-    uint8_t* st = smem + buf * kStage;
-    const size_t ko = (size_t)kb * kBK;
+    const uint32_t st = lds0 + buf * kStage;
+    const uint8_t* ab = a_base + (size_t)kb * kBK;
+    const uint8_t* bb = b_base + (size_t)kb * kBK;
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      __builtin_amdgcn_global_load_lds((const void*)(ga[j] + ko),
-                                       (lds_ptr_t)(st + (wid * 8 + j) * 1024), 16, 0, 0);
+      dma16(ab, oa[j], __builtin_amdgcn_readfirstlane(st + (wid * 8 + j) * 1024));
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      __builtin_amdgcn_global_load_lds((const void*)(gb[j] + ko),
-                                       (lds_ptr_t)(st + kABytes + (wid * 4 + j) * 1024), 16, 0,
-                                       0);
-    __builtin_amdgcn_global_load_lds((const void*)(gs + kb),
-                                     (lds_ptr_t)(st + kABytes + kBBytes + wid * 256), 4, 0, 0);
+      dma16(bb, ob[j], __builtin_amdgcn_readfirstlane(st + kABytes + (wid * 4 + j) * 1024));
+    dma4(s_base + kb, os, __builtin_amdgcn_readfirstlane(st + kABytes + kBBytes + wid * 256));
   };
 
   const int wr = wid >> 1, wn = wid & 1;
@@ -178,12 +204,20 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_fp8_kernel(
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 
-  issue(0, 0);
-  __syncthreads();
+  // prologue: stages 0 .. kStages-2 in flight, stage 0 landed
+#pragma unroll
+  for (int s = 0; s < kStages - 1; ++s)
+    if (s < ksb) issue(s, s);
+  if (ksb > 1) wait_vm_lgkm0<kLoadsPerStage>();
+  else wait_vm_lgkm0<0>();
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 
+  int buf = 0;
   for (int kb = 0; kb < ksb; ++kb) {
-    const int buf = kb & 1;
-    if (kb + 1 < ksb) issue(kb + 1, buf ^ 1);
+    // refill the slot consumed in the previous step (free after its barrier)
+    const int nxt = kb + kStages - 1;
+    if (nxt < ksb) issue(nxt, nxt % kStages);
     const uint8_t* sA = smem + buf * kStage;
     const uint8_t* sB = sA + kABytes;
     const float* sS = (const float*)(sB + kBBytes);
@@ -203,7 +237,12 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_fp8_kernel(
         for (int v = 0; v < 4; ++v) acc[i][j][v] = __builtin_fmaf(p[v], sc, acc[i][j][v]);
       }
     }
-    __syncthreads();
+    // stage kb+1 must have landed for every wave; later stages may still fly
+    if (kb + kStages - 1 < ksb) wait_vm_lgkm0<kLoadsPerStage>();
+    else wait_vm_lgkm0<0>();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    buf = (buf + 1 == kStages) ? 0 : buf + 1;
   }
 
   // ---- epilogue: lane holds row (lane%16); v -> col (lane/16)*4 + v ------
