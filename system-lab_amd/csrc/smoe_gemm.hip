@@ -38,21 +38,35 @@ typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-constexpr int kBM = 256;  // activation rows per tile
-constexpr int kBN = 128;  // output columns per tile
 constexpr int kBK = 128;  // K per step (= scale block)
-constexpr int kThreads = 256;
-constexpr int kGroupM = 4;                      // m-tiles per scheduling group
-constexpr int kRow = kBK;                       // bytes per LDS tile row
-constexpr int kABytes = kBM * kRow;             // 32 KiB
-constexpr int kBBytes = kBN * kRow;             // 16 KiB
-constexpr int kSBytes = kBM * 4;                // 1 KiB of activation scales
-constexpr int kStage = kABytes + kBBytes + kSBytes;
-constexpr int kStages = 3;                      // LDS ring depth (3 x 49 KiB)
-constexpr int kLoadsPerStage = 13;              // per wave: 8 A + 4 B + 1 scale
+constexpr int kGroupM = 4;  // m-tiles per scheduling group
+constexpr int kRow = kBK;   // bytes per LDS tile row
 
-// s_waitcnt with vmcnt = n (n < 16), expcnt and lgkmcnt not waited on except
-// lgkmcnt(0): the encoding is vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8].
+// Tile configuration: waves form a kWR (rows) x kWN (columns) grid; each wave
+// owns kRB 16-row blocks x 4 16-column blocks (kRB*16 rows x 64 columns).
+// kStages LDS stages of (activation tile | weight tile | activation scales).
+template <int kWR_, int kWN_, int kRB_, int kStages_>
+struct Cfg {
+  static constexpr int kWR = kWR_, kWN = kWN_, kRB = kRB_, kStages = kStages_;
+  static constexpr int kWaves = kWR * kWN;
+  static constexpr int kThreads = kWaves * kWave;
+  static constexpr int kBM = kWR * kRB * 16;
+  static constexpr int kBN = kWN * 64;
+  static constexpr int kABytes = kBM * kRow;
+  static constexpr int kBBytes = kBN * kRow;
+  static constexpr int kSBytes = kBM * 4;
+  static constexpr int kStage = kABytes + kBBytes + kSBytes;
+  static constexpr int kASegs = kABytes / 1024 / kWaves;  // 1 KiB DMA segments per wave
+  static constexpr int kBSegs = kBBytes / 1024 / kWaves;
+  static constexpr int kSWaves = kBM / 64;                 // waves loading 256 B of scales
+  static_assert(kASegs * kWaves * 1024 == kABytes, "A tile split");
+  static_assert(kBSegs * kWaves * 1024 == kBBytes, "B tile split");
+  static_assert(kSWaves <= kWaves, "scale split");
+  static_assert(kStages * kStage + 4200 <= 160 * 1024, "LDS budget");
+};
+
+// s_waitcnt with vmcnt = n (n < 16), expcnt not waited on, lgkmcnt(0): the
+// encoding is vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8].
 template <int n>
 __device__ __forceinline__ void wait_vm_lgkm0() {
   static_assert(n >= 0 && n < 16, "vmcnt immediate");
@@ -90,10 +104,14 @@ __device__ __forceinline__ v8i lds_frag(const uint8_t* base, int row, int c0) {
   return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
-__global__ __launch_bounds__(kThreads, 1) void grouped_gemm_fp8_kernel(
+template <class C>
+__global__ __launch_bounds__(C::kThreads, 1) void grouped_gemm_fp8_kernel(
     const uint8_t* __restrict__ a, const float* __restrict__ as, const uint8_t* __restrict__ b,
     const float* __restrict__ bs, const int32_t* __restrict__ offsets, int E, int N, int Kd,
     int mt_bound, uint16_t* __restrict__ c) {
+  constexpr int kThreads = C::kThreads, kBM = C::kBM, kBN = C::kBN, kStage = C::kStage;
+  constexpr int kStages = C::kStages, kABytes = C::kABytes, kBBytes = C::kBBytes;
+  constexpr int kASegs = C::kASegs, kBSegs = C::kBSegs, kRB = C::kRB;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kStages * kStage];
   __shared__ int mstart[SMOE_MAX_EXPERTS + 1];
   __shared__ int wsum[kThreads / kWave];
@@ -135,7 +153,7 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_fp8_kernel(
   const int nblk = gridDim.x;  // multiple of 8
   const int bid = blockIdx.x;
   const int lin = (bid & 7) * (nblk >> 3) + (bid >> 3);
-  const int NT = N / kBN;
+  const int NT = (N + kBN - 1) / kBN;
   const int grp = lin / (kGroupM * NT);
   const int in_g = lin - grp * kGroupM * NT;
   const int mt = grp * kGroupM + (in_g % kGroupM);
@@ -155,30 +173,46 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_fp8_kernel(
   const int ksb = Kd / kBK;
 
   // ---- direct global->LDS loaders ---------------------------------------
-  // Wave w fills 1 KiB LDS segments: A segments w*8..w*8+7, B segments
-  // w*4..w*4+3 (8 rows each), and scale rows w*64..w*64+63.  Lane i of a
-  // segment writes LDS position i: row = seg*8 + i/8, chunk slot i%8, which
-  // holds global chunk (i%8) ^ (row & 7).
-  // per-lane 32-bit byte offsets from wave-uniform (SGPR) base pointers
+  // Wave w fills 1 KiB LDS segments: A segments w*kASegs.., B segments
+  // w*kBSegs.. (8 rows each), and (waves below kBM/64) scale rows w*64..+63.
+  // Lane i of a segment writes LDS position i: row = seg*8 + i/8, chunk slot
+  // i%8, which holds global chunk (i%8) ^ (row & 7).  Offsets are per-lane
+  // 32-bit byte offsets from wave-uniform (SGPR) base pointers; rows past the
+  // expert's end (A) or past N (B) are clamped to the last valid row.
   const uint8_t* a_base = a + (size_t)row0 * Kd;
   const uint8_t* b_base = b + ((size_t)e * N + n0) * Kd;
   const float* s_base = as + (size_t)row0 * ksb;
-  uint32_t oa[8], ob[4];
+  const int ncols = min(kBN, N - n0);
+  uint32_t oa[kASegs], ob[kBSegs];
   {
     const int slot = lane & 7;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int row = (wid * 8 + j) * 8 + (lane >> 3);
+    for (int j = 0; j < kASegs; ++j) {
+      const int row = (wid * kASegs + j) * 8 + (lane >> 3);
       oa[j] = (uint32_t)(min(row, rows - 1) * Kd + ((slot ^ (row & 7)) << 4));
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int row = (wid * 4 + j) * 8 + (lane >> 3);
-      ob[j] = (uint32_t)(row * Kd + ((slot ^ (row & 7)) << 4));
+    for (int j = 0; j < kBSegs; ++j) {
+      const int row = (wid * kBSegs + j) * 8 + (lane >> 3);
+      ob[j] = (uint32_t)(min(row, ncols - 1) * Kd + ((slot ^ (row & 7)) << 4));
     }
   }
-  const uint32_t os = (uint32_t)(min(wid * 64 + lane, rows - 1) * ksb) * 4u;
-  const float* sb_ptr = bs + ((size_t)e * (N / kGroup) + n0 / kGroup) * ksb;
+  const uint32_t os = (uint32_t)(min((wid % C::kSWaves) * 64 + lane, rows - 1) * ksb) * 4u;
+  const int wr = wid / C::kWN, wn = wid % C::kWN;
+  // The tile's weight-block scales (kBN/128 blocks x ksb) move to LDS before
+  // the K loop, into the expert table's space (dead from here on): a
+  // compiler-visible global load inside the loop would make the compiler drain
+  // vmcnt to zero, i.e. wait for every DMA stage in flight.
+  constexpr int kNB128 = kBN / kGroup;
+  float* sbt = (float*)mstart;
+  __syncthreads();
+  for (int i = tid; i < kNB128 * ksb; i += kThreads) {
+    const int nb = i / ksb, kb = i - nb * ksb;
+    const int blk = min(n0 / kGroup + nb, N / kGroup - 1);
+    sbt[i] = bs[((size_t)e * (N / kGroup) + blk) * ksb + kb];
+  }
+  __syncthreads();
+  const float* sb_row = sbt + ((wn * 64) / kGroup) * ksb;
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_ptr_t)smem;
 
   auto issue = [&](int kb, int buf) {
@@ -186,21 +220,24 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_fp8_kernel(
     const uint8_t* ab = a_base + (size_t)kb * kBK;
     const uint8_t* bb = b_base + (size_t)kb * kBK;
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      dma16(ab, oa[j], __builtin_amdgcn_readfirstlane(st + (wid * 8 + j) * 1024));
+    for (int j = 0; j < kASegs; ++j)
+      dma16(ab, oa[j], __builtin_amdgcn_readfirstlane(st + (wid * kASegs + j) * 1024));
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      dma16(bb, ob[j], __builtin_amdgcn_readfirstlane(st + kABytes + (wid * 4 + j) * 1024));
-    dma4(s_base + kb, os, __builtin_amdgcn_readfirstlane(st + kABytes + kBBytes + wid * 256));
+    for (int j = 0; j < kBSegs; ++j)
+      dma16(bb, ob[j],
+            __builtin_amdgcn_readfirstlane(st + kABytes + (wid * kBSegs + j) * 1024));
+    if (wid < C::kSWaves)
+      dma4(s_base + kb, os, __builtin_amdgcn_readfirstlane(st + kABytes + kBBytes + wid * 256));
   };
+  // loads one stage leaves outstanding per wave (waves 0-3 also load scales)
+  const bool scale_wave = wid < C::kSWaves;
 
-  const int wr = wid >> 1, wn = wid & 1;
   const int frow = lane & 15;
   const int fch = (lane >> 4) * 2;
 
-  v4f acc[8][4];
+  v4f acc[kRB][4];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < kRB; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 
@@ -208,8 +245,12 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_fp8_kernel(
 #pragma unroll
   for (int s = 0; s < kStages - 1; ++s)
     if (s < ksb) issue(s, s);
-  if (ksb > 1) wait_vm_lgkm0<kLoadsPerStage>();
-  else wait_vm_lgkm0<0>();
+  if (kStages > 2 && ksb > 1) {
+    if (scale_wave) wait_vm_lgkm0<kASegs + kBSegs + 1>();
+    else wait_vm_lgkm0<kASegs + kBSegs>();
+  } else {
+    wait_vm_lgkm0<0>();
+  }
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 
@@ -221,13 +262,13 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_fp8_kernel(
     const uint8_t* sA = smem + buf * kStage;
     const uint8_t* sB = sA + kABytes;
     const float* sS = (const float*)(sB + kBBytes);
-    const float sb = sb_ptr[kb];
+    const float sb = sb_row[kb];
     v8i fw[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) fw[j] = lds_frag(sB, wn * 64 + j * 16 + frow, fch);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int r = wr * 128 + i * 16 + frow;
+    for (int i = 0; i < kRB; ++i) {
+      const int r = wr * kRB * 16 + i * 16 + frow;
       const v8i fx = lds_frag(sA, r, fch);
       const float sc = sS[r] * sb;
 #pragma unroll
@@ -238,8 +279,12 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_fp8_kernel(
       }
     }
     // stage kb+1 must have landed for every wave; later stages may still fly
-    if (kb + kStages - 1 < ksb) wait_vm_lgkm0<kLoadsPerStage>();
-    else wait_vm_lgkm0<0>();
+    if (kStages > 2 && kb + kStages - 1 < ksb) {
+      if (scale_wave) wait_vm_lgkm0<kASegs + kBSegs + 1>();
+      else wait_vm_lgkm0<kASegs + kBSegs>();
+    } else {
+      wait_vm_lgkm0<0>();
+    }
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     buf = (buf + 1 == kStages) ? 0 : buf + 1;
@@ -247,12 +292,14 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_fp8_kernel(
 
   // ---- epilogue: lane holds row (lane%16); v -> col (lane/16)*4 + v ------
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int rl = wr * 128 + i * 16 + frow;
+  for (int i = 0; i < kRB; ++i) {
+    const int rl = wr * kRB * 16 + i * 16 + frow;
     if (rl >= rows) continue;
-    uint16_t* crow = c + (size_t)(row0 + rl) * N + n0 + wn * 64 + (lane >> 4) * 4;
+    const int cl = wn * 64 + (lane >> 4) * 4;
+    uint16_t* crow = c + (size_t)(row0 + rl) * N + n0 + cl;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
+      if (cl + j * 16 >= ncols) continue;
       uint2 o;
       o.x = f32_to_bf16(acc[i][j][0]) | (f32_to_bf16(acc[i][j][1]) << 16);
       o.y = f32_to_bf16(acc[i][j][2]) | (f32_to_bf16(acc[i][j][3]) << 16);
@@ -260,6 +307,11 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_fp8_kernel(
     }
   }
 }
+
+#ifndef SMOE_GEMM_CFG
+#define SMOE_GEMM_CFG Cfg<2, 4, 8, 2>
+#endif
+using GemmCfg = SMOE_GEMM_CFG;
 
 }  // namespace smoe
 
@@ -278,19 +330,21 @@ extern "C" int smoe_grouped_gemm_fp8(const uint8_t* a, const float* as, const ui
   if (R <= 0 || N <= 0 || Kdim <= 0) return SMOE_EINVAL_DIM;
   if (E <= 0 || E > SMOE_MAX_EXPERTS) return SMOE_EINVAL_EXPERTS;
   if (N % kGroup || Kdim % kGroup) return SMOE_EINVAL_ALIGN128;
+  if (Kdim > 65536) return SMOE_EINVAL_DIM;  // weight-scale table fits the LDS expert table
   SMOE_CHECK_PTR(a);
   SMOE_CHECK_PTR(b);
   SMOE_CHECK_PTR(c);
   if (!as || !bs || !offsets) return SMOE_EINVAL_NULL;
   if (((uintptr_t)as | (uintptr_t)bs | (uintptr_t)offsets) & 3u) return SMOE_EINVAL_PTRALIGN;
-  const long long mt_bound = (R + kBM - 1) / kBM + E;
-  const long long NT = N / kBN;
+  using C = GemmCfg;
+  const long long mt_bound = (R + C::kBM - 1) / C::kBM + E;
+  const long long NT = (N + C::kBN - 1) / C::kBN;
   // pad the m-tile count to whole scheduling groups, the grid to a multiple of 8
   const long long mt_pad = (mt_bound + kGroupM - 1) / kGroupM * kGroupM;
   long long nblk = mt_pad * NT;
   nblk = (nblk + 7) / 8 * 8;
   if (nblk > 0x7fffffffLL) return SMOE_EINVAL_DIM;
-  grouped_gemm_fp8_kernel<<<dim3((unsigned)nblk), dim3(kThreads), 0, (hipStream_t)stream>>>(
+  grouped_gemm_fp8_kernel<C><<<dim3((unsigned)nblk), dim3(C::kThreads), 0, (hipStream_t)stream>>>(
       a, as, b, bs, offsets, E, N, Kdim, (int)mt_bound, c);
   SMOE_RETURN_LAUNCH();
 }
