@@ -30,6 +30,9 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "system-lab_amd"))
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per permute_quant launch at config 2 from rocprofv3 FETCH_SIZE
+# (x2.0 copy calibration) + WRITE_SIZE (x1.0): profiles/permute_quant_cfg2.md
+PERMUTE_TRAFFIC_BYTES = 1_212_500_000
 FP8_PEAK_TFLOPS = 5000.0
 
 
@@ -154,6 +157,30 @@ def bench_layer(dev, steps, warmup):
             "ms": round(t, 4), "tflops": round(fl / (t * 1e-3) / 1e12, 1)}
 
 
+def run_only(args, dev, c):
+    """One kernel family, for profiler runs: permute = the dispatch step
+    (route sort + permute_quant), gemm = DSv3 fc1 + fc2, combine = config-2
+    sized combine, copy = a plain 1 GiB device copy (calibrates the
+    FETCH_SIZE / WRITE_SIZE counters against known traffic)."""
+    import torch
+    from smoe import ops, workloads as W
+    if args.only == "copy":
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        ms = timed(lambda: dst.copy_(src), args.steps, args.warmup)
+        print(json.dumps({"only": "copy", "bytes_read": 1 << 30, "bytes_written": 1 << 30, "ms": ms}))
+    elif args.only == "permute":
+        x = W.tokens(c.T, c.H, device=dev, outliers=True)
+        idx, _ = ops.router_topk(W.logits(c.T, c.E, device=dev), c.K, W.router_bias(c.E, device=dev))
+        ms = timed(lambda: ops.permute_quant(x, idx, c.E), args.steps, args.warmup)
+        print(json.dumps({"only": "permute", "ms": ms,
+                          "gbs": dispatch_bytes(c.T, c.H, c.E, c.K) / (ms * 1e-3) / 1e9}))
+    elif args.only == "gemm":
+        print(json.dumps({"only": "gemm", **bench_gemm(dev, args.steps, args.warmup)}))
+    else:
+        print(json.dumps({"only": "combine", **bench_combine(dev, c, args.steps, args.warmup)}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -161,6 +188,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-extra", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--only", choices=["permute", "gemm", "combine", "copy"],
+                    help="run one kernel family only (for rocprofv3 runs) and print its timing")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has expert-parallel degree 1 "
@@ -173,6 +202,8 @@ def main():
     smoe._C.lib()  # fail loudly when the HIP library is missing
     dev = torch.device("cuda:0")
     c = W.CONFIGS["permute"]
+    if args.only:
+        return run_only(args, dev, c)
 
     x = W.tokens(c.T, c.H, device=dev, outliers=True)
     idx, _ = ops.router_topk(W.logits(c.T, c.E, device=dev), c.K, W.router_bias(c.E, device=dev))
@@ -215,9 +246,10 @@ def main():
     pk_bytes = permute_kernel_bytes(c.T, c.H, c.K)
     pk_gbs = pk_bytes / (pk_ms * 1e-3) / 1e9
     log(f"permute_quant kernel {pk_ms:.4f} ms  {pk_gbs:.1f} GB/s")
-    roof = {"kernel": "smoe::permute_quant_kernel<7>", "bound": "hbm", "achieved": round(pk_gbs, 1),
+    roof = {"kernel": "smoe::permute_quant_kernel<4, true>", "bound": "hbm", "achieved": round(pk_gbs, 1),
             "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(pk_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None, "kernel_ms": round(pk_ms, 4), "bytes_per_launch": pk_bytes}
+            "traffic": PERMUTE_TRAFFIC_BYTES, "kernel_ms": round(pk_ms, 4),
+            "bytes_per_launch": pk_bytes}
     del x, xq, xs
     torch.cuda.empty_cache()
 
