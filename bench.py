@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the SimpleMoE expert-layer hot path on one MI355X.
 
-Headline (the metric's quoted configuration): one step is
+Headline (benchmark config 2, the permute+quantise shape the metric is quoted on): one step is
 the dispatch of one batch — stable expert sort + fused permute/1x128 fp8
 quantisation — for T=16384 tokens, H=7168, E=256, top-8, inputs resident in
 HBM.  ``value`` is the algorithmic HBM traffic of that step
@@ -12,7 +12,7 @@ Also reported on the same line:
                 events on the launch stream, algorithmic bytes / duration;
   cpu_baseline  the numpy oracle (route sort + permute-quantise) on a bounded
                 sample of the same workload, on this host's cores;
-  extra         fp8 grouped GEMM TFLOPS on BASELINE config 4 (DeepSeek-V3
+  extra         fp8 grouped GEMM TFLOPS on benchmark config 4 (DeepSeek-V3
                 local experts, Zipf loads, fc1 + fc2), the combine GB/s at
                 config-2 size, and the whole SimpleMoE forward of config 3.
 

@@ -4,7 +4,7 @@ Seeds: 0 activations, 1 router logits, 2 router bias, 3 weights, 4 grads,
 5 expert-id shuffle.  Generators run on the requested device; CPU generation
 is bit-reproducible everywhere and is what the parity tests use.
 
-Configurations:
+Benchmark configurations 1-5:
   tiny     T=2048  H=1024 E=8   K=2 I=2048     whole layer, CPU-checkable
   permute  T=16384 H=7168 E=256 K=8            permute + quantise (headline)
   mixtral  T=8192  H=4096 E=8   K=2 I=14336    whole layer

@@ -171,7 +171,7 @@ def test_permute_quant_zero_and_saturating_groups(dev):
 
 
 def test_permute_quant_config2_full(dev):
-    """BASELINE config 2 at full size (T=16384, H=7168, E=256, top-8, bias,
+    """Benchmark config 2 at full size (T=16384, H=7168, E=256, top-8, bias,
     outliers): ids, maps, counts, fp8 bytes and scales all bit-exact."""
     say("permute_quant config2 full")
     c = W.CONFIGS["permute"]
@@ -261,7 +261,7 @@ def test_gemm_skewed_experts(dev, counts, N, Kd):
 
 
 def test_gemm_dsv3_shape_sampled_rows(dev):
-    """BASELINE config 4 at full size (R=65536, 32 experts, Zipf loads with
+    """Benchmark config 4 at full size (R=65536, 32 experts, Zipf loads with
     zero-token experts, fc1 N=4096 K=7168 and fc2 N=7168 K=2048); the oracle
     checks a sample of rows from every non-empty expert."""
     say("gemm dsv3 full")
@@ -355,7 +355,7 @@ def test_layer_golden_fixture_stagewise(dev):
 
 
 def test_simple_moe_config1_end_to_end(dev):
-    """BASELINE config 1 (T=2048, H=1024, E=8, top-2, I=2048) through
+    """Benchmark config 1 (T=2048, H=1024, E=8, top-2, I=2048) through
     SimpleMoE.forward vs the oracle's whole layer on the same fp8 weights."""
     say("SimpleMoE config1")
     c = W.CONFIGS["tiny"]
