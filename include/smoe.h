@@ -144,6 +144,14 @@ int smoe_swiglu_quant(const uint16_t* c1, int R, int I, uint8_t* hq, float* hs,
                       void* stream);
 
 /*
+ * As smoe_swiglu_quant, and when h is not NULL also writes h rounded to bf16
+ * (h [R,I]): the activation the fc2 weight gradient needs in the backward
+ * pass (saved by the forward instead of recomputed).
+ */
+int smoe_swiglu_quant_h(const uint16_t* c1, int R, int I, uint8_t* hq, float* hs, uint16_t* h,
+                        void* stream);
+
+/*
  * Weighted unpermute/combine: out[t] = bf16( sum_k w[t,k] * y[inv_map[t*K+k]] )
  * accumulated in fp32 in k order (each product and sum rounded separately).
  * y [T*K,H] bf16, inv_map [T*K] i32, w [T,K] f32 -> out [T,H] bf16.
@@ -153,6 +161,76 @@ int smoe_swiglu_quant(const uint16_t* c1, int R, int I, uint8_t* hq, float* hs,
  */
 int smoe_unpermute_combine(const uint16_t* y, const int32_t* inv_map, const float* w,
                            int T, int K, int H, uint16_t* out, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Backward pass of the expert FFN in fp8.  The recipe is
+ * the blockwise one: 1x128 row tiles for the dgrad operands, transposed
+ * 128x1 column tiles for the wgrad operands, 128x128 weight blocks
+ * (moe/MegatronCore_MoE_reading_notes.md:498-501); the wgrad GEMM is the
+ * "variable-K" grouped GEMM of the reference's backends
+ * (notes/2026-04/2026-04-21_gptoss_10_moe_fp8_grouped_gemm_diagnosis.md:125,
+ * notes/2026-04/2026-04-25_gptoss_21_turbo_grouped_mlp_trace_evidence.md:95).
+ * ------------------------------------------------------------------------- */
+
+/*
+ * Plain 1x128 row quantisation (no permutation): x [M,C] bf16 ->
+ * q [M,C] u8, s [M,C/128] f32 with the forward rule.  Used for output grads
+ * entering the dgrad GEMM (replaces quantize_fp8 of the grad,
+ * notes/2026-04/2026-04-21_gptoss_10_moe_fp8_grouped_gemm_diagnosis.md:99).
+ */
+int smoe_quant_rows_1x128(const uint16_t* x, int M, int C, uint8_t* q, float* s, void* stream);
+
+/*
+ * Blockwise weight transpose for dgrad: wq [E,N,K] u8 + ws [E,N/128,K/128]
+ * -> wqT [E,K,N] + wsT [E,K/128,N/128].  128x128 block quantisation commutes
+ * with the transpose, so no requantisation is needed.  Replaces the NK/KN
+ * weight cache (summary/fp8_expert_gemm_optimization.md:135-143).
+ */
+int smoe_transpose_blockwise_fp8(const uint8_t* wq, const float* ws, int E, int N, int Kdim,
+                                 uint8_t* wqT, float* wsT, void* stream);
+
+/*
+ * Transposed 128x1 column quantisation of x [R,C] bf16 whose rows are the
+ * expert segments offsets[E+1].  Each expert's rows are split into 128-row
+ * groups from its first row (short last groups zero-padded); group g of
+ * expert e is column block pad[e]/128 + g of the output.  -> xTq [C, ld] u8,
+ * xTs [C, ld/128] f32, pad [E+1] i32 (pad[e+1] = pad[e] + ceil(count/128)*128).
+ * ld must be >= smoe_quant_cols_ld(R, E) (an upper bound known on the host;
+ * columns past pad[E] are left untouched).
+ */
+int smoe_quant_cols_ld(int R, int E);
+int smoe_quant_cols_128x1(const uint16_t* x, int R, int C, const int32_t* offsets, int E, int ld,
+                          uint8_t* xTq, float* xTs, int32_t* pad, void* stream);
+
+/*
+ * Variable-K grouped fp8 GEMM for weight gradients:
+ *   dW[e][n][k] = sum over expert e's groups g of aTs[n,g]*bTs[k,g]*sum_r aT[n,r]*bT[k,r]
+ * aT [N, ld] / bT [Kdim, ld] u8 and scales [*, ld/128] from
+ * smoe_quant_cols_128x1, pad [E+1] -> dW [E, N, Kdim] f32 (zeros for experts
+ * without rows).  Replaces the grouped variable-K wgrad
+ * (notes/2026-04/2026-04-25_gptoss_21_turbo_grouped_mlp_trace_evidence.md:95).
+ */
+int smoe_grouped_gemm_fp8_wgrad(const uint8_t* aT, const float* aTs, const uint8_t* bT,
+                                const float* bTs, const int32_t* pad, int E, int N, int Kdim,
+                                int ld, float* dW, void* stream);
+
+/*
+ * SwiGLU backward: c1 [R,2I] (gate | up) and dh [R,I] bf16 -> dc1 [R,2I]
+ * bf16 = [dg | du] with s = 1/(1+exp(-g)), du = dh*(g*s),
+ * dg = (dh*u)*(s*(1 + g*(1-s))) in fp32 (library exp).  Replaces the SwiGLU
+ * backward (notes/2026-04/2026-04-24_gptoss_16_tier1_elementwise_tax_audit.md:54).
+ */
+int smoe_swiglu_bwd(const uint16_t* c1, const uint16_t* dh, int R, int I, uint16_t* dc1,
+                    void* stream);
+
+/*
+ * Combine backward: dy [T*K,H] bf16 with dy[inv_map[t*K+k]] = bf16(w[t,k]*dout[t]),
+ * and dw [T,K] f32 = <dout[t], y[inv_map[t*K+k]]> (fp32 reduction).
+ * Replaces the unpermute backward (moe/MoE_detailed_computation_dataflow.md:209-226).
+ */
+int smoe_unpermute_combine_bwd(const uint16_t* dout, const uint16_t* y, const int32_t* inv_map,
+                               const float* w, int T, int K, int H, uint16_t* dy, float* dw,
+                               void* stream);
 
 #ifdef __cplusplus
 }

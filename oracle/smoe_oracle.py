@@ -364,3 +364,132 @@ def moe_forward(x_bf16, logits, w1q, w1s, w2q, w2s, K, bias=None):
     out = unpermute_combine(y, inv_map, w, K)
     return dict(topk_idx=idx, topk_w=w, row_map=row_map, inv_map=inv_map, counts=counts,
                 offsets=offsets, xq=xq, xs=xs, c1=c1, hq=hq, hs=hs, y=y, out=out)
+
+
+# ---------------------------------------------------------------------------
+# Backward (config 5): dgrad / wgrad grouped GEMMs, 128x1 column quantisation,
+# SwiGLU and combine backward.  Recipe: E4M3 1x128 activation/grad tiles for
+# the row-major (dgrad) operands and transposed 128x1 column tiles for the
+# wgrad operands (moe/MegatronCore_MoE_reading_notes.md:498-501); variable-K
+# wgrad grouped GEMM (notes/2026-04/2026-04-21_gptoss_10_moe_fp8_grouped_gemm_diagnosis.md:125;
+# notes/2026-04/2026-04-25_gptoss_21_turbo_grouped_mlp_trace_evidence.md:95).
+# ---------------------------------------------------------------------------
+
+
+def transpose_blockwise(wq: np.ndarray, ws: np.ndarray):
+    """[E,N,K] fp8 + [E,N/128,K/128] scales -> [E,K,N] + [E,K/128,N/128].
+    128x128 block quantisation commutes with the transpose, so the dgrad
+    weights are the forward bytes transposed (no requantisation)."""
+    return np.ascontiguousarray(wq.transpose(0, 2, 1)), np.ascontiguousarray(ws.transpose(0, 2, 1))
+
+
+def pad_offsets(offsets: np.ndarray) -> np.ndarray:
+    """Per-expert row segments rounded up to whole 128-row groups:
+    pad[e+1] = pad[e] + ceil(count_e / 128) * 128."""
+    off = np.asarray(offsets, np.int64)
+    cnt = np.diff(off)
+    pad = np.zeros(off.size, np.int64)
+    pad[1:] = np.cumsum((cnt + GROUP - 1) // GROUP * GROUP)
+    return pad.astype(np.int32)
+
+
+def quant_cols_128x1(x: np.ndarray, offsets: np.ndarray):
+    """Transposed 128x1 quantisation for the wgrad operands.  x [R, C] float32
+    with expert row segments offsets[E+1].  Each expert's rows are split into
+    groups of 128 starting at its first row (the last group may be short);
+    group g of expert e lands at columns pad[e] + 128*g .. of the transposed
+    output, short groups zero-padded.  C3 applies per (column, group).
+    -> xT_q [C, Rp] u8, xT_s [C, Rp/128] f32, pad offsets [E+1] i32."""
+    x = np.asarray(x, np.float32)
+    R, C = x.shape
+    pad = pad_offsets(offsets)
+    Rp = int(pad[-1])
+    xt = np.zeros((C, Rp), np.float32)
+    for e in range(len(offsets) - 1):
+        lo, hi = int(offsets[e]), int(offsets[e + 1])
+        xt[:, pad[e]:pad[e] + (hi - lo)] = x[lo:hi].T
+    q, s = quant_1x128(xt) if Rp else (np.zeros((C, 0), np.uint8), np.zeros((C, 0), np.float32))
+    return q, s, pad
+
+
+def grouped_gemm_fp8_wgrad(aTq, aTs, bTq, bTs, pad, E: int) -> np.ndarray:
+    """dW[e] = A_e^T B_e over expert e's rows: aT [N, Rp], bT [K, Rp] (rows
+    contiguous, 128x1 scales [*, Rp/128]) -> float64 [E, N, K]; zero for
+    experts without rows."""
+    N, K = aTq.shape[0], bTq.shape[0]
+    out = np.zeros((E, N, K), np.float64)
+    for e in range(E):
+        lo, hi = int(pad[e]), int(pad[e + 1])
+        if hi <= lo:
+            continue
+        A = dequant_rows(aTq[:, lo:hi], aTs[:, lo // GROUP:hi // GROUP])
+        B = dequant_rows(bTq[:, lo:hi], bTs[:, lo // GROUP:hi // GROUP])
+        out[e] = A @ B.T
+    return out
+
+
+def swiglu_bwd(c1_bf16: np.ndarray, dh_bf16: np.ndarray) -> np.ndarray:
+    """d(silu(g)*u): with s = 1/(1+exp(-g)) (fp32, library exp, IEEE division):
+    du = dh*(g*s); dg = (dh*u) * (s*(1 + g*(1 - s))); evaluated in exactly this
+    order in fp32, stored as bf16 [R, 2I] = [dg | du]."""
+    c1 = bf16_to_f32(c1_bf16)
+    dh = bf16_to_f32(dh_bf16)
+    I = c1.shape[1] // 2
+    g, u = c1[:, :I], c1[:, I:]
+    one = F32(1.0)
+    s = (one / (one + expf32(-g)).astype(np.float32)).astype(np.float32)
+    silu = (g * s).astype(np.float32)
+    ds = (s * (one + (g * (one - s).astype(np.float32)).astype(np.float32)).astype(np.float32)).astype(np.float32)
+    du = (dh * silu).astype(np.float32)
+    dg = ((dh * u).astype(np.float32) * ds).astype(np.float32)
+    return f32_to_bf16(np.concatenate([dg, du], axis=1))
+
+
+def combine_bwd(dout_bf16, y_bf16, inv_map, w, K: int):
+    """Backward of C7: dy[inv_map[t*K+k]] = bf16(w[t,k] * dout[t]) and
+    dw[t,k] = sum_h dout[t,h] * y[inv_map[t*K+k], h] (float64 here; the kernel
+    reduces in fp32).  -> (dy [R,H] bf16, dw [T,K] float64)."""
+    dout = bf16_to_f32(dout_bf16)
+    y = bf16_to_f32(y_bf16)
+    T, H = dout.shape
+    dst = np.asarray(inv_map, np.int64).reshape(T, K)
+    w = np.asarray(w, np.float32).reshape(T, K)
+    dy = np.zeros((T * K, H), np.uint16)
+    dw = np.zeros((T, K), np.float64)
+    for k in range(K):
+        dy[dst[:, k]] = f32_to_bf16((w[:, k:k + 1] * dout).astype(np.float32))
+        dw[:, k] = (dout.astype(np.float64) * y[dst[:, k]].astype(np.float64)).sum(1)
+    return dy, dw
+
+
+def moe_backward(fwd: dict, x_bf16, w1q, w1s, w2q, w2s, dout_bf16, K: int):
+    """Backward of moe_forward given its intermediates and dout [T,H] bf16.
+    Stages: combine bwd -> dy quant (1x128) -> fc2 dgrad (W2^T) -> fc2 wgrad
+    (128x1 dy, h) -> SwiGLU bwd -> dc1 quant -> fc1 dgrad (W1^T) -> fc1 wgrad
+    (128x1 dc1, x) -> un-permute (sum of the K replicas).  GEMM outputs are
+    rounded to bf16 between stages like the kernels; wgrads stay float64."""
+    E = w1q.shape[0]
+    off = fwd["offsets"]
+    inv = fwd["inv_map"]
+    T = x_bf16.shape[0]
+    dy, dw = combine_bwd(dout_bf16, fwd["y"], inv, fwd["topk_w"], K)
+    dyq, dys = quant_1x128(bf16_to_f32(dy))
+    w2tq, w2ts = transpose_blockwise(w2q, w2s)
+    dh = f32_to_bf16(grouped_gemm_fp8(dyq, dys, w2tq, w2ts, off).astype(np.float32))
+    h = bf16_to_f32(fwd["c1"])
+    I = h.shape[1] // 2
+    # h as the forward saves it: silu(g)*u in fp32, rounded to bf16
+    hh = bf16_to_f32(f32_to_bf16((silu_f32(h[:, :I]) * h[:, I:]).astype(np.float32)))
+    dyTq, dyTs, pad = quant_cols_128x1(bf16_to_f32(dy), off)
+    hTq, hTs, _ = quant_cols_128x1(hh, off)
+    dW2 = grouped_gemm_fp8_wgrad(dyTq, dyTs, hTq, hTs, pad, E)
+    dc1 = swiglu_bwd(fwd["c1"], dh)
+    dc1q, dc1s = quant_1x128(bf16_to_f32(dc1))
+    w1tq, w1ts = transpose_blockwise(w1q, w1s)
+    dxs = f32_to_bf16(grouped_gemm_fp8(dc1q, dc1s, w1tq, w1ts, off).astype(np.float32))
+    xs_sorted = bf16_to_f32(x_bf16)[fwd["row_map"] // K]
+    dcTq, dcTs, _ = quant_cols_128x1(bf16_to_f32(dc1), off)
+    xTq, xTs, _ = quant_cols_128x1(xs_sorted, off)
+    dW1 = grouped_gemm_fp8_wgrad(dcTq, dcTs, xTq, xTs, pad, E)
+    dx = unpermute_combine(dxs, inv, np.ones((T, K), np.float32), K)
+    return dict(dy=dy, dw=dw, dh=dh, dW2=dW2, dc1=dc1, dxs=dxs, dW1=dW1, dx=dx, pad=pad)

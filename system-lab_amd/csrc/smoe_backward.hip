@@ -1,0 +1,318 @@
+// smoe_backward.hip — the backward-pass data kernels of the SimpleMoE expert
+// layer on gfx950: blockwise fp8 weight transpose (dgrad operands), 128x1
+// column quantisation into transposed, expert-segment-aligned layout (wgrad
+// operands), SwiGLU backward and combine backward.
+#include "smoe_common.h"
+
+namespace smoe {
+
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+
+// ------------------------------------------------------ weight transpose
+// [E, N, K] fp8 -> [E, K, N].  One 256-thread workgroup per 64x64-byte tile:
+// each thread loads 16 bytes of a source row into LDS (row stride 80 bytes
+// keeps the column reads spread over banks), then assembles 16 bytes of a
+// destination row from 16 LDS bytes of one source column.
+__global__ __launch_bounds__(256) void transpose_fp8_kernel(const uint8_t* __restrict__ src,
+                                                            int N, int Kd,
+                                                            uint8_t* __restrict__ dst) {
+  __shared__ uint8_t tile[64][80];
+  const int tk = blockIdx.x, tn = blockIdx.y, e = blockIdx.z;
+  const int t = threadIdx.x;
+  const int r = t >> 2, c16 = (t & 3) * 16;
+  const uint8_t* s = src + ((size_t)e * N + tn * 64 + r) * Kd + tk * 64 + c16;
+  *(uint4*)&tile[r][c16] = *(const uint4*)s;
+  __syncthreads();
+  // destination row k = tk*64 + r, columns n = tn*64 + c16 .. +16
+  uint32_t w[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    w[q] = (uint32_t)tile[c16 + 4 * q][r] | ((uint32_t)tile[c16 + 4 * q + 1][r] << 8) |
+           ((uint32_t)tile[c16 + 4 * q + 2][r] << 16) | ((uint32_t)tile[c16 + 4 * q + 3][r] << 24);
+  }
+  *(uint4*)(dst + ((size_t)e * Kd + tk * 64 + r) * N + tn * 64 + c16) =
+      make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// [E, NB, KB] f32 -> [E, KB, NB]
+__global__ __launch_bounds__(256) void transpose_scales_kernel(const float* __restrict__ s,
+                                                               int E, int NB, int KB,
+                                                               float* __restrict__ d) {
+  const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (long long)E * NB * KB) return;
+  const int e = (int)(i / ((long long)NB * KB));
+  const int rem = (int)(i - (long long)e * NB * KB);
+  const int nb = rem / KB, kb = rem - nb * KB;
+  d[((size_t)e * KB + kb) * NB + nb] = s[i];
+}
+
+// ---------------------------------------------------- padded segments
+// pad[e+1] = pad[e] + ceil(count_e / 128) * 128, one workgroup.
+__global__ __launch_bounds__(1024) void pad_offsets_kernel(const int32_t* __restrict__ offsets,
+                                                           int E, int32_t* __restrict__ pad) {
+  __shared__ int part[1024];
+  const int t = threadIdx.x;
+  int v = 0;
+  if (t < E) v = (offsets[t + 1] - offsets[t] + kGroup - 1) / kGroup * kGroup;
+  part[t] = v;
+  __syncthreads();
+  for (int o = 1; o < 1024; o <<= 1) {
+    const int u = t >= o ? part[t - o] : 0;
+    __syncthreads();
+    part[t] += u;
+    __syncthreads();
+  }
+  if (t < E) pad[t + 1] = part[t];
+  if (t == 0) pad[0] = 0;
+}
+
+// --------------------------------------------- 128x1 column quantisation
+// One 256-thread workgroup per (128-row group, 64-column slab).  The group's
+// rows (an expert's rows split into 128-row groups from its first row; short
+// last groups are zero-padded) are staged as fp32 in LDS; thread t owns
+// column t/4 and rows (t%4)*32 .. +32 of the group; the column amax is a
+// 2-step shuffle over the 4 threads of a column.  The 128 fp8 bytes of a
+// column land contiguously in the transposed output row (ld bytes apart).
+__global__ __launch_bounds__(256) void quant_cols_kernel(const uint16_t* __restrict__ x, int C,
+                                                         const int32_t* __restrict__ offsets,
+                                                         const int32_t* __restrict__ pad, int E,
+                                                         int ld, uint8_t* __restrict__ q,
+                                                         float* __restrict__ s) {
+  __shared__ float tile[128][65];
+  __shared__ int pad_l[SMOE_MAX_EXPERTS + 1];
+  const int t = threadIdx.x;
+  for (int i = t; i <= E; i += 256) pad_l[i] = pad[i];
+  __syncthreads();
+  const int gpos = blockIdx.x * kGroup;  // position in the padded row space
+  if (gpos >= pad_l[E]) return;          // whole workgroup leaves together
+  int lo = 0, hi = E;                    // largest e with pad[e] <= gpos
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (pad_l[mid] <= gpos) lo = mid;
+    else hi = mid;
+  }
+  const int e = lo;
+  const int row0 = offsets[e] + (gpos - pad_l[e]);
+  const int valid = min(kGroup, offsets[e + 1] - row0);
+  const int c0 = blockIdx.y * 64;
+  // stage 128 x 64 bf16 as fp32: each thread 4 x (8 bf16)
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int idx = j * 256 + t;
+    const int r = idx >> 3, cc = (idx & 7) * 8;
+    float f[8];
+    if (r < valid && c0 + cc < C) {
+      const uint4 v = *(const uint4*)(x + (size_t)(row0 + r) * C + c0 + cc);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        f[2 * i] = __uint_as_float(w[i] << 16);
+        f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) f[i] = 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) tile[r][cc + i] = f[i];
+  }
+  __syncthreads();
+  const int col = t >> 2, part = t & 3;
+  if (c0 + col >= C) return;
+  float v[32];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    v[i] = tile[part * 32 + i][col];
+    amax = fmaxf(amax, fabsf(v[i]));
+  }
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 4));
+  amax = fmaxf(amax, __shfl_xor(amax, 2, 4));
+  const float sc = group_scale(amax);
+  uint32_t w[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    w[i] = quant_one(v[4 * i], sc) | (quant_one(v[4 * i + 1], sc) << 8) |
+           (quant_one(v[4 * i + 2], sc) << 16) | (quant_one(v[4 * i + 3], sc) << 24);
+  uint8_t* dst = q + (size_t)(c0 + col) * ld + gpos + part * 32;
+  *(uint4*)dst = make_uint4(w[0], w[1], w[2], w[3]);
+  *(uint4*)(dst + 16) = make_uint4(w[4], w[5], w[6], w[7]);
+  if (part == 0) s[(size_t)(c0 + col) * (ld / kGroup) + gpos / kGroup] = sc;
+}
+
+// ------------------------------------------------------- SwiGLU backward
+// One wave per row; a lane owns 8 consecutive columns of a 512-column chunk.
+// s = 1/(1+exp(-g)); du = dh*(g*s); dg = (dh*u) * (s*(1 + g*(1-s))).
+__global__ __launch_bounds__(256) void swiglu_bwd_kernel(const uint16_t* __restrict__ c1,
+                                                         const uint16_t* __restrict__ dh, int R,
+                                                         int I, uint16_t* __restrict__ dc1) {
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= R) return;
+  const uint16_t* grow = c1 + (size_t)r * 2 * I;
+  for (int col = lane * 8; col < I; col += kWave * 8) {
+    const uint4 vg = *(const uint4*)(grow + col);
+    const uint4 vu = *(const uint4*)(grow + I + col);
+    const uint4 vd = *(const uint4*)(dh + (size_t)r * I + col);
+    const uint32_t g4[4] = {vg.x, vg.y, vg.z, vg.w};
+    const uint32_t u4[4] = {vu.x, vu.y, vu.z, vu.w};
+    const uint32_t d4[4] = {vd.x, vd.y, vd.z, vd.w};
+    uint32_t og[4], ou[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t gb[2], ub[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const float g = h ? __uint_as_float(g4[i] & 0xffff0000u) : __uint_as_float(g4[i] << 16);
+        const float u = h ? __uint_as_float(u4[i] & 0xffff0000u) : __uint_as_float(u4[i] << 16);
+        const float d = h ? __uint_as_float(d4[i] & 0xffff0000u) : __uint_as_float(d4[i] << 16);
+        const float s = 1.0f / (1.0f + expf32(-g));
+        const float silu = g * s;
+        const float ds = s * (1.0f + g * (1.0f - s));
+        ub[h] = f32_to_bf16(d * silu);
+        gb[h] = f32_to_bf16((d * u) * ds);
+      }
+      og[i] = gb[0] | (gb[1] << 16);
+      ou[i] = ub[0] | (ub[1] << 16);
+    }
+    uint16_t* orow = dc1 + (size_t)r * 2 * I;
+    *(uint4*)(orow + col) = make_uint4(og[0], og[1], og[2], og[3]);
+    *(uint4*)(orow + I + col) = make_uint4(ou[0], ou[1], ou[2], ou[3]);
+  }
+}
+
+// ------------------------------------------------------ combine backward
+// One wave per token: reads dout[t] once, and for each of its K rows writes
+// dy[r] = bf16(w[t,k] * dout[t]) and reduces dw[t,k] = <dout[t], y[r]> in
+// fp32 (lane partials over the row, then a wave tree).
+template <int kMaxK>
+__global__ __launch_bounds__(256) void combine_bwd_kernel(
+    const uint16_t* __restrict__ dout, const uint16_t* __restrict__ y,
+    const int32_t* __restrict__ inv_map, const float* __restrict__ w, int T, int K, int H,
+    uint16_t* __restrict__ dy, float* __restrict__ dw) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const int R = T * K;
+  int r[kMaxK];
+  float wk[kMaxK], part[kMaxK];
+#pragma unroll
+  for (int k = 0; k < kMaxK; ++k) {
+    part[k] = 0.0f;
+    if (k < K) {
+      r[k] = inv_map[(size_t)t * K + k];
+      wk[k] = w[(size_t)t * K + k];
+    }
+  }
+  for (int col = lane * 8; col < H; col += kWave * 8) {
+    const uint4 vd = *(const uint4*)(dout + (size_t)t * H + col);
+    const uint32_t d4[4] = {vd.x, vd.y, vd.z, vd.w};
+    float d[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      d[2 * i] = __uint_as_float(d4[i] << 16);
+      d[2 * i + 1] = __uint_as_float(d4[i] & 0xffff0000u);
+    }
+#pragma unroll
+    for (int k = 0; k < kMaxK; ++k) {
+      if (k >= K || (unsigned)r[k] >= (unsigned)R) continue;
+      const uint4 vy = *(const uint4*)(y + (size_t)r[k] * H + col);
+      const uint32_t y4[4] = {vy.x, vy.y, vy.z, vy.w};
+      uint32_t o[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float y0 = __uint_as_float(y4[i] << 16);
+        const float y1 = __uint_as_float(y4[i] & 0xffff0000u);
+        part[k] = part[k] + d[2 * i] * y0;
+        part[k] = part[k] + d[2 * i + 1] * y1;
+        o[i] = f32_to_bf16(wk[k] * d[2 * i]) | (f32_to_bf16(wk[k] * d[2 * i + 1]) << 16);
+      }
+      *(uint4*)(dy + (size_t)r[k] * H + col) = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kMaxK; ++k) {
+    if (k >= K) continue;
+    const float tot = wave_sum_tree(part[k]);
+    if (lane == 0) dw[(size_t)t * K + k] = tot;
+  }
+}
+
+}  // namespace smoe
+
+using namespace smoe;
+
+extern "C" int smoe_transpose_blockwise_fp8(const uint8_t* wq, const float* ws, int E, int N,
+                                            int Kdim, uint8_t* wqT, float* wsT, void* stream) {
+  if (N <= 0 || Kdim <= 0) return SMOE_EINVAL_DIM;
+  if (E <= 0 || E > SMOE_MAX_EXPERTS) return SMOE_EINVAL_EXPERTS;
+  if (N % kGroup || Kdim % kGroup) return SMOE_EINVAL_ALIGN128;
+  SMOE_CHECK_PTR(wq);
+  SMOE_CHECK_PTR(wqT);
+  if (!ws || !wsT) return SMOE_EINVAL_NULL;
+  if (((uintptr_t)ws | (uintptr_t)wsT) & 3u) return SMOE_EINVAL_PTRALIGN;
+  hipStream_t s = (hipStream_t)stream;
+  transpose_fp8_kernel<<<dim3(Kdim / 64, N / 64, E), dim3(256), 0, s>>>(wq, N, Kdim, wqT);
+  const long long ns = (long long)E * (N / kGroup) * (Kdim / kGroup);
+  transpose_scales_kernel<<<dim3((unsigned)((ns + 255) / 256)), dim3(256), 0, s>>>(
+      ws, E, N / kGroup, Kdim / kGroup, wsT);
+  SMOE_RETURN_LAUNCH();
+}
+
+extern "C" int smoe_quant_cols_ld(int R, int E) {
+  if (R < 0 || E <= 0) return 0;
+  const long long ld = ((long long)(R + kGroup - 1) / kGroup + E) * kGroup;
+  return ld > 0x7fffffffLL ? 0 : (int)ld;
+}
+
+extern "C" int smoe_quant_cols_128x1(const uint16_t* x, int R, int C, const int32_t* offsets,
+                                     int E, int ld, uint8_t* xTq, float* xTs, int32_t* pad,
+                                     void* stream) {
+  if (R <= 0 || C <= 0) return SMOE_EINVAL_DIM;
+  if (E <= 0 || E > SMOE_MAX_EXPERTS) return SMOE_EINVAL_EXPERTS;
+  if (C % kGroup) return SMOE_EINVAL_ALIGN128;
+  if (ld < smoe_quant_cols_ld(R, E) || ld % kGroup) return SMOE_EINVAL_DIM;
+  SMOE_CHECK_PTR(x);
+  SMOE_CHECK_PTR(xTq);
+  if (!offsets || !xTs || !pad) return SMOE_EINVAL_NULL;
+  if (((uintptr_t)offsets | (uintptr_t)xTs | (uintptr_t)pad) & 3u) return SMOE_EINVAL_PTRALIGN;
+  hipStream_t s = (hipStream_t)stream;
+  pad_offsets_kernel<<<1, 1024, 0, s>>>(offsets, E, pad);
+  quant_cols_kernel<<<dim3(ld / kGroup, C / 64), dim3(256), 0, s>>>(x, C, offsets, pad, E, ld,
+                                                                    xTq, xTs);
+  SMOE_RETURN_LAUNCH();
+}
+
+extern "C" int smoe_swiglu_bwd(const uint16_t* c1, const uint16_t* dh, int R, int I,
+                               uint16_t* dc1, void* stream) {
+  if (R <= 0 || I <= 0) return SMOE_EINVAL_DIM;
+  if (I % kGroup) return SMOE_EINVAL_ALIGN128;
+  SMOE_CHECK_PTR(c1);
+  SMOE_CHECK_PTR(dh);
+  SMOE_CHECK_PTR(dc1);
+  swiglu_bwd_kernel<<<dim3((R + 3) / 4), dim3(256), 0, (hipStream_t)stream>>>(c1, dh, R, I, dc1);
+  SMOE_RETURN_LAUNCH();
+}
+
+extern "C" int smoe_unpermute_combine_bwd(const uint16_t* dout, const uint16_t* y,
+                                          const int32_t* inv_map, const float* w, int T, int K,
+                                          int H, uint16_t* dy, float* dw, void* stream) {
+  if (T <= 0 || H <= 0) return SMOE_EINVAL_DIM;
+  if (H % kGroup) return SMOE_EINVAL_ALIGN128;
+  if (K <= 0 || K > 32) return SMOE_EINVAL_TOPK;
+  if ((long long)T * K > 0x7fffffffLL) return SMOE_EINVAL_DIM;
+  SMOE_CHECK_PTR(dout);
+  SMOE_CHECK_PTR(y);
+  SMOE_CHECK_PTR(dy);
+  if (!inv_map || !w || !dw) return SMOE_EINVAL_NULL;
+  if (((uintptr_t)inv_map | (uintptr_t)w | (uintptr_t)dw) & 3u) return SMOE_EINVAL_PTRALIGN;
+  const dim3 grid((T + 3) / 4), block(256);
+  hipStream_t s = (hipStream_t)stream;
+#define SMOE_CBB(MK) \
+  combine_bwd_kernel<MK><<<grid, block, 0, s>>>(dout, y, inv_map, w, T, K, H, dy, dw)
+  if (K <= 2) SMOE_CBB(2);
+  else if (K <= 8) SMOE_CBB(8);
+  else SMOE_CBB(32);
+#undef SMOE_CBB
+  SMOE_RETURN_LAUNCH();
+}

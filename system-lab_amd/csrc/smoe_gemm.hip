@@ -29,18 +29,11 @@
 // (no host sync, no workspace) and leaves when its tile index is past the
 // real total.  Zero-token experts own no tiles; rows past an expert's end are
 // clamped on load and masked on store.
-#include "smoe_common.h"
+#include "smoe_mfma.h"
 
 namespace smoe {
 
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v8i __attribute__((ext_vector_type(8)));
-typedef float v4f __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
-constexpr int kBK = 128;  // K per step (= scale block)
 constexpr int kGroupM = 4;  // m-tiles per scheduling group
-constexpr int kRow = kBK;   // bytes per LDS tile row
 
 // Tile configuration: waves form a kWR (rows) x kWN (columns) grid; each wave
 // owns kRB 16-row blocks x 4 16-column blocks (kRB*16 rows x 64 columns).
@@ -64,45 +57,6 @@ struct Cfg {
   static_assert(kSWaves <= kWaves, "scale split");
   static_assert(kStages * kStage + 4200 <= 160 * 1024, "LDS budget");
 };
-
-// s_waitcnt with vmcnt = n (n < 16), expcnt not waited on, lgkmcnt(0): the
-// encoding is vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8].
-template <int n>
-__device__ __forceinline__ void wait_vm_lgkm0() {
-  static_assert(n >= 0 && n < 16, "vmcnt immediate");
-  __builtin_amdgcn_s_waitcnt(n | (7 << 4));
-}
-
-// Direct global->LDS loads issued as inline asm: lane i's 16 (or 4) bytes at
-// base + voff land at LDS address m0 + i*16 (i*4).  The compiler does not see
-// these as LDS writes, so it inserts no vmcnt(0) before the fragment reads of
-// other stages; completion is tracked explicitly with s_waitcnt vmcnt(n)
-// followed by a workgroup barrier.  No compiler-visible global loads are
-// issued inside the K loop, so the counts are exact.
-__device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff),
-               "s"(base)
-               : "memory");
-}
-__device__ __forceinline__ void dma4(const void* base, uint32_t voff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds), "v"(voff),
-               "s"(base)
-               : "memory");
-}
-
-__device__ __forceinline__ int swz(int row, int chunk) {
-  return row * kRow + ((chunk ^ (row & 7)) << 4);
-}
-
-__device__ __forceinline__ v4f mfma16(v8i a, v8i b, v4f c) {
-  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
-}
-
-__device__ __forceinline__ v8i lds_frag(const uint8_t* base, int row, int c0) {
-  const v4i lo = *(const v4i*)(base + swz(row, c0));
-  const v4i hi = *(const v4i*)(base + swz(row, c0 + 1));
-  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-}
 
 template <class C>
 __global__ __launch_bounds__(C::kThreads, 1) void grouped_gemm_fp8_kernel(

@@ -1,0 +1,156 @@
+// smoe_gemm_wgrad.hip — variable-K fp8 grouped GEMM for the weight gradient
+// of the expert FFN (gfx950):
+//
+//   dW[e][n][k] = sum_g sa[n,g] * sb[k,g] * sum_{r in g} aT[n,r] * bT[k,r]
+//
+// over expert e's 128-row groups g in [pad[e], pad[e+1]) of the transposed,
+// 128x1-quantised operands aT [N, ld] (e.g. output grads) and bT [K, ld]
+// (e.g. activations), both with the reduction index r contiguous.  Output is
+// fp32 [E, N, K]; experts without rows get zeros.
+//
+// A workgroup of 4 waves owns a 128 (n) x 128 (k) tile of one expert; wave w
+// owns 64 x 64, i.e. 4 x 4 blocks of v_mfma_f32_16x16x128_f8f6f4, one MFMA
+// per 128-row group.  aT rows feed the MFMA's A operand and bT rows its B
+// operand, so an output lane holds one k (lane % 16) and four consecutive n.
+// Both scales vary per row and group, so each partial is multiplied by
+// sa[n,g]*sb[k,g] before accumulation.  Operands and both scale vectors of a
+// group are staged by direct global->LDS DMA, two stages deep, as in the
+// forward grouped GEMM.
+#include "smoe_mfma.h"
+
+namespace smoe {
+
+constexpr int kWT = 128;                    // tile edge (n and k)
+constexpr int kWThreads = 256;
+constexpr int kWA = kWT * kRow;             // 16 KiB of aT
+constexpr int kWB = kWT * kRow;             // 16 KiB of bT
+constexpr int kWStage = kWA + kWB + 2 * kWT * 4;
+
+__global__ __launch_bounds__(kWThreads, 2) void grouped_gemm_fp8_wgrad_kernel(
+    const uint8_t* __restrict__ aT, const float* __restrict__ aTs, const uint8_t* __restrict__ bT,
+    const float* __restrict__ bTs, const int32_t* __restrict__ pad, int N, int Kd, int ld,
+    float* __restrict__ dW) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * kWStage];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int e = blockIdx.z;
+  const int n0 = blockIdx.y * kWT, k0 = blockIdx.x * kWT;
+  const int g0 = pad[e], g1 = pad[e + 1];
+  const int steps = (g1 - g0) / kGroup;
+  const int nrows = min(kWT, N - n0), krows = min(kWT, Kd - k0);
+  const int lds_ld = ld / kGroup;  // scale row length
+
+  // DMA: wave w fills aT segments w*4..w*4+3 and bT segments w*4..w*4+3
+  // (8 rows of 128 bytes each); waves 0/1 load the 128 aT scales, 2/3 the bT
+  // scales, 64 rows each.
+  uint32_t oa[4], ob[4];
+  const int slot = lane & 7;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int row = (wid * 4 + j) * 8 + (lane >> 3);
+    oa[j] = (uint32_t)(min(row, nrows - 1) * ld + ((slot ^ (row & 7)) << 4));
+    ob[j] = (uint32_t)(min(row, krows - 1) * ld + ((slot ^ (row & 7)) << 4));
+  }
+  const int srow = (wid & 1) * 64 + lane;
+  const uint32_t os =
+      (uint32_t)(min(srow, (wid < 2 ? nrows : krows) - 1) * lds_ld) * 4u;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_ptr_t)smem;
+  auto issue = [&](int st_idx, int buf) {
+    const uint32_t st = lds0 + buf * kWStage;
+    const int r0 = g0 + st_idx * kGroup;
+    const uint8_t* ab = aT + (size_t)n0 * ld + r0;
+    const uint8_t* bb = bT + (size_t)k0 * ld + r0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      dma16(ab, oa[j], __builtin_amdgcn_readfirstlane(st + (wid * 4 + j) * 1024));
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      dma16(bb, ob[j], __builtin_amdgcn_readfirstlane(st + kWA + (wid * 4 + j) * 1024));
+    const float* sbase = wid < 2 ? aTs + (size_t)n0 * lds_ld : bTs + (size_t)k0 * lds_ld;
+    dma4(uniform_ptr(sbase + r0 / kGroup), os,
+         __builtin_amdgcn_readfirstlane(st + kWA + kWB + (wid >> 1) * kWT * 4 + (wid & 1) * 256));
+  };
+
+  const int wk = wid >> 1, wn = wid & 1;  // wave's k half and n half
+  const int frow = lane & 15;
+  const int fch = (lane >> 4) * 2;
+  v4f acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+  if (steps > 0) {
+    issue(0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  }
+  for (int st = 0; st < steps; ++st) {
+    const int buf = st & 1;
+    if (st + 1 < steps) issue(st + 1, buf ^ 1);
+    const uint8_t* sA = smem + buf * kWStage;
+    const uint8_t* sB = sA + kWA;
+    const float* sSa = (const float*)(sB + kWB);
+    const float* sSb = sSa + kWT;
+    v8i fa[4];
+    v4f sa[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      fa[j] = lds_frag(sA, wn * 64 + j * 16 + frow, fch);
+      sa[j] = *(const v4f*)(sSa + wn * 64 + j * 16 + (lane >> 4) * 4);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int kr = wk * 64 + i * 16 + frow;
+      const v8i fb = lds_frag(sB, kr, fch);
+      const float sb = sSb[kr];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const v4f p = mfma16(fa[j], fb, v4f{0.0f, 0.0f, 0.0f, 0.0f});
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          acc[i][j][v] = __builtin_fmaf(p[v] * sa[j][v], sb, acc[i][j][v]);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  }
+
+  // lane holds k = (lane%16) of each 16-row block i, n = (lane/16)*4 + v
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int kl = wk * 64 + i * 16 + frow;
+    if (kl >= krows) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int nl = wn * 64 + j * 16 + (lane >> 4) * 4 + v;
+        if (nl < nrows) dW[((size_t)e * N + n0 + nl) * Kd + k0 + kl] = acc[i][j][v];
+      }
+    }
+  }
+}
+
+}  // namespace smoe
+
+using namespace smoe;
+
+extern "C" int smoe_grouped_gemm_fp8_wgrad(const uint8_t* aT, const float* aTs,
+                                           const uint8_t* bT, const float* bTs,
+                                           const int32_t* pad, int E, int N, int Kdim, int ld,
+                                           float* dW, void* stream) {
+  if (N <= 0 || Kdim <= 0 || ld <= 0) return SMOE_EINVAL_DIM;
+  if (E <= 0 || E > SMOE_MAX_EXPERTS) return SMOE_EINVAL_EXPERTS;
+  if (N % kGroup || Kdim % kGroup || ld % kGroup) return SMOE_EINVAL_ALIGN128;
+  if ((long long)kWT * ld >= (1LL << 31)) return SMOE_EINVAL_DIM;
+  SMOE_CHECK_PTR(aT);
+  SMOE_CHECK_PTR(bT);
+  SMOE_CHECK_PTR(dW);
+  if (!aTs || !bTs || !pad) return SMOE_EINVAL_NULL;
+  if (((uintptr_t)aTs | (uintptr_t)bTs | (uintptr_t)pad) & 3u) return SMOE_EINVAL_PTRALIGN;
+  grouped_gemm_fp8_wgrad_kernel<<<dim3(Kdim / kWT, N / kWT, E), dim3(kWThreads), 0,
+                                  (hipStream_t)stream>>>(aT, aTs, bT, bTs, pad, N, Kdim, ld, dW);
+  SMOE_RETURN_LAUNCH();
+}

@@ -74,7 +74,8 @@ __global__ __launch_bounds__(256) void permute_quant_kernel(
   const int R = T * K;
   const int sub = lane & 7, gl = lane >> 3;
   // destination rows: lane k holds inv_map[t*K + k]
-  const int my_r = lane < K ? inv_map[(size_t)t * K + lane] : 0;
+  // inv_map == nullptr (K == 1): rows stay in place (plain 1x128 row quant)
+  const int my_r = inv_map ? (lane < K ? inv_map[(size_t)t * K + lane] : 0) : t;
   const uint16_t* xrow = x + (size_t)t * H;
   for (int c0 = 0; c0 * 8 < G; c0 += kUnroll) {
     uint4 v[kUnroll][2];
@@ -113,11 +114,14 @@ __global__ __launch_bounds__(256) void permute_quant_kernel(
 }
 
 // ------------------------------------------------------------ swiglu_quant
-template <int kUnroll>
+// kSaveH: also write h rounded to bf16 (the fc2 wgrad operand of the
+// backward pass), saving a recompute from c1.
+template <int kUnroll, bool kSaveH>
 __global__ __launch_bounds__(256) void swiglu_quant_kernel(const uint16_t* __restrict__ c1,
                                                            int R, int I,
                                                            uint8_t* __restrict__ hq,
-                                                           float* __restrict__ hs) {
+                                                           float* __restrict__ hs,
+                                                           uint16_t* __restrict__ hb) {
   const int lane = threadIdx.x & 63;
   const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (r >= R) return;
@@ -151,6 +155,14 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const uint16_t* __res
       for (int i = 0; i < 16; ++i) h[i] = silu32(fg[i]) * fu[i];
       const Q16 q = quant16(h);
       const int g = (c0 + u) * 8 + gl;
+      if (kSaveH && g < G) {
+        uint32_t w[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w[i] = f32_to_bf16(h[2 * i]) | (f32_to_bf16(h[2 * i + 1]) << 16);
+        uint16_t* hp = hb + (size_t)r * I + g * kGroup + sub * 16;
+        *(uint4*)hp = make_uint4(w[0], w[1], w[2], w[3]);
+        *(uint4*)(hp + 8) = make_uint4(w[4], w[5], w[6], w[7]);
+      }
       if (g < G) {
         store16<true>(hq + (size_t)r * I + g * kGroup + sub * 16, q.q);
         if (sub == 0) hs[(size_t)r * G + g] = q.scale;
@@ -233,6 +245,27 @@ extern "C" int smoe_permute_quant(const uint16_t* x, const int32_t* inv_map, int
   SMOE_RETURN_LAUNCH();
 }
 
+extern "C" int smoe_quant_rows_1x128(const uint16_t* x, int M, int C, uint8_t* q, float* s,
+                                     void* stream) {
+  if (M <= 0 || C <= 0) return SMOE_EINVAL_DIM;
+  if (C % kGroup) return SMOE_EINVAL_ALIGN128;
+  SMOE_CHECK_PTR(x);
+  SMOE_CHECK_PTR(q);
+  SMOE_CHECK_PTR(s);
+  const int chunks = (C / kGroup + 7) / 8;
+  const dim3 grid((M + 3) / 4), block(256);
+  hipStream_t st = (hipStream_t)stream;
+#define SMOE_QR(U) permute_quant_kernel<U, true><<<grid, block, 0, st>>>(x, nullptr, M, C, 1, q, s)
+  switch (chunks) {
+    case 1: SMOE_QR(1); break;
+    case 2: SMOE_QR(2); break;
+    case 3: SMOE_QR(3); break;
+    default: SMOE_QR(4); break;
+  }
+#undef SMOE_QR
+  SMOE_RETURN_LAUNCH();
+}
+
 extern "C" int smoe_dispatch_quant(const uint16_t* x, const int32_t* topk_idx, int T, int H,
                                    int K, int E, int32_t* row_map, int32_t* inv_map,
                                    int32_t* counts, int32_t* offsets, uint8_t* xq, float* xs,
@@ -248,22 +281,32 @@ extern "C" int smoe_dispatch_quant(const uint16_t* x, const int32_t* topk_idx, i
   return smoe_permute_quant(x, inv_map, T, H, K, xq, xs, stream);
 }
 
-extern "C" int smoe_swiglu_quant(const uint16_t* c1, int R, int I, uint8_t* hq, float* hs,
-                                 void* stream) {
+extern "C" int smoe_swiglu_quant_h(const uint16_t* c1, int R, int I, uint8_t* hq, float* hs,
+                                   uint16_t* h, void* stream) {
   if (R <= 0 || I <= 0) return SMOE_EINVAL_DIM;
   if (I % kGroup) return SMOE_EINVAL_ALIGN128;
   SMOE_CHECK_PTR(c1);
   SMOE_CHECK_PTR(hq);
   SMOE_CHECK_PTR(hs);
+  if (h && ((uintptr_t)h & 15u)) return SMOE_EINVAL_PTRALIGN;
   const int chunks = (I / kGroup + 7) / 8;
   const dim3 grid((R + 3) / 4), block(256);
   hipStream_t s = (hipStream_t)stream;
-#define SMOE_SW(U) swiglu_quant_kernel<U><<<grid, block, 0, s>>>(c1, R, I, hq, hs)
+#define SMOE_SW(U)                                                                        \
+  do {                                                                                    \
+    if (h) swiglu_quant_kernel<U, true><<<grid, block, 0, s>>>(c1, R, I, hq, hs, h);      \
+    else swiglu_quant_kernel<U, false><<<grid, block, 0, s>>>(c1, R, I, hq, hs, nullptr); \
+  } while (0)
   if (chunks <= 1) SMOE_SW(1);
   else if (chunks <= 2) SMOE_SW(2);
   else SMOE_SW(4);
 #undef SMOE_SW
   SMOE_RETURN_LAUNCH();
+}
+
+extern "C" int smoe_swiglu_quant(const uint16_t* c1, int R, int I, uint8_t* hq, float* hs,
+                                 void* stream) {
+  return smoe_swiglu_quant_h(c1, R, I, hq, hs, nullptr, stream);
 }
 
 extern "C" int smoe_quantize_weight_blockwise(const uint16_t* w, int E, int N, int Kdim,

@@ -66,11 +66,51 @@ class SimpleMoE(nn.Module):
         idx, w = ops.router_topk(logits.contiguous(), self.top_k, self.router_bias)
         xq, xs, row_map, inv_map, counts, offsets = ops.permute_quant(x, idx, self.num_experts)
         c1 = ops.grouped_gemm_fp8(xq, xs, w1q, w1s, offsets)
-        hq, hs = ops.swiglu_quant(c1)
+        if return_intermediates:
+            hq, hs, h = ops.swiglu_quant(c1, save_h=True)
+        else:
+            hq, hs = ops.swiglu_quant(c1)
+            h = None
         y = ops.grouped_gemm_fp8(hq, hs, w2q, w2s, offsets)
         out = ops.unpermute_combine(y, inv_map, w)
         if return_intermediates:
-            return out, dict(topk_idx=idx, topk_w=w, row_map=row_map, inv_map=inv_map,
+            return out, dict(x=x, topk_idx=idx, topk_w=w, row_map=row_map, inv_map=inv_map,
                              counts=counts, offsets=offsets, xq=xq, xs=xs, c1=c1, hq=hq,
-                             hs=hs, y=y)
+                             hs=hs, h=h, y=y)
         return out
+
+    @torch.no_grad()
+    def backward_from(self, inter: dict, dout: torch.Tensor) -> dict:
+        """Backward of one forward call given its intermediates
+        (``forward(..., return_intermediates=True)``) and dout [T,H] bf16.
+
+        combine bwd -> dy 1x128 quant -> fc2 dgrad (W2^T) and fc2 wgrad
+        (128x1 dy, h) -> SwiGLU bwd -> dc1 quant -> fc1 dgrad (W1^T) and fc1
+        wgrad (128x1 dc1, sorted x) -> sum of the K replicas into dx.
+        Returns dx [T,H] bf16, dw1 [E,2I,H] f32, dw2 [E,H,I] f32 and the
+        router-weight gradient dtopk_w [T,K] f32.  Every stage is a HIP kernel;
+        nothing synchronises with the host."""
+        w1q, w1s, w2q, w2s = self.fp8_weights()
+        if getattr(self, "_fp8_t", None) is None or self._fp8_t[0] is not w1q:
+            self._fp8_t = (w1q,) + ops.transpose_blockwise(w1q, w1s) + ops.transpose_blockwise(w2q, w2s)
+        _, w1tq, w1ts, w2tq, w2ts = self._fp8_t
+        off, inv = inter["offsets"], inter["inv_map"]
+        K = self.top_k
+        dy, dw = ops.unpermute_combine_bwd(dout.contiguous(), inter["y"], inv, inter["topk_w"])
+        dyq, dys = ops.quant_rows(dy)
+        dh = ops.grouped_gemm_fp8(dyq, dys, w2tq, w2ts, off)
+        h = inter["h"]
+        dyTq, dyTs, pad, ld = ops.quant_cols(dy, off)
+        hTq, hTs, _, _ = ops.quant_cols(h, off)
+        dw2 = ops.grouped_gemm_fp8_wgrad(dyTq, dyTs, hTq, hTs, pad, ld)
+        dc1 = ops.swiglu_bwd(inter["c1"], dh)
+        dcq, dcs = ops.quant_rows(dc1)
+        dxs = ops.grouped_gemm_fp8(dcq, dcs, w1tq, w1ts, off)
+        xs = inter["x"].index_select(0, (inter["row_map"] // K).long())
+        dcTq, dcTs, _, _ = ops.quant_cols(dc1, off)
+        xTq, xTs, _, _ = ops.quant_cols(xs, off)
+        dw1 = ops.grouped_gemm_fp8_wgrad(dcTq, dcTs, xTq, xTs, pad, ld)
+        ones = torch.ones_like(inter["topk_w"])
+        dx = ops.unpermute_combine(dxs, inv, ones)
+        return dict(dx=dx, dw1=dw1, dw2=dw2, dtopk_w=dw, dy=dy, dh=dh, dc1=dc1, dxs=dxs)
+

@@ -171,9 +171,10 @@ def grouped_gemm_fp8(xq: torch.Tensor, xs: torch.Tensor, wq: torch.Tensor, ws: t
 
 
 # ------------------------------------------------------------------ SwiGLU
-def swiglu_quant(c1: torch.Tensor):
+def swiglu_quant(c1: torch.Tensor, save_h: bool = False):
     """h = silu(gate)*up (gate = columns [0,I), up = [I,2I)) requantised 1x128.
-    c1 [R,2I] bf16 -> (hq [R,I] fp8, hs [R,I/128] f32)."""
+    c1 [R,2I] bf16 -> (hq [R,I] fp8, hs [R,I/128] f32), plus h as bf16 [R,I]
+    when ``save_h`` (the fc2 wgrad operand for the backward pass)."""
     _check(c1, "c1", (torch.bfloat16,), 2)
     R, I2 = c1.shape
     if I2 % 2:
@@ -181,8 +182,9 @@ def swiglu_quant(c1: torch.Tensor):
     I = I2 // 2
     hq = torch.empty((R, I), dtype=FP8, device=c1.device)
     hs = torch.empty((R, I // GROUP), dtype=torch.float32, device=c1.device)
-    _C.call("smoe_swiglu_quant", _ptr(c1), R, I, _ptr(hq), _ptr(hs), _stream())
-    return hq, hs
+    h = torch.empty((R, I), dtype=torch.bfloat16, device=c1.device) if save_h else None
+    _C.call("smoe_swiglu_quant_h", _ptr(c1), R, I, _ptr(hq), _ptr(hs), _ptr(h), _stream())
+    return (hq, hs, h) if save_h else (hq, hs)
 
 
 # ----------------------------------------------------------------- combine
@@ -202,3 +204,88 @@ def unpermute_combine(y: torch.Tensor, inv_map: torch.Tensor, topk_w: torch.Tens
     _C.call("smoe_unpermute_combine", _ptr(y), _ptr(inv_map), _ptr(topk_w), T, K, H, _ptr(out),
             _stream())
     return out
+
+
+# ---------------------------------------------------------------- backward
+def quant_rows(x: torch.Tensor):
+    """1x128 row quantisation without permutation: x [M,C] bf16 ->
+    (q [M,C] fp8, s [M,C/128] f32)."""
+    _check(x, "x", (torch.bfloat16,), 2)
+    M, C = x.shape
+    q = torch.empty((M, C), dtype=FP8, device=x.device)
+    s = torch.empty((M, C // GROUP), dtype=torch.float32, device=x.device)
+    _C.call("smoe_quant_rows_1x128", _ptr(x), M, C, _ptr(q), _ptr(s), _stream())
+    return q, s
+
+
+def transpose_blockwise(wq: torch.Tensor, ws: torch.Tensor):
+    """[E,N,K] fp8 + [E,N/128,K/128] -> [E,K,N] + [E,K/128,N/128] (dgrad
+    weights; blockwise quantisation commutes with the transpose)."""
+    _check(wq, "wq", (FP8, torch.uint8), 3)
+    _check(ws, "ws", (torch.float32,), 3)
+    E, N, Kd = wq.shape
+    wqT = torch.empty((E, Kd, N), dtype=FP8, device=wq.device)
+    wsT = torch.empty((E, Kd // GROUP, N // GROUP), dtype=torch.float32, device=wq.device)
+    _C.call("smoe_transpose_blockwise_fp8", _ptr(_bytes(wq)), _ptr(ws), E, N, Kd,
+            _ptr(wqT), _ptr(wsT), _stream())
+    return wqT, wsT
+
+
+def quant_cols(x: torch.Tensor, offsets: torch.Tensor):
+    """Transposed 128x1 quantisation of x [R,C] bf16 over the expert row
+    segments ``offsets`` (E+1).  -> (xTq [C, ld] fp8, xTs [C, ld/128] f32,
+    pad [E+1] i32, ld) where pad are the 128-aligned segment starts."""
+    _check(x, "x", (torch.bfloat16,), 2)
+    _check(offsets, "offsets", (torch.int32,), 1)
+    R, C = x.shape
+    E = offsets.numel() - 1
+    ld = int(_C.lib().smoe_quant_cols_ld(R, E))
+    xTq = torch.empty((C, ld), dtype=FP8, device=x.device)
+    xTs = torch.empty((C, ld // GROUP), dtype=torch.float32, device=x.device)
+    pad = torch.empty(E + 1, dtype=torch.int32, device=x.device)
+    _C.call("smoe_quant_cols_128x1", _ptr(x), R, C, _ptr(offsets), E, ld, _ptr(xTq), _ptr(xTs),
+            _ptr(pad), _stream())
+    return xTq, xTs, pad, ld
+
+
+def grouped_gemm_fp8_wgrad(aTq, aTs, bTq, bTs, pad, ld: int) -> torch.Tensor:
+    """dW[e] = A_e^T B_e over each expert's rows from quant_cols operands:
+    aT [N, ld], bT [K, ld] -> fp32 [E, N, K]."""
+    _check(aTq, "aTq", (FP8, torch.uint8), 2)
+    _check(bTq, "bTq", (FP8, torch.uint8), 2)
+    _check(pad, "pad", (torch.int32,), 1)
+    N, K, E = aTq.shape[0], bTq.shape[0], pad.numel() - 1
+    if aTq.shape[1] != ld or bTq.shape[1] != ld:
+        raise ValueError("operands must share the padded row length ld")
+    dW = torch.empty((E, N, K), dtype=torch.float32, device=aTq.device)
+    _C.call("smoe_grouped_gemm_fp8_wgrad", _ptr(_bytes(aTq)), _ptr(aTs), _ptr(_bytes(bTq)),
+            _ptr(bTs), _ptr(pad), E, N, K, ld, _ptr(dW), _stream())
+    return dW
+
+
+def swiglu_bwd(c1: torch.Tensor, dh: torch.Tensor) -> torch.Tensor:
+    """c1 [R,2I] (gate | up), dh [R,I] bf16 -> dc1 [R,2I] bf16 = [dg | du]."""
+    _check(c1, "c1", (torch.bfloat16,), 2)
+    _check(dh, "dh", (torch.bfloat16,), 2)
+    R, I2 = c1.shape
+    if dh.shape != (R, I2 // 2):
+        raise ValueError("dh must be [R, I]")
+    dc1 = torch.empty_like(c1)
+    _C.call("smoe_swiglu_bwd", _ptr(c1), _ptr(dh), R, I2 // 2, _ptr(dc1), _stream())
+    return dc1
+
+
+def unpermute_combine_bwd(dout: torch.Tensor, y: torch.Tensor, inv_map: torch.Tensor,
+                          topk_w: torch.Tensor):
+    """Backward of unpermute_combine: -> (dy [T*K,H] bf16, dw [T,K] f32)."""
+    _check(dout, "dout", (torch.bfloat16,), 2)
+    _check(y, "y", (torch.bfloat16,), 2)
+    _check(inv_map, "inv_map", (torch.int32,))
+    _check(topk_w, "topk_w", (torch.float32,), 2)
+    T, K = topk_w.shape
+    H = dout.shape[1]
+    dy = torch.empty((T * K, H), dtype=torch.bfloat16, device=dout.device)
+    dw = torch.empty((T, K), dtype=torch.float32, device=dout.device)
+    _C.call("smoe_unpermute_combine_bwd", _ptr(dout), _ptr(y), _ptr(inv_map), _ptr(topk_w), T, K,
+            H, _ptr(dy), _ptr(dw), _stream())
+    return dy, dw

@@ -1,0 +1,229 @@
+"""GPU parity of the backward-pass kernels (config 5: fp8 dgrad and wgrad
+grouped GEMMs with transposed 128x1 requantisation) against the CPU oracle.
+
+Bars: bit-exact for row/column quantisation bytes and scales, the weight
+transpose, the SwiGLU backward and the combine-backward dy; the dgrad GEMM
+(bf16 output) within max 1e-2 / mean 1e-3 of the float64 oracle rounded to
+bf16; the wgrad GEMM (fp32 output) and the router-weight gradient within
+max 1e-2 / mean 1e-3 of the float64 oracle."""
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import smoe_oracle as O
+import smoe
+from smoe import ops, workloads as W
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+
+
+def u16(t):
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def u8(t):
+    return t.detach().cpu().contiguous().view(torch.uint8).numpy()
+
+
+def bf(u, dev):
+    return torch.from_numpy(np.ascontiguousarray(u).view(np.int16)).view(torch.bfloat16).to(dev)
+
+
+def close(got, ref, what, bf16_out=False, mx_tol=1e-2, mn_tol=1e-3):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    if bf16_out:
+        ref = O.bf16_to_f32(O.f32_to_bf16(ref.astype(np.float32))).astype(np.float64)
+    d = np.abs(got - ref)
+    mx = d.max() / max(np.abs(ref).max(), 1e-30)
+    mn = d.mean() / max(np.abs(ref).mean(), 1e-30)
+    assert mx <= mx_tol and mn <= mn_tol, f"{what}: max_rel={mx:.3e} mean_rel={mn:.3e}"
+
+
+def _offsets(counts):
+    return np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+
+
+@pytest.mark.parametrize("M,C", [(1000, 2048), (7, 768), (130, 1536)])
+def test_quant_rows_bit_exact(dev, M, C):
+    say("quant_rows", M, C)
+    x = W.tokens(M, C, seed=M + C)
+    q, s = ops.quant_rows(x.to(dev))
+    rq, rs = O.quant_1x128(O.bf16_to_f32(u16(x)))
+    assert np.array_equal(u8(q), rq) and np.array_equal(s.cpu().numpy(), rs)
+
+
+@pytest.mark.parametrize("E,N,K", [(3, 256, 384), (2, 768, 2048), (1, 128, 128)])
+def test_transpose_blockwise_bit_exact(dev, E, N, K):
+    say("transpose", E, N, K)
+    w = W.weights(E, N, K, seed=E + N)
+    wq, ws = ops.quantize_weight_blockwise(w.to(dev))
+    tq, ts = ops.transpose_blockwise(wq, ws)
+    rq, rs = O.transpose_blockwise(u8(wq), ws.cpu().numpy())
+    assert np.array_equal(u8(tq), rq) and np.array_equal(ts.cpu().numpy(), rs)
+
+
+@pytest.mark.parametrize("counts,C", [([130, 0, 5, 256, 1], 256), ([1000, 24, 0, 2000], 768),
+                                      ([128], 128), ([0, 0, 3], 1536)])
+def test_quant_cols_bit_exact(dev, counts, C):
+    say("quant_cols", counts, C)
+    off = _offsets(counts)
+    R = int(off[-1])
+    x = W.tokens(R, C, seed=R + C)
+    q, s, pad, ld = ops.quant_cols(x.to(dev), torch.from_numpy(off).to(dev))
+    rq, rs, rpad = O.quant_cols_128x1(O.bf16_to_f32(u16(x)), off)
+    Rp = int(rpad[-1])
+    assert np.array_equal(pad.cpu().numpy(), rpad)
+    assert np.array_equal(u8(q)[:, :Rp], rq)
+    assert np.array_equal(s.cpu().numpy()[:, :Rp // 128], rs)
+
+
+@pytest.mark.parametrize("counts,N,K", [([3, 0, 200, 129], 256, 384), ([1024] * 4, 768, 2048),
+                                        ([0, 0], 128, 128), ([5000, 17], 2048, 768)])
+def test_wgrad_gemm(dev, counts, N, K):
+    say("wgrad", counts, N, K)
+    off = _offsets(counts)
+    R = int(off[-1])
+    E = len(counts)
+    if R == 0:
+        a = torch.zeros((1, N), dtype=torch.bfloat16, device=dev)
+        off_t = torch.from_numpy(off).to(dev)
+        aq, as_, pad, ld = ops.quant_cols(a, torch.tensor([0] * (E + 1), dtype=torch.int32, device=dev))
+        bq, bs_, _, _ = ops.quant_cols(torch.zeros((1, K), dtype=torch.bfloat16, device=dev),
+                                       torch.tensor([0] * (E + 1), dtype=torch.int32, device=dev))
+        dW = ops.grouped_gemm_fp8_wgrad(aq, as_, bq, bs_, pad, ld)
+        assert not dW.any()
+        return
+    dy = W.tokens(R, N, seed=R + 1)
+    h = W.tokens(R, K, seed=R + 2)
+    off_t = torch.from_numpy(off).to(dev)
+    aq, as_, pad, ld = ops.quant_cols(dy.to(dev), off_t)
+    bq, bs_, _, _ = ops.quant_cols(h.to(dev), off_t)
+    dW = ops.grouped_gemm_fp8_wgrad(aq, as_, bq, bs_, pad, ld)
+    raq, ras, rpad = O.quant_cols_128x1(O.bf16_to_f32(u16(dy)), off)
+    rbq, rbs, _ = O.quant_cols_128x1(O.bf16_to_f32(u16(h)), off)
+    ref = O.grouped_gemm_fp8_wgrad(raq, ras, rbq, rbs, rpad, E)
+    got = dW.cpu().numpy()
+    for e in range(E):
+        if counts[e] == 0:
+            assert not got[e].any()
+    close(got, ref, f"wgrad {counts}")
+
+
+@pytest.mark.parametrize("R,I", [(1000, 768), (9, 2048), (300, 128)])
+def test_swiglu_bwd_bit_exact(dev, R, I):
+    say("swiglu_bwd", R, I)
+    rng = np.random.default_rng(R + I)
+    c1 = O.f32_to_bf16((rng.standard_normal((R, 2 * I)) * 4).astype(np.float32))
+    c1[0, :6] = O.f32_to_bf16(np.array([0, 100, -100, 88.5, -88.5, -87.2], np.float32))
+    dh = O.f32_to_bf16(rng.standard_normal((R, I)).astype(np.float32))
+    got = ops.swiglu_bwd(bf(c1, dev), bf(dh, dev))
+    assert np.array_equal(u16(got), O.swiglu_bwd(c1, dh))
+
+
+@pytest.mark.parametrize("R,I", [(777, 768), (5, 2048)])
+def test_swiglu_quant_saved_h(dev, R, I):
+    say("swiglu_quant save_h", R, I)
+    rng = np.random.default_rng(R)
+    c1 = O.f32_to_bf16((rng.standard_normal((R, 2 * I)) * 3).astype(np.float32))
+    hq, hs, h = ops.swiglu_quant(bf(c1, dev), save_h=True)
+    rq, rs = O.swiglu_quant(c1)
+    f = O.bf16_to_f32(c1)
+    rh = O.f32_to_bf16((O.silu_f32(f[:, :I]) * f[:, I:]).astype(np.float32))
+    assert np.array_equal(u8(hq), rq) and np.array_equal(hs.cpu().numpy(), rs)
+    assert np.array_equal(u16(h), rh)
+
+
+@pytest.mark.parametrize("T,K,H", [(1000, 8, 2048), (33, 2, 1024), (5, 1, 128)])
+def test_combine_bwd(dev, T, K, H):
+    say("combine_bwd", T, K, H)
+    rng = np.random.default_rng(T + K)
+    dout = O.f32_to_bf16(rng.standard_normal((T, H)).astype(np.float32))
+    y = O.f32_to_bf16(rng.standard_normal((T * K, H)).astype(np.float32))
+    inv = rng.permutation(T * K).astype(np.int32)
+    w = rng.random((T, K)).astype(np.float32)
+    dy, dw = ops.unpermute_combine_bwd(bf(dout, dev), bf(y, dev), torch.from_numpy(inv).to(dev),
+                                       torch.from_numpy(w).to(dev))
+    rdy, rdw = O.combine_bwd(dout, y, inv, w, K)
+    assert np.array_equal(u16(dy), rdy)
+    close(dw.cpu().numpy(), rdw, "dw")
+
+
+def _layer(dev, T, H, I, E, K, seed=0):
+    m = smoe.SimpleMoE(H, I, E, K, device=dev)
+    with torch.no_grad():
+        m.w1.copy_(W.weights(E, 2 * I, H, seed=3 + seed).to(dev))
+        m.w2.copy_(W.weights(E, H, I, seed=13 + seed).to(dev))
+    x, lg = W.tokens(T, H, seed=seed), W.logits(T, E, seed=1 + seed)
+    return m, x, lg
+
+
+def _layer_case(dev, T, H, I, E, K):
+    m, x, lg = _layer(dev, T, H, I, E, K)
+    out, st = m(x.to(dev), lg.to(dev), return_intermediates=True)
+    dout = W.tokens(T, H, seed=4)
+    w1q, w1s, w2q, w2s = m.fp8_weights()
+    fwd = {k: (u16(v) if v.dtype == torch.bfloat16 else v.cpu().numpy())
+           for k, v in st.items() if k in ("topk_w", "row_map", "inv_map", "offsets", "c1", "y")}
+    r = O.moe_backward(fwd, u16(x), u8(w1q), w1s.cpu().numpy(), u8(w2q), w2s.cpu().numpy(),
+                       u16(dout), K)
+    return m, x, st, dout, fwd, r
+
+
+CASES = [(256, 256, 256, 8, 2), (1024, 2048, 768, 128, 8)]
+
+
+@pytest.mark.parametrize("T,H,I,E,K", CASES)
+def test_layer_backward_stagewise(dev, T, H, I, E, K):
+    """Each backward stage on the GPU, fed the oracle's previous-stage output
+    (so fp8 requantisation flips cannot cascade), against the oracle; the
+    config-5 layer shape H=2048, I=768, E=128, top-8 at T=1024."""
+    say("layer backward stagewise", T, H, I, E, K)
+    m, x, st, dout, fwd, r = _layer_case(dev, T, H, I, E, K)
+    w1q, w1s, w2q, w2s = m.fp8_weights()
+    off, inv = st["offsets"], st["inv_map"]
+    f = lambda a: O.bf16_to_f32(a).astype(np.float64)
+    dy, dw = ops.unpermute_combine_bwd(dout.to(dev), st["y"], inv, st["topk_w"])
+    assert np.array_equal(u16(dy), r["dy"])
+    close(dw.cpu().numpy(), r["dw"], "dtopk_w")
+    w2tq, w2ts = ops.transpose_blockwise(w2q, w2s)
+    dh = ops.grouped_gemm_fp8(*ops.quant_rows(dy), w2tq, w2ts, off)
+    close(f(u16(dh)), f(r["dh"]), "dh", bf16_out=True)
+    aq, as_, pad, ld = ops.quant_cols(dy, off)
+    bq, bs_, _, _ = ops.quant_cols(st["h"], off)
+    close(ops.grouped_gemm_fp8_wgrad(aq, as_, bq, bs_, pad, ld).cpu().numpy(), r["dW2"], "dW2")
+    dc1 = ops.swiglu_bwd(st["c1"], bf(r["dh"], dev))
+    assert np.array_equal(u16(dc1), r["dc1"])
+    w1tq, w1ts = ops.transpose_blockwise(w1q, w1s)
+    dxs = ops.grouped_gemm_fp8(*ops.quant_rows(dc1), w1tq, w1ts, off)
+    close(f(u16(dxs)), f(r["dxs"]), "dxs", bf16_out=True)
+    xs = x.to(dev).index_select(0, (st["row_map"] // K).long())
+    cq, cs, _, _ = ops.quant_cols(dc1, off)
+    xq, xs_s, _, _ = ops.quant_cols(xs, off)
+    close(ops.grouped_gemm_fp8_wgrad(cq, cs, xq, xs_s, pad, ld).cpu().numpy(), r["dW1"], "dW1")
+    dx = ops.unpermute_combine(bf(r["dxs"], dev), inv, torch.ones_like(st["topk_w"]))
+    assert np.array_equal(u16(dx), r["dx"])
+
+
+@pytest.mark.parametrize("T,H,I,E,K", CASES)
+def test_layer_backward_end_to_end(dev, T, H, I, E, K):
+    """SimpleMoE.backward_from end to end.  Requantisation flips cascade
+    through dc1, so the max bound is 2e-2 here (mean stays 1e-3); the
+    per-stage bars are held by test_layer_backward_stagewise."""
+    say("layer backward e2e", T, H, I, E, K)
+    m, x, st, dout, fwd, r = _layer_case(dev, T, H, I, E, K)
+    g = m.backward_from(st, dout.to(dev))
+    f = lambda a: O.bf16_to_f32(a).astype(np.float64)
+    assert np.array_equal(u16(g["dy"]), r["dy"])
+    close(g["dw2"].cpu().numpy(), r["dW2"], "dW2")
+    close(g["dw1"].cpu().numpy(), r["dW1"], "dW1", mx_tol=2e-2)
+    close(f(u16(g["dx"])), f(r["dx"]), "dx", mx_tol=2e-2)
+    close(g["dtopk_w"].cpu().numpy(), r["dw"], "dtopk_w")

@@ -287,3 +287,116 @@ def test_oracle_tiny_fixture_regression():
     assert np.abs(out - ref).max() <= 0.1 * np.abs(ref).max()
     assert np.abs(out - ref).mean() <= 0.05 * np.abs(ref).mean()
     assert E == 4
+
+
+# ------------------------------------------------------------- backward
+def test_transpose_blockwise_commutes_with_dequant():
+    rng = np.random.default_rng(8)
+    w = O.f32_to_bf16((rng.standard_normal((2, 256, 384)) * 0.02).astype(np.float32))
+    wq, ws = O.quantize_weight_blockwise(w)
+    tq, ts = O.transpose_blockwise(wq, ws)
+    for e in range(2):
+        assert np.array_equal(O.dequant_weight(tq[e], ts[e]), O.dequant_weight(wq[e], ws[e]).T)
+    # requantising the transposed dequantised block gives the same bytes
+    rq, rs = O.quantize_weight_blockwise(O.f32_to_bf16(O.bf16_to_f32(w).transpose(0, 2, 1).copy()))
+    assert np.array_equal(rq, tq) and np.array_equal(rs, ts)
+
+
+def test_quant_cols_matches_padded_transpose_and_closed_form():
+    rng = np.random.default_rng(9)
+    counts = [130, 0, 5, 256, 1]
+    off = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    R, C = off[-1], 256
+    x = rng.standard_normal((R, C)).astype(np.float32)
+    q, s, pad = O.quant_cols_128x1(x, off)
+    assert pad.tolist() == [0, 256, 256, 384, 640, 768]
+    # independent construction: per expert, per column, python slicing
+    for e, cnt in enumerate(counts):
+        for g0 in range(0, cnt, 128):
+            rows = x[off[e] + g0: off[e] + min(cnt, g0 + 128)]
+            for col in (0, 77, 255):
+                seg = rows[:, col]
+                amax = np.float32(np.abs(seg).max())
+                sc = np.float32(1.0) if amax == 0 else amax / np.float32(448)
+                pos = pad[e] + g0
+                assert s[col, pos // 128] == sc
+                assert np.array_equal(q[col, pos:pos + seg.size], O.quant_rule(seg, sc))
+                assert not q[col, pos + seg.size:pos + 128].any()  # zero padding
+
+
+def test_wgrad_brute_force():
+    rng = np.random.default_rng(10)
+    counts = [3, 0, 200]
+    off = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    R = off[-1]
+    dy = rng.standard_normal((R, 128)).astype(np.float32)
+    h = rng.standard_normal((R, 256)).astype(np.float32)
+    aq, as_, pad = O.quant_cols_128x1(dy, off)
+    bq, bs_, _ = O.quant_cols_128x1(h, off)
+    dW = O.grouped_gemm_fp8_wgrad(aq, as_, bq, bs_, pad, 3)
+    assert not dW[1].any()
+    A = O.e4m3_decode(aq).astype(np.float64)
+    B = O.e4m3_decode(bq).astype(np.float64)
+    for e in (0, 2):
+        for n, k in ((0, 0), (5, 200), (127, 31)):
+            ref = 0.0
+            for r in range(pad[e], pad[e + 1]):
+                ref += A[n, r] * float(as_[n, r // 128]) * B[k, r] * float(bs_[k, r // 128])
+            assert abs(dW[e, n, k] - ref) <= 1e-9 * max(1, abs(ref))
+    # and it approximates the unquantised product
+    ref = dy[off[2]:].astype(np.float64).T @ h[off[2]:].astype(np.float64)
+    assert np.abs(dW[2] - ref).max() <= 0.1 * np.abs(ref).max()
+
+
+def test_swiglu_bwd_matches_float64_derivative():
+    rng = np.random.default_rng(11)
+    c1 = O.f32_to_bf16((rng.standard_normal((16, 512)) * 3).astype(np.float32))
+    dh = O.f32_to_bf16(rng.standard_normal((16, 256)).astype(np.float32))
+    dc = O.bf16_to_f32(O.swiglu_bwd(c1, dh)).astype(np.float64)
+    c = O.bf16_to_f32(c1).astype(np.float64)
+    d = O.bf16_to_f32(dh).astype(np.float64)
+    g, u = c[:, :256], c[:, 256:]
+    s = 1 / (1 + np.exp(-g))
+    ref = np.concatenate([d * u * s * (1 + g * (1 - s)), d * g * s], axis=1)
+    assert np.abs(dc - ref).max() <= 2 ** -7 * np.abs(ref).max()
+    # finite differences on the gate
+    eps = 1e-6
+    f = lambda gg: gg / (1 + np.exp(-gg)) * u
+    num = (f(g + eps) - f(g - eps)) / (2 * eps) * d
+    assert np.abs(ref[:, :256] - num).max() <= 1e-6 * np.abs(num).max() + 1e-9
+
+
+def test_moe_backward_against_float64_autograd():
+    """The whole backward against torch autograd in float64 on the
+    dequantised weights with the same routing: quantisation noise only."""
+    g = np.load(os.path.join(GOLDEN, "oracle_tiny.npz"))
+    K = int(g["K"])
+    rng = np.random.default_rng(12)
+    dout = O.f32_to_bf16(rng.standard_normal(g["out"].shape).astype(np.float32))
+    fwd = {k: g[k] for k in ("topk_idx", "topk_w", "row_map", "inv_map", "offsets", "c1", "y")}
+    b = O.moe_backward(fwd, g["x"], g["w1q"], g["w1s"], g["w2q"], g["w2s"], dout, K)
+    E = g["w1q"].shape[0]
+    W1 = torch.tensor(np.stack([O.dequant_weight(g["w1q"][e], g["w1s"][e]) for e in range(E)]), requires_grad=True)
+    W2 = torch.tensor(np.stack([O.dequant_weight(g["w2q"][e], g["w2s"][e]) for e in range(E)]), requires_grad=True)
+    x = torch.tensor(O.bf16_to_f32(g["x"]).astype(np.float64), requires_grad=True)
+    wts = torch.tensor(g["topk_w"].astype(np.float64), requires_grad=True)
+    T = x.shape[0]
+    out = torch.zeros_like(x)
+    outs = []
+    for t in range(T):
+        acc = 0
+        for k in range(K):
+            e = int(g["topk_idx"][t, k])
+            c = W1[e] @ x[t]
+            I = c.shape[0] // 2
+            h = torch.nn.functional.silu(c[:I]) * c[I:]
+            acc = acc + wts[t, k] * (W2[e] @ h)
+        outs.append(acc)
+    out = torch.stack(outs)
+    loss = (out * torch.tensor(O.bf16_to_f32(dout).astype(np.float64))).sum()
+    loss.backward()
+    rel = lambda a, r: np.abs(a - r).max() / np.abs(r).max()
+    assert rel(O.bf16_to_f32(b["dx"]).astype(np.float64), x.grad.numpy()) < 0.1
+    assert rel(b["dW1"], W1.grad.numpy()) < 0.1
+    assert rel(b["dW2"], W2.grad.numpy()) < 0.1
+    assert rel(b["dw"], wts.grad.numpy()) < 0.08
