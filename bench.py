@@ -14,7 +14,8 @@ Also reported on the same line:
                 sample of the same workload, on this host's cores;
   extra         fp8 grouped GEMM TFLOPS on benchmark config 4 (DeepSeek-V3
                 local experts, Zipf loads, fc1 + fc2), the combine GB/s at
-                config-2 size, and the whole SimpleMoE forward of config 3.
+                config-2 size, the whole SimpleMoE forward of config 3 and the
+                forward+backward step of config 5.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--skip-extra]
 """
@@ -157,6 +158,37 @@ def bench_layer(dev, steps, warmup):
             "ms": round(t, 4), "tflops": round(fl / (t * 1e-3) / 1e12, 1)}
 
 
+def bench_fwd_bwd(dev, steps, warmup):
+    """Benchmark config 5 (Qwen3-30B-A3B-shaped expert layer, T=16384, H=2048,
+    I=768, E=128, top-8): one forward with saved intermediates plus the full
+    fp8 backward (dgrad + wgrad for fc1 and fc2), 3.71e12 FLOP per step."""
+    import torch
+    import smoe
+    from smoe import workloads as W
+    c = W.CONFIGS["qwen3"]
+    m = smoe.SimpleMoE(c.H, c.I, c.E, c.K, device=dev)
+    with torch.no_grad():
+        m.w1.copy_(W.weights(c.E, 2 * c.I, c.H, device=dev))
+        m.w2.copy_(W.weights(c.E, c.H, c.I, device=dev, seed=13))
+    m.refresh_fp8_cache()
+    x, lg = W.tokens(c.T, c.H, device=dev), W.logits(c.T, c.E, device=dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(4)
+    dout = (torch.randn((c.T, c.H), generator=g, device=dev) * 1e-3).to(torch.bfloat16)
+
+    def step():
+        _, st = m(x, lg, return_intermediates=True)
+        m.backward_from(st, dout)
+
+    t = timed(step, steps, warmup)
+    R = c.T * c.K
+    fwd = 2.0 * R * (2 * c.I) * c.H + 2.0 * R * c.H * c.I
+    del m
+    torch.cuda.empty_cache()
+    return {"workload": "qwen3 layer fwd+bwd T=16384 H=2048 I=768 E=128 top8",
+            "ms": round(t, 4), "tflops": round(3 * fwd / (t * 1e-3) / 1e12, 1)}
+
+
 def run_only(args, dev, c):
     """One kernel family, for profiler runs: permute = the dispatch step
     (route sort + permute_quant), gemm = DSv3 fc1 + fc2, combine = config-2
@@ -175,6 +207,8 @@ def run_only(args, dev, c):
         ms = timed(lambda: ops.permute_quant(x, idx, c.E), args.steps, args.warmup)
         print(json.dumps({"only": "permute", "ms": ms,
                           "gbs": dispatch_bytes(c.T, c.H, c.E, c.K) / (ms * 1e-3) / 1e9}))
+    elif args.only == "fwdbwd":
+        print(json.dumps({"only": "fwdbwd", **bench_fwd_bwd(dev, args.steps, args.warmup)}))
     elif args.only == "gemm":
         print(json.dumps({"only": "gemm", **bench_gemm(dev, args.steps, args.warmup)}))
     else:
@@ -188,7 +222,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-extra", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--only", choices=["permute", "gemm", "combine", "copy"],
+    ap.add_argument("--only", choices=["permute", "gemm", "combine", "copy", "fwdbwd"],
                     help="run one kernel family only (for rocprofv3 runs) and print its timing")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -262,6 +296,8 @@ def main():
         log("combine", extra["combine_cfg2"])
         extra["layer_mixtral"] = bench_layer(dev, 3, 1)
         log("layer", extra["layer_mixtral"])
+        extra["layer_qwen3_fwd_bwd"] = bench_fwd_bwd(dev, 3, 1)
+        log("fwd+bwd", extra["layer_qwen3_fwd_bwd"])
 
     cpu = None if args.skip_cpu else cpu_baseline(c)
     line = {"metric": "fp8 grouped-GEMM TFLOPS & permute-quant GB/s, % of MI355X roofline, 1 GPU",

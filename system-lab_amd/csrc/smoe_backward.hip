@@ -67,19 +67,28 @@ __global__ __launch_bounds__(1024) void pad_offsets_kernel(const int32_t* __rest
 }
 
 // --------------------------------------------- 128x1 column quantisation
-// One 256-thread workgroup per (128-row group, 64-column slab).  The group's
+// One 256-thread workgroup per (128-row group, 128-column slab).  The group's
 // rows (an expert's rows split into 128-row groups from its first row; short
-// last groups are zero-padded) are staged as fp32 in LDS; thread t owns
-// column t/4 and rows (t%4)*32 .. +32 of the group; the column amax is a
-// 2-step shuffle over the 4 threads of a column.  The 128 fp8 bytes of a
-// column land contiguously in the transposed output row (ld bytes apart).
-__global__ __launch_bounds__(256) void quant_cols_kernel(const uint16_t* __restrict__ x, int C,
-                                                         const int32_t* __restrict__ offsets,
-                                                         const int32_t* __restrict__ pad, int E,
-                                                         int ld, uint8_t* __restrict__ q,
-                                                         float* __restrict__ s) {
-  __shared__ float tile[128][65];
+// last groups are zero-padded) are loaded with 8 128-bit non-temporal loads
+// per thread (16 threads per 256-byte row slice), optionally gathered through
+// src = gather[r] / gather_div, and staged as bf16 in LDS.  Thread t then owns
+// column t % 128 and rows (t / 128) * 64 .. +64, so the two halves of a
+// column sit in different waves and every wave reads 64 consecutive columns
+// of one row at a time (conflict-free).  A first pass over LDS finds the
+// half-column amax (the halves meet in LDS), a second quantises; keeping the
+// values in LDS rather than registers leaves room for more resident waves.
+// Each thread writes its 64 fp8 bytes as 4 128-bit stores into the transposed
+// output row (ld bytes apart); the two halves of a row chunk merge in L2.
+constexpr int kQcCols = 128;
+constexpr int kQcPitch = kQcCols + 8;
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void quant_cols_kernel(
+    const uint16_t* __restrict__ x, const int32_t* __restrict__ gather, int gather_div, int C,
+    const int32_t* __restrict__ offsets, const int32_t* __restrict__ pad, int E, int ld,
+    uint8_t* __restrict__ q, float* __restrict__ s) {
+  __shared__ __attribute__((aligned(16))) uint16_t tile[kGroup * kQcPitch];
   __shared__ int pad_l[SMOE_MAX_EXPERTS + 1];
+  __shared__ float hmax[2][kQcCols];
   const int t = threadIdx.x;
   for (int i = t; i <= E; i += 256) pad_l[i] = pad[i];
   __syncthreads();
@@ -94,50 +103,52 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(const uint16_t* __restr
   const int e = lo;
   const int row0 = offsets[e] + (gpos - pad_l[e]);
   const int valid = min(kGroup, offsets[e + 1] - row0);
-  const int c0 = blockIdx.y * 64;
-  // stage 128 x 64 bf16 as fp32: each thread 4 x (8 bf16)
+  const int c0 = blockIdx.y * kQcCols;
+  const int cc = (t & 15) * 8;  // this thread's 8 columns of each row slice
+  v4u v[8];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int idx = j * 256 + t;
-    const int r = idx >> 3, cc = (idx & 7) * 8;
-    float f[8];
+  for (int j = 0; j < 8; ++j) {
+    const int r = j * 16 + (t >> 4);
+    v[j] = v4u{0u, 0u, 0u, 0u};
     if (r < valid && c0 + cc < C) {
-      const uint4 v = *(const uint4*)(x + (size_t)(row0 + r) * C + c0 + cc);
-      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        f[2 * i] = __uint_as_float(w[i] << 16);
-        f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) f[i] = 0.0f;
+      const int src = gather ? gather[row0 + r] / gather_div : row0 + r;
+      v[j] = __builtin_nontemporal_load((const v4u*)(x + (size_t)src * C + c0 + cc));
     }
+  }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) tile[r][cc + i] = f[i];
+  for (int j = 0; j < 8; ++j) {
+    const int r = j * 16 + (t >> 4);
+    *(v4u*)&tile[r * kQcPitch + cc] = v[j];
   }
   __syncthreads();
-  const int col = t >> 2, part = t & 3;
-  if (c0 + col >= C) return;
-  float v[32];
+  const int col = t & (kQcCols - 1), half = t >> 7;
+  const uint16_t* tcol = tile + half * 64 * kQcPitch + col;
   float amax = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 32; ++i) {
-    v[i] = tile[part * 32 + i][col];
-    amax = fmaxf(amax, fabsf(v[i]));
-  }
-  amax = fmaxf(amax, __shfl_xor(amax, 1, 4));
-  amax = fmaxf(amax, __shfl_xor(amax, 2, 4));
+#pragma unroll 16
+  for (int i = 0; i < 64; ++i)
+    amax = fmaxf(amax, fabsf(__uint_as_float((uint32_t)tcol[i * kQcPitch] << 16)));
+  hmax[half][col] = amax;
+  __syncthreads();
+  if (c0 + col >= C) return;
+  amax = fmaxf(hmax[0][col], hmax[1][col]);
   const float sc = group_scale(amax);
-  uint32_t w[8];
+  uint8_t* dst = q + (size_t)(c0 + col) * ld + gpos + half * 64;
+#pragma unroll 1
+  for (int i0 = 0; i0 < 64; i0 += 16) {
+    uint32_t w[4];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
-    w[i] = quant_one(v[4 * i], sc) | (quant_one(v[4 * i + 1], sc) << 8) |
-           (quant_one(v[4 * i + 2], sc) << 16) | (quant_one(v[4 * i + 3], sc) << 24);
-  uint8_t* dst = q + (size_t)(c0 + col) * ld + gpos + part * 32;
-  *(uint4*)dst = make_uint4(w[0], w[1], w[2], w[3]);
-  *(uint4*)(dst + 16) = make_uint4(w[4], w[5], w[6], w[7]);
-  if (part == 0) s[(size_t)(c0 + col) * (ld / kGroup) + gpos / kGroup] = sc;
+    for (int i = 0; i < 4; ++i) {
+      uint32_t b = 0;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float f = __uint_as_float((uint32_t)tcol[(i0 + 4 * i + k) * kQcPitch] << 16);
+        b |= quant_one(f, sc) << (8 * k);
+      }
+      w[i] = b;
+    }
+    *(uint4*)(dst + i0) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+  if (half == 0) s[(size_t)(c0 + col) * (ld / kGroup) + gpos / kGroup] = sc;
 }
 
 // ------------------------------------------------------- SwiGLU backward
@@ -265,10 +276,12 @@ extern "C" int smoe_quant_cols_ld(int R, int E) {
   return ld > 0x7fffffffLL ? 0 : (int)ld;
 }
 
-extern "C" int smoe_quant_cols_128x1(const uint16_t* x, int R, int C, const int32_t* offsets,
-                                     int E, int ld, uint8_t* xTq, float* xTs, int32_t* pad,
-                                     void* stream) {
+extern "C" int smoe_quant_cols_128x1(const uint16_t* x, const int32_t* gather, int gather_div,
+                                     int R, int C, const int32_t* offsets, int E, int ld,
+                                     uint8_t* xTq, float* xTs, int32_t* pad, void* stream) {
   if (R <= 0 || C <= 0) return SMOE_EINVAL_DIM;
+  if (gather && gather_div <= 0) return SMOE_EINVAL_DIM;
+  if (gather && ((uintptr_t)gather & 3u)) return SMOE_EINVAL_PTRALIGN;
   if (E <= 0 || E > SMOE_MAX_EXPERTS) return SMOE_EINVAL_EXPERTS;
   if (C % kGroup) return SMOE_EINVAL_ALIGN128;
   if (ld < smoe_quant_cols_ld(R, E) || ld % kGroup) return SMOE_EINVAL_DIM;
@@ -278,8 +291,8 @@ extern "C" int smoe_quant_cols_128x1(const uint16_t* x, int R, int C, const int3
   if (((uintptr_t)offsets | (uintptr_t)xTs | (uintptr_t)pad) & 3u) return SMOE_EINVAL_PTRALIGN;
   hipStream_t s = (hipStream_t)stream;
   pad_offsets_kernel<<<1, 1024, 0, s>>>(offsets, E, pad);
-  quant_cols_kernel<<<dim3(ld / kGroup, C / 64), dim3(256), 0, s>>>(x, C, offsets, pad, E, ld,
-                                                                    xTq, xTs);
+  quant_cols_kernel<<<dim3(ld / kGroup, (C + kQcCols - 1) / kQcCols), dim3(256), 0, s>>>(
+      x, gather, gather ? gather_div : 1, C, offsets, pad, E, ld, xTq, xTs);
   SMOE_RETURN_LAUNCH();
 }
 

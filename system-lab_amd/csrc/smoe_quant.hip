@@ -32,7 +32,8 @@ __device__ __forceinline__ Q16 quant16(const float (&f)[16]) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     w[i] = quant_one(f[4 * i], s) | (quant_one(f[4 * i + 1], s) << 8) |
-           (quant_one(f[4 * i + 2], s) << 16) | (quant_one(f[4 * i + 3], s) << 24);
+           (quant_one(f[4 * i + 2], s) << 16) |
+           (quant_one(f[4 * i + 3], s) << 24);
   }
   Q16 r;
   r.q = make_uint4(w[0], w[1], w[2], w[3]);

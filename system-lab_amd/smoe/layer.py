@@ -106,9 +106,9 @@ class SimpleMoE(nn.Module):
         dc1 = ops.swiglu_bwd(inter["c1"], dh)
         dcq, dcs = ops.quant_rows(dc1)
         dxs = ops.grouped_gemm_fp8(dcq, dcs, w1tq, w1ts, off)
-        xs = inter["x"].index_select(0, (inter["row_map"] // K).long())
         dcTq, dcTs, _, _ = ops.quant_cols(dc1, off)
-        xTq, xTs, _, _ = ops.quant_cols(xs, off)
+        # the sorted tokens x[row_map // K], gathered inside the quantiser
+        xTq, xTs, _, _ = ops.quant_cols(inter["x"], off, gather=inter["row_map"], gather_div=K)
         dw1 = ops.grouped_gemm_fp8_wgrad(dcTq, dcTs, xTq, xTs, pad, ld)
         ones = torch.ones_like(inter["topk_w"])
         dx = ops.unpermute_combine(dxs, inv, ones)

@@ -231,20 +231,27 @@ def transpose_blockwise(wq: torch.Tensor, ws: torch.Tensor):
     return wqT, wsT
 
 
-def quant_cols(x: torch.Tensor, offsets: torch.Tensor):
-    """Transposed 128x1 quantisation of x [R,C] bf16 over the expert row
-    segments ``offsets`` (E+1).  -> (xTq [C, ld] fp8, xTs [C, ld/128] f32,
+def quant_cols(x: torch.Tensor, offsets: torch.Tensor, gather: torch.Tensor | None = None,
+               gather_div: int = 1):
+    """Transposed 128x1 quantisation over the expert row segments ``offsets``
+    (E+1) of x [R,C] bf16, or, with ``gather`` [R] i32, of the rows
+    x[gather[r] // gather_div].  -> (xTq [C, ld] fp8, xTs [C, ld/128] f32,
     pad [E+1] i32, ld) where pad are the 128-aligned segment starts."""
     _check(x, "x", (torch.bfloat16,), 2)
     _check(offsets, "offsets", (torch.int32,), 1)
-    R, C = x.shape
+    C = x.shape[1]
+    if gather is not None:
+        _check(gather, "gather", (torch.int32,), 1)
+        R = gather.numel()
+    else:
+        R = x.shape[0]
     E = offsets.numel() - 1
     ld = int(_C.lib().smoe_quant_cols_ld(R, E))
     xTq = torch.empty((C, ld), dtype=FP8, device=x.device)
     xTs = torch.empty((C, ld // GROUP), dtype=torch.float32, device=x.device)
     pad = torch.empty(E + 1, dtype=torch.int32, device=x.device)
-    _C.call("smoe_quant_cols_128x1", _ptr(x), R, C, _ptr(offsets), E, ld, _ptr(xTq), _ptr(xTs),
-            _ptr(pad), _stream())
+    _C.call("smoe_quant_cols_128x1", _ptr(x), _ptr(gather), gather_div, R, C, _ptr(offsets), E,
+            ld, _ptr(xTq), _ptr(xTs), _ptr(pad), _stream())
     return xTq, xTs, pad, ld
 
 

@@ -86,6 +86,21 @@ def test_quant_cols_bit_exact(dev, counts, C):
     assert np.array_equal(s.cpu().numpy()[:, :Rp // 128], rs)
 
 
+def test_quant_cols_gather_bit_exact(dev):
+    say("quant_cols gather")
+    rng = np.random.default_rng(3)
+    T, K, C = 300, 3, 768
+    x = W.tokens(T, C, seed=9)
+    idx = rng.integers(0, 5, (T, K)).astype(np.int32)
+    row_map, _, counts, off = O.route_sort(idx, 5)
+    q, s, pad, ld = ops.quant_cols(x.to(dev), torch.from_numpy(off).to(dev),
+                                   gather=torch.from_numpy(row_map).to(dev), gather_div=K)
+    rq, rs, rpad = O.quant_cols_128x1(O.bf16_to_f32(u16(x))[row_map // K], off)
+    Rp = int(rpad[-1])
+    assert np.array_equal(u8(q)[:, :Rp], rq)
+    assert np.array_equal(s.cpu().numpy()[:, :Rp // 128], rs)
+
+
 @pytest.mark.parametrize("counts,N,K", [([3, 0, 200, 129], 256, 384), ([1024] * 4, 768, 2048),
                                         ([0, 0], 128, 128), ([5000, 17], 2048, 768)])
 def test_wgrad_gemm(dev, counts, N, K):
@@ -205,9 +220,8 @@ def test_layer_backward_stagewise(dev, T, H, I, E, K):
     w1tq, w1ts = ops.transpose_blockwise(w1q, w1s)
     dxs = ops.grouped_gemm_fp8(*ops.quant_rows(dc1), w1tq, w1ts, off)
     close(f(u16(dxs)), f(r["dxs"]), "dxs", bf16_out=True)
-    xs = x.to(dev).index_select(0, (st["row_map"] // K).long())
     cq, cs, _, _ = ops.quant_cols(dc1, off)
-    xq, xs_s, _, _ = ops.quant_cols(xs, off)
+    xq, xs_s, _, _ = ops.quant_cols(x.to(dev), off, gather=st["row_map"], gather_div=K)
     close(ops.grouped_gemm_fp8_wgrad(cq, cs, xq, xs_s, pad, ld).cpu().numpy(), r["dW1"], "dW1")
     dx = ops.unpermute_combine(bf(r["dxs"], dev), inv, torch.ones_like(st["topk_w"]))
     assert np.array_equal(u16(dx), r["dx"])
