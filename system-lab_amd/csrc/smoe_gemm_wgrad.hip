@@ -8,9 +8,9 @@
 // (e.g. activations), both with the reduction index r contiguous.  Output is
 // fp32 [E, N, K]; experts without rows get zeros.
 //
-// A workgroup of 4 waves owns a 128 (n) x 128 (k) tile of one expert; wave w
-// owns 64 x 64, i.e. 4 x 4 blocks of v_mfma_f32_16x16x128_f8f6f4, one MFMA
-// per 128-row group.  aT rows feed the MFMA's A operand and bT rows its B
+// A workgroup of 8 waves owns a 256 (n) x 256 (k) tile of one expert; each
+// wave owns 64 n x 128 k, i.e. 4 x 8 blocks of v_mfma_f32_16x16x128_f8f6f4,
+// one MFMA per 128-row group.  aT rows feed the MFMA's A operand and bT rows its B
 // operand, so an output lane holds one k (lane % 16) and four consecutive n.
 // Both scales vary per row and group, so each partial is multiplied by
 // sa[n,g]*sb[k,g] before accumulation.  Operands and both scale vectors of a
@@ -20,28 +20,31 @@
 
 namespace smoe {
 
-constexpr int kWT = 128;                    // tile edge (n and k)
-constexpr int kWThreads = 256;
-constexpr int kWA = kWT * kRow;             // 16 KiB of aT
-constexpr int kWB = kWT * kRow;             // 16 KiB of bT
-constexpr int kWStage = kWA + kWB + 2 * kWT * 4;
+// Tile: 256 (n, aT rows) x 256 (k, bT rows) per workgroup of 8 waves in a
+// 2 (k) x 4 (n) grid; each wave owns 128 k x 64 n = 8 x 4 blocks of the
+// 16x16 MFMA.  Stage = aT tile | bT tile | aT scales | bT scales.
+constexpr int kWN = 256, kWK = 256;
+constexpr int kWThreads = 512;
+constexpr int kWA = kWN * kRow;  // 32 KiB of aT
+constexpr int kWB = kWK * kRow;  // 32 KiB of bT
+constexpr int kWStage = kWA + kWB + (kWN + kWK) * 4;
 
-__global__ __launch_bounds__(kWThreads, 2) void grouped_gemm_fp8_wgrad_kernel(
+__global__ __launch_bounds__(kWThreads, 1) void grouped_gemm_fp8_wgrad_kernel(
     const uint8_t* __restrict__ aT, const float* __restrict__ aTs, const uint8_t* __restrict__ bT,
     const float* __restrict__ bTs, const int32_t* __restrict__ pad, int N, int Kd, int ld,
     float* __restrict__ dW) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * kWStage];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int e = blockIdx.z;
-  const int n0 = blockIdx.y * kWT, k0 = blockIdx.x * kWT;
+  const int n0 = blockIdx.y * kWN, k0 = blockIdx.x * kWK;
   const int g0 = pad[e], g1 = pad[e + 1];
   const int steps = (g1 - g0) / kGroup;
-  const int nrows = min(kWT, N - n0), krows = min(kWT, Kd - k0);
-  const int lds_ld = ld / kGroup;  // scale row length
+  const int nrows = min(kWN, N - n0), krows = min(kWK, Kd - k0);
+  const int sld = ld / kGroup;  // scale row length
 
-  // DMA: wave w fills aT segments w*4..w*4+3 and bT segments w*4..w*4+3
-  // (8 rows of 128 bytes each); waves 0/1 load the 128 aT scales, 2/3 the bT
-  // scales, 64 rows each.
+  // DMA per wave and stage: aT segments w*4..w*4+3, bT segments w*4..w*4+3
+  // (8 rows of 128 bytes each); waves 0-3 load 64 aT scales each, waves 4-7
+  // 64 bT scales each.
   uint32_t oa[4], ob[4];
   const int slot = lane & 7;
 #pragma unroll
@@ -50,9 +53,8 @@ __global__ __launch_bounds__(kWThreads, 2) void grouped_gemm_fp8_wgrad_kernel(
     oa[j] = (uint32_t)(min(row, nrows - 1) * ld + ((slot ^ (row & 7)) << 4));
     ob[j] = (uint32_t)(min(row, krows - 1) * ld + ((slot ^ (row & 7)) << 4));
   }
-  const int srow = (wid & 1) * 64 + lane;
-  const uint32_t os =
-      (uint32_t)(min(srow, (wid < 2 ? nrows : krows) - 1) * lds_ld) * 4u;
+  const int srow = (wid & 3) * 64 + lane;
+  const uint32_t os = (uint32_t)(min(srow, (wid < 4 ? nrows : krows) - 1) * sld) * 4u;
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_ptr_t)smem;
   auto issue = [&](int st_idx, int buf) {
     const uint32_t st = lds0 + buf * kWStage;
@@ -65,17 +67,18 @@ __global__ __launch_bounds__(kWThreads, 2) void grouped_gemm_fp8_wgrad_kernel(
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       dma16(bb, ob[j], __builtin_amdgcn_readfirstlane(st + kWA + (wid * 4 + j) * 1024));
-    const float* sbase = wid < 2 ? aTs + (size_t)n0 * lds_ld : bTs + (size_t)k0 * lds_ld;
+    const float* sbase = wid < 4 ? aTs + (size_t)n0 * sld : bTs + (size_t)k0 * sld;
     dma4(uniform_ptr(sbase + r0 / kGroup), os,
-         __builtin_amdgcn_readfirstlane(st + kWA + kWB + (wid >> 1) * kWT * 4 + (wid & 1) * 256));
+         __builtin_amdgcn_readfirstlane(st + kWA + kWB + (wid < 4 ? 0 : kWN * 4) +
+                                        (wid & 3) * 256));
   };
 
-  const int wk = wid >> 1, wn = wid & 1;  // wave's k half and n half
+  const int wk = wid >> 2, wn = wid & 3;  // wave's k half and n quarter
   const int frow = lane & 15;
   const int fch = (lane >> 4) * 2;
-  v4f acc[4][4];
+  v4f acc[8][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 8; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 
@@ -91,7 +94,7 @@ __global__ __launch_bounds__(kWThreads, 2) void grouped_gemm_fp8_wgrad_kernel(
     const uint8_t* sA = smem + buf * kWStage;
     const uint8_t* sB = sA + kWA;
     const float* sSa = (const float*)(sB + kWB);
-    const float* sSb = sSa + kWT;
+    const float* sSb = sSa + kWN;
     v8i fa[4];
     v4f sa[4];
 #pragma unroll
@@ -100,8 +103,8 @@ __global__ __launch_bounds__(kWThreads, 2) void grouped_gemm_fp8_wgrad_kernel(
       sa[j] = *(const v4f*)(sSa + wn * 64 + j * 16 + (lane >> 4) * 4);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int kr = wk * 64 + i * 16 + frow;
+    for (int i = 0; i < 8; ++i) {
+      const int kr = wk * 128 + i * 16 + frow;
       const v8i fb = lds_frag(sB, kr, fch);
       const float sb = sSb[kr];
 #pragma unroll
@@ -119,8 +122,8 @@ __global__ __launch_bounds__(kWThreads, 2) void grouped_gemm_fp8_wgrad_kernel(
 
   // lane holds k = (lane%16) of each 16-row block i, n = (lane/16)*4 + v
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int kl = wk * 64 + i * 16 + frow;
+  for (int i = 0; i < 8; ++i) {
+    const int kl = wk * 128 + i * 16 + frow;
     if (kl >= krows) continue;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -144,13 +147,14 @@ extern "C" int smoe_grouped_gemm_fp8_wgrad(const uint8_t* aT, const float* aTs,
   if (N <= 0 || Kdim <= 0 || ld <= 0) return SMOE_EINVAL_DIM;
   if (E <= 0 || E > SMOE_MAX_EXPERTS) return SMOE_EINVAL_EXPERTS;
   if (N % kGroup || Kdim % kGroup || ld % kGroup) return SMOE_EINVAL_ALIGN128;
-  if ((long long)kWT * ld >= (1LL << 31)) return SMOE_EINVAL_DIM;
+  if ((long long)kWN * ld >= (1LL << 31)) return SMOE_EINVAL_DIM;
   SMOE_CHECK_PTR(aT);
   SMOE_CHECK_PTR(bT);
   SMOE_CHECK_PTR(dW);
   if (!aTs || !bTs || !pad) return SMOE_EINVAL_NULL;
   if (((uintptr_t)aTs | (uintptr_t)bTs | (uintptr_t)pad) & 3u) return SMOE_EINVAL_PTRALIGN;
-  grouped_gemm_fp8_wgrad_kernel<<<dim3(Kdim / kWT, N / kWT, E), dim3(kWThreads), 0,
+  grouped_gemm_fp8_wgrad_kernel<<<dim3((Kdim + kWK - 1) / kWK, (N + kWN - 1) / kWN, E),
+                                  dim3(kWThreads), 0,
                                   (hipStream_t)stream>>>(aT, aTs, bT, bTs, pad, N, Kdim, ld, dW);
   SMOE_RETURN_LAUNCH();
 }
