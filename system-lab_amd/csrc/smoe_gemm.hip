@@ -220,17 +220,22 @@ __global__ __launch_bounds__(C::kThreads, 1) void grouped_gemm_fp8_kernel(
     v8i fw[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) fw[j] = lds_frag(sB, wn * 64 + j * 16 + frow, fch);
+    // the next row block's activation fragment is read before this block's
+    // MFMAs are issued, so its LDS latency hides behind them
+    const int rbase = wr * kRB * 16 + frow;
+    v8i fx = lds_frag(sA, rbase, fch);
 #pragma unroll
     for (int i = 0; i < kRB; ++i) {
-      const int r = wr * kRB * 16 + i * 16 + frow;
-      const v8i fx = lds_frag(sA, r, fch);
-      const float sc = sS[r] * sb;
+      v8i fxn = fx;
+      if (i + 1 < kRB) fxn = lds_frag(sA, rbase + (i + 1) * 16, fch);
+      const float sc = sS[rbase + i * 16] * sb;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const v4f p = mfma16(fw[j], fx, v4f{0.0f, 0.0f, 0.0f, 0.0f});
 #pragma unroll
         for (int v = 0; v < 4; ++v) acc[i][j][v] = __builtin_fmaf(p[v], sc, acc[i][j][v]);
       }
+      fx = fxn;
     }
     // stage kb+1 must have landed for every wave; later stages may still fly
     if (kStages > 2 && kb + kStages - 1 < ksb) {
