@@ -66,7 +66,9 @@ __global__ __launch_bounds__(C::kThreads, 1) void grouped_gemm_fp8_kernel(
   constexpr int kThreads = C::kThreads, kBM = C::kBM, kBN = C::kBN, kStage = C::kStage;
   constexpr int kStages = C::kStages, kABytes = C::kABytes, kBBytes = C::kBBytes;
   constexpr int kASegs = C::kASegs, kBSegs = C::kBSegs, kRB = C::kRB;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[kStages * kStage];
+  constexpr int kCPitch = kBN * 2 + 16;  // bytes per staged output row (+16: banks)
+  constexpr int kSmem = kStages * kStage > kBM * kCPitch ? kStages * kStage : kBM * kCPitch;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kSmem];
   __shared__ int mstart[SMOE_MAX_EXPERTS + 1];
   __shared__ int wsum[kThreads / kWave];
 
@@ -249,21 +251,30 @@ __global__ __launch_bounds__(C::kThreads, 1) void grouped_gemm_fp8_kernel(
     buf = (buf + 1 == kStages) ? 0 : buf + 1;
   }
 
-  // ---- epilogue: lane holds row (lane%16); v -> col (lane/16)*4 + v ------
+  // ---- epilogue: the bf16 tile is staged in LDS (the stage buffers are free
+  // now; the last barrier of the K loop ordered every fragment read before) and written out row by row with 16-byte stores, so each output row
+  // segment of kBN columns leaves as whole 128-byte lines.
+  uint8_t* ct = smem;
 #pragma unroll
   for (int i = 0; i < kRB; ++i) {
     const int rl = wr * kRB * 16 + i * 16 + frow;
-    if (rl >= rows) continue;
     const int cl = wn * 64 + (lane >> 4) * 4;
-    uint16_t* crow = c + (size_t)(row0 + rl) * N + n0 + cl;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      if (cl + j * 16 >= ncols) continue;
       uint2 o;
       o.x = f32_to_bf16(acc[i][j][0]) | (f32_to_bf16(acc[i][j][1]) << 16);
       o.y = f32_to_bf16(acc[i][j][2]) | (f32_to_bf16(acc[i][j][3]) << 16);
-      *(uint2*)(crow + j * 16) = o;
+      *(uint2*)(ct + rl * kCPitch + (cl + j * 16) * 2) = o;
     }
+  }
+  __syncthreads();
+  constexpr int kChunks = kBN * 2 / 16;  // 16-byte chunks per row
+  const int nchunks = ncols * 2 / 16;
+  for (int idx = tid; idx < rows * kChunks; idx += kThreads) {
+    const int r = idx / kChunks, ch = idx - r * kChunks;
+    if (ch < nchunks)
+      *(uint4*)((uint8_t*)(c + (size_t)(row0 + r) * N + n0) + ch * 16) =
+          *(const uint4*)(ct + r * kCPitch + ch * 16);
   }
 }
 
