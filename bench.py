@@ -108,12 +108,19 @@ def bench_gemm(dev, steps, warmup):
     f2 = lambda: ops.grouped_gemm_fp8(hq, hs, w2q, w2s, off, out=y)
     t1 = timed(f1, steps, warmup)
     t2 = timed(f2, steps, warmup)
+    # fc1 with SwiGLU + requant fused into the epilogue (the inference path),
+    # against fc1 followed by the stand-alone SwiGLU kernel
+    fsw = lambda: ops.swiglu_quant(c1)
+    t_sw = timed(fsw, steps, warmup)
+    f1s = lambda: ops.grouped_gemm_fp8_swiglu(xq, xs, w1q, w1s, off)
+    t1s = timed(f1s, steps, warmup)
     fl1 = 2.0 * R * (2 * c.I) * c.H
     fl2 = 2.0 * R * c.H * c.I
     tf = (fl1 + fl2) / ((t1 + t2) * 1e-3) / 1e12
     out = {"workload": "dsv3 local experts R=65536 H=7168 I=2048 E=32 zipf1.2",
            "fc1_ms": round(t1, 4), "fc1_tflops": round(fl1 / (t1 * 1e-3) / 1e12, 1),
            "fc2_ms": round(t2, 4), "fc2_tflops": round(fl2 / (t2 * 1e-3) / 1e12, 1),
+           "fc1_swiglu_fused_ms": round(t1s, 4), "fc1_then_swiglu_ms": round(t1 + t_sw, 4),
            "tflops": round(tf, 1), "roofline_frac": round(tf / FP8_PEAK_TFLOPS, 4),
            "peak_tflops": FP8_PEAK_TFLOPS}
     del xq, xs, hq, hs, w1q, w1s, w2q, w2s, c1, y

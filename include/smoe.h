@@ -132,6 +132,22 @@ int smoe_grouped_gemm_fp8(const uint8_t* a, const float* as, const uint8_t* b,
                           int Kdim, uint16_t* c, void* ws, size_t ws_bytes, void* stream);
 
 /*
+ * fc1 grouped GEMM with the SwiGLU + 1x128 requantisation fused into its
+ * epilogue: the result equals smoe_grouped_gemm_fp8(a, as, w1, w1s) -> c1
+ * [R,2I] bf16 followed by smoe_swiglu_quant(c1) -> hq [R,I] u8, hs [R,I/128]
+ * f32, byte for byte, without the c1 round trip through HBM.  w1 [E,2I,Kdim]
+ * u8 holds gate rows [0,I) and up rows [I,2I); w1s [E,2I/128,Kdim/128].  c1
+ * may be NULL; when given it also receives the bf16 fc1 output (the backward
+ * pass needs it).  Requires I % 128 == 0 and 2*I*Kdim < 2^31.
+ * Replaces the grouped GEMM + activation_func_with_probs pair of the expert
+ * FFN (moe/MoE_detailed_computation_dataflow.md:168-174;
+ * notes/2026-04/2026-04-21_gptoss_10_moe_fp8_grouped_gemm_diagnosis.md:39-46).
+ */
+int smoe_grouped_gemm_fp8_swiglu(const uint8_t* a, const float* as, const uint8_t* w1,
+                                 const float* w1s, const int32_t* offsets, int E, int R, int I,
+                                 int Kdim, uint8_t* hq, float* hs, uint16_t* c1, void* stream);
+
+/*
  * SwiGLU + 1x128 requantisation.  c1 [R,2I] bf16 with gate columns [0,I) and
  * up columns [I,2I): h = silu(g)*u in fp32 -> hq [R,I] u8, hs [R,I/128] f32.
  * silu(g) = g / (1 + exp(-g)) with exp evaluated by the library's own

@@ -110,6 +110,42 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// ------------------------------------------- 1x128 group quantisation ----
+struct Q16 {
+  uint4 q;      // 16 fp8 bytes
+  float scale;  // group scale (identical in the 8 lanes of a group)
+};
+
+// Quantise 16 fp32 values owned by this lane whose group spans 8 lanes.
+__device__ __forceinline__ Q16 quant16(const float (&f)[16]) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(f[i]));
+  amax = group_max<8>(amax);
+  const float s = group_scale(amax);
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    w[i] = quant_one(f[4 * i], s) | (quant_one(f[4 * i + 1], s) << 8) |
+           (quant_one(f[4 * i + 2], s) << 16) |
+           (quant_one(f[4 * i + 3], s) << 24);
+  }
+  Q16 r;
+  r.q = make_uint4(w[0], w[1], w[2], w[3]);
+  r.scale = s;
+  return r;
+}
+
+__device__ __forceinline__ void unpack_bf16x8(const uint4& v, float* f) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __uint_as_float(w[i] << 16);
+    f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+
+// ---------------------------------------------------------- permute_quant
 }  // namespace smoe
 
 // ------------------------------------------------------ host validation ----

@@ -58,11 +58,20 @@ struct Cfg {
   static_assert(kStages * kStage + 4200 <= 160 * 1024, "LDS budget");
 };
 
-template <class C>
+// kSwiGLU: the fc1 GEMM with SwiGLU + 1x128 requantisation fused into the
+// epilogue.  b is W1 [E, N = 2I, K] (gate rows [0, I), up rows [I, 2I)); tile
+// nt pairs gate columns nt*128 .. +128 with up columns I + nt*128 .. +128, so
+// each tile row holds exactly one 128-wide group of h = silu(g)*u.  Outputs
+// are hq [R, I] fp8 and hs [R, I/128]; c (c1 [R, 2I] bf16) is written only
+// when not null.  h is computed from the bf16-rounded fc1 values exactly as
+// the stand-alone SwiGLU kernel does, so the fused path is bit-identical to
+// GEMM -> bf16 c1 -> swiglu_quant.
+template <class C, bool kSwiGLU>
 __global__ __launch_bounds__(C::kThreads, 1) void grouped_gemm_fp8_kernel(
     const uint8_t* __restrict__ a, const float* __restrict__ as, const uint8_t* __restrict__ b,
     const float* __restrict__ bs, const int32_t* __restrict__ offsets, int E, int N, int Kd,
-    int mt_bound, uint16_t* __restrict__ c) {
+    int mt_bound, uint16_t* __restrict__ c, uint8_t* __restrict__ hq, float* __restrict__ hs) {
+  static_assert(!kSwiGLU || C::kBN == 256, "fused SwiGLU pairs 128 gate with 128 up columns");
   constexpr int kThreads = C::kThreads, kBM = C::kBM, kBN = C::kBN, kStage = C::kStage;
   constexpr int kStages = C::kStages, kABytes = C::kABytes, kBBytes = C::kBBytes;
   constexpr int kASegs = C::kASegs, kBSegs = C::kBSegs, kRB = C::kRB;
@@ -109,7 +118,8 @@ __global__ __launch_bounds__(C::kThreads, 1) void grouped_gemm_fp8_kernel(
   const int nblk = gridDim.x;  // multiple of 8
   const int bid = blockIdx.x;
   const int lin = (bid & 7) * (nblk >> 3) + (bid >> 3);
-  const int NT = (N + kBN - 1) / kBN;
+  const int I = N / 2;
+  const int NT = kSwiGLU ? I / kGroup : (N + kBN - 1) / kBN;
   const int grp = lin / (kGroupM * NT);
   const int in_g = lin - grp * kGroupM * NT;
   const int mt = grp * kGroupM + (in_g % kGroupM);
@@ -136,9 +146,14 @@ __global__ __launch_bounds__(C::kThreads, 1) void grouped_gemm_fp8_kernel(
   // 32-bit byte offsets from wave-uniform (SGPR) base pointers; rows past the
   // expert's end (A) or past N (B) are clamped to the last valid row.
   const uint8_t* a_base = a + (size_t)row0 * Kd;
-  const uint8_t* b_base = b + ((size_t)e * N + n0) * Kd;
+  const uint8_t* b_base = b + ((size_t)e * N + (kSwiGLU ? 0 : n0)) * Kd;
   const float* s_base = as + (size_t)row0 * ksb;
-  const int ncols = min(kBN, N - n0);
+  const int ncols = kSwiGLU ? kBN : min(kBN, N - n0);
+  // weight row of tile column row (fused: gate half, then up half)
+  auto wrow = [&](int row) {
+    if constexpr (kSwiGLU) return row < kGroup ? nt * kGroup + row : I + nt * kGroup + row - kGroup;
+    else return min(row, ncols - 1);
+  };
   uint32_t oa[kASegs], ob[kBSegs];
   {
     const int slot = lane & 7;
@@ -150,7 +165,7 @@ __global__ __launch_bounds__(C::kThreads, 1) void grouped_gemm_fp8_kernel(
 #pragma unroll
     for (int j = 0; j < kBSegs; ++j) {
       const int row = (wid * kBSegs + j) * 8 + (lane >> 3);
-      ob[j] = (uint32_t)(min(row, ncols - 1) * Kd + ((slot ^ (row & 7)) << 4));
+      ob[j] = (uint32_t)(wrow(row) * Kd + ((slot ^ (row & 7)) << 4));
     }
   }
   const uint32_t os = (uint32_t)(min((wid % C::kSWaves) * 64 + lane, rows - 1) * ksb) * 4u;
@@ -164,7 +179,7 @@ __global__ __launch_bounds__(C::kThreads, 1) void grouped_gemm_fp8_kernel(
   __syncthreads();
   for (int i = tid; i < kNB128 * ksb; i += kThreads) {
     const int nb = i / ksb, kb = i - nb * ksb;
-    const int blk = min(n0 / kGroup + nb, N / kGroup - 1);
+    const int blk = kSwiGLU ? (nb == 0 ? nt : I / kGroup + nt) : min(n0 / kGroup + nb, N / kGroup - 1);
     sbt[i] = bs[((size_t)e * (N / kGroup) + blk) * ksb + kb];
   }
   __syncthreads();
@@ -252,8 +267,9 @@ __global__ __launch_bounds__(C::kThreads, 1) void grouped_gemm_fp8_kernel(
   }
 
   // ---- epilogue: the bf16 tile is staged in LDS (the stage buffers are free
-  // now; the last barrier of the K loop ordered every fragment read before) and written out row by row with 16-byte stores, so each output row
-  // segment of kBN columns leaves as whole 128-byte lines.
+  // now: the K loop's last barrier ordered every fragment read before) and
+  // written out row by row with 16-byte stores, so each output row segment of
+  // kBN columns leaves as whole 128-byte lines.
   uint8_t* ct = smem;
 #pragma unroll
   for (int i = 0; i < kRB; ++i) {
@@ -268,13 +284,40 @@ __global__ __launch_bounds__(C::kThreads, 1) void grouped_gemm_fp8_kernel(
     }
   }
   __syncthreads();
-  constexpr int kChunks = kBN * 2 / 16;  // 16-byte chunks per row
-  const int nchunks = ncols * 2 / 16;
-  for (int idx = tid; idx < rows * kChunks; idx += kThreads) {
-    const int r = idx / kChunks, ch = idx - r * kChunks;
-    if (ch < nchunks)
-      *(uint4*)((uint8_t*)(c + (size_t)(row0 + r) * N + n0) + ch * 16) =
-          *(const uint4*)(ct + r * kCPitch + ch * 16);
+  if constexpr (kSwiGLU) {
+    // 8 lanes per row, 16 columns each: h = silu(g) * u from the staged bf16
+    // values, amax over the 8 lanes, 16 fp8 bytes per lane.
+    for (int idx = tid; idx < rows * 8; idx += kThreads) {
+      const int r = idx >> 3, sub = idx & 7;
+      const uint8_t* rowp = ct + r * kCPitch;
+      float fg[16], fu[16], h[16];
+      unpack_bf16x8(*(const uint4*)(rowp + sub * 32), fg);
+      unpack_bf16x8(*(const uint4*)(rowp + sub * 32 + 16), fg + 8);
+      unpack_bf16x8(*(const uint4*)(rowp + 256 + sub * 32), fu);
+      unpack_bf16x8(*(const uint4*)(rowp + 256 + sub * 32 + 16), fu + 8);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) h[i] = silu32(fg[i]) * fu[i];
+      const Q16 q = quant16(h);
+      const size_t gr = (size_t)(row0 + r);
+      *(uint4*)(hq + gr * I + nt * kGroup + sub * 16) = q.q;
+      if (sub == 0) hs[gr * (I / kGroup) + nt] = q.scale;
+      if (c) {
+        uint16_t* crow = c + gr * N + nt * kGroup + sub * 16;
+        *(uint4*)crow = *(const uint4*)(rowp + sub * 32);
+        *(uint4*)(crow + 8) = *(const uint4*)(rowp + sub * 32 + 16);
+        *(uint4*)(crow + I) = *(const uint4*)(rowp + 256 + sub * 32);
+        *(uint4*)(crow + I + 8) = *(const uint4*)(rowp + 256 + sub * 32 + 16);
+      }
+    }
+  } else {
+    constexpr int kChunks = kBN * 2 / 16;  // 16-byte chunks per row
+    const int nchunks = ncols * 2 / 16;
+    for (int idx = tid; idx < rows * kChunks; idx += kThreads) {
+      const int r = idx / kChunks, ch = idx - r * kChunks;
+      if (ch < nchunks)
+        *(uint4*)((uint8_t*)(c + (size_t)(row0 + r) * N + n0) + ch * 16) =
+            *(const uint4*)(ct + r * kCPitch + ch * 16);
+    }
   }
 }
 
@@ -314,7 +357,39 @@ extern "C" int smoe_grouped_gemm_fp8(const uint8_t* a, const float* as, const ui
   long long nblk = mt_pad * NT;
   nblk = (nblk + 7) / 8 * 8;
   if (nblk > 0x7fffffffLL) return SMOE_EINVAL_DIM;
-  grouped_gemm_fp8_kernel<C><<<dim3((unsigned)nblk), dim3(C::kThreads), 0, (hipStream_t)stream>>>(
-      a, as, b, bs, offsets, E, N, Kdim, (int)mt_bound, c);
+  grouped_gemm_fp8_kernel<C, false>
+      <<<dim3((unsigned)nblk), dim3(C::kThreads), 0, (hipStream_t)stream>>>(
+          a, as, b, bs, offsets, E, N, Kdim, (int)mt_bound, c, nullptr, nullptr);
+  SMOE_RETURN_LAUNCH();
+}
+
+extern "C" int smoe_grouped_gemm_fp8_swiglu(const uint8_t* a, const float* as, const uint8_t* w1,
+                                            const float* w1s, const int32_t* offsets, int E,
+                                            int R, int I, int Kdim, uint8_t* hq, float* hs,
+                                            uint16_t* c1, void* stream) {
+  if (R <= 0 || I <= 0 || Kdim <= 0) return SMOE_EINVAL_DIM;
+  if (E <= 0 || E > SMOE_MAX_EXPERTS) return SMOE_EINVAL_EXPERTS;
+  if (I % kGroup || Kdim % kGroup) return SMOE_EINVAL_ALIGN128;
+  if (Kdim > 65536) return SMOE_EINVAL_DIM;
+  // weight-row offsets are 32-bit from the expert's base
+  if (2LL * I * Kdim >= (1LL << 31)) return SMOE_EINVAL_DIM;
+  SMOE_CHECK_PTR(a);
+  SMOE_CHECK_PTR(w1);
+  SMOE_CHECK_PTR(hq);
+  if (c1 && ((uintptr_t)c1 & 15u)) return SMOE_EINVAL_PTRALIGN;
+  if (!as || !w1s || !offsets || !hs) return SMOE_EINVAL_NULL;
+  if (((uintptr_t)as | (uintptr_t)w1s | (uintptr_t)offsets | (uintptr_t)hs) & 3u)
+    return SMOE_EINVAL_PTRALIGN;
+  using C = GemmCfg;
+  const int N = 2 * I;
+  const long long mt_bound = (R + C::kBM - 1) / C::kBM + E;
+  const long long NT = I / kGroup;
+  const long long mt_pad = (mt_bound + kGroupM - 1) / kGroupM * kGroupM;
+  long long nblk = mt_pad * NT;
+  nblk = (nblk + 7) / 8 * 8;
+  if (nblk > 0x7fffffffLL) return SMOE_EINVAL_DIM;
+  grouped_gemm_fp8_kernel<C, true>
+      <<<dim3((unsigned)nblk), dim3(C::kThreads), 0, (hipStream_t)stream>>>(
+          a, as, w1, w1s, offsets, E, N, Kdim, (int)mt_bound, c1, hq, hs);
   SMOE_RETURN_LAUNCH();
 }

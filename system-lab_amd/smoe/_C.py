@@ -30,6 +30,8 @@ SIGNATURES = {
     "smoe_grouped_gemm_fp8_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int]),
     "smoe_grouped_gemm_fp8": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int, P, P,
                                       c_size_t, P]),
+    "smoe_grouped_gemm_fp8_swiglu": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int, P, P,
+                                             P, P]),
     "smoe_swiglu_quant": (c_int, [P, c_int, c_int, P, P, P]),
     "smoe_swiglu_quant_h": (c_int, [P, c_int, c_int, P, P, P, P]),
     "smoe_unpermute_combine": (c_int, [P, P, P, c_int, c_int, c_int, P, P]),

@@ -65,12 +65,14 @@ class SimpleMoE(nn.Module):
         w1q, w1s, w2q, w2s = self.fp8_weights()
         idx, w = ops.router_topk(logits.contiguous(), self.top_k, self.router_bias)
         xq, xs, row_map, inv_map, counts, offsets = ops.permute_quant(x, idx, self.num_experts)
-        c1 = ops.grouped_gemm_fp8(xq, xs, w1q, w1s, offsets)
         if return_intermediates:
+            # the backward pass needs c1 and bf16 h, so fc1 and SwiGLU run
+            # as two kernels here
+            c1 = ops.grouped_gemm_fp8(xq, xs, w1q, w1s, offsets)
             hq, hs, h = ops.swiglu_quant(c1, save_h=True)
         else:
-            hq, hs = ops.swiglu_quant(c1)
-            h = None
+            # inference: SwiGLU + requantisation run in the fc1 epilogue
+            hq, hs = ops.grouped_gemm_fp8_swiglu(xq, xs, w1q, w1s, offsets)
         y = ops.grouped_gemm_fp8(hq, hs, w2q, w2s, offsets)
         out = ops.unpermute_combine(y, inv_map, w)
         if return_intermediates:

@@ -170,6 +170,36 @@ def grouped_gemm_fp8(xq: torch.Tensor, xs: torch.Tensor, wq: torch.Tensor, ws: t
     return out
 
 
+def grouped_gemm_fp8_swiglu(xq: torch.Tensor, xs: torch.Tensor, w1q: torch.Tensor,
+                            w1s: torch.Tensor, offsets: torch.Tensor, save_c1: bool = False):
+    """fc1 GEMM with SwiGLU + 1x128 requantisation fused into the epilogue.
+    Same bytes as ``swiglu_quant(grouped_gemm_fp8(xq, xs, w1q, w1s, offsets))``;
+    returns (hq [R,I] fp8, hs [R,I/128] f32), plus c1 [R,2I] bf16 when
+    ``save_c1``.  Rows outside [offsets[0], offsets[E]) are not written."""
+    for t, n in ((xq, "xq"), (w1q, "w1q")):
+        _check(t, n, (FP8, torch.uint8))
+    _check(xs, "xs", (torch.float32,), 2)
+    _check(w1s, "w1s", (torch.float32,), 3)
+    _check(offsets, "offsets", (torch.int32,), 1)
+    R, Kd = xq.shape
+    E, N, Kw = w1q.shape
+    if Kw != Kd:
+        raise ValueError(f"K mismatch: xq has {Kd}, w1q has {Kw}")
+    if N % (2 * GROUP):
+        raise ValueError("w1q rows must be gate | up halves of a multiple of 128 each")
+    if offsets.numel() != E + 1:
+        raise ValueError("offsets must have E+1 entries")
+    if xs.shape != (R, Kd // GROUP) or w1s.shape != (E, N // GROUP, Kd // GROUP):
+        raise ValueError("scale shapes do not match the operands")
+    I = N // 2
+    hq = torch.empty((R, I), dtype=FP8, device=xq.device)
+    hs = torch.empty((R, I // GROUP), dtype=torch.float32, device=xq.device)
+    c1 = torch.empty((R, N), dtype=torch.bfloat16, device=xq.device) if save_c1 else None
+    _C.call("smoe_grouped_gemm_fp8_swiglu", _ptr(_bytes(xq)), _ptr(xs), _ptr(_bytes(w1q)),
+            _ptr(w1s), _ptr(offsets), E, R, I, Kd, _ptr(hq), _ptr(hs), _ptr(c1), _stream())
+    return (hq, hs, c1) if save_c1 else (hq, hs)
+
+
 # ------------------------------------------------------------------ SwiGLU
 def swiglu_quant(c1: torch.Tensor, save_h: bool = False):
     """h = silu(gate)*up (gate = columns [0,I), up = [I,2I)) requantised 1x128.
