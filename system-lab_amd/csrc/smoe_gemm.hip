@@ -141,10 +141,11 @@ __global__ __launch_bounds__(C::kThreads, 1) void grouped_gemm_fp8_kernel(
   // ---- direct global->LDS loaders ---------------------------------------
   // Wave w fills 1 KiB LDS segments: A segments w*kASegs.., B segments
   // w*kBSegs.. (8 rows each), and (waves below kBM/64) scale rows w*64..+63.
-  // Lane i of a segment writes LDS position i: row = seg*8 + i/8, chunk slot
-  // i%8, which holds global chunk (i%8) ^ (row & 7).  Offsets are per-lane
-  // 32-bit byte offsets from wave-uniform (SGPR) base pointers; rows past the
-  // expert's end (A) or past N (B) are clamped to the last valid row.
+  // Lane i of a segment writes row position p = seg*8 + i/8, chunk slot i%8;
+  // that position holds tile row tile_row(p) and the slot holds its global
+  // chunk (i%8) ^ (row & 7).  Offsets are per-lane 32-bit byte offsets from
+  // wave-uniform (SGPR) base pointers; rows past the expert's end (A) or past
+  // N (B) are clamped to the last valid row.
   const uint8_t* a_base = a + (size_t)row0 * Kd;
   const uint8_t* b_base = b + ((size_t)e * N + (kSwiGLU ? 0 : n0)) * Kd;
   const float* s_base = as + (size_t)row0 * ksb;
@@ -159,12 +160,12 @@ __global__ __launch_bounds__(C::kThreads, 1) void grouped_gemm_fp8_kernel(
     const int slot = lane & 7;
 #pragma unroll
     for (int j = 0; j < kASegs; ++j) {
-      const int row = (wid * kASegs + j) * 8 + (lane >> 3);
+      const int row = tile_row((wid * kASegs + j) * 8 + (lane >> 3));
       oa[j] = (uint32_t)(min(row, rows - 1) * Kd + ((slot ^ (row & 7)) << 4));
     }
 #pragma unroll
     for (int j = 0; j < kBSegs; ++j) {
-      const int row = (wid * kBSegs + j) * 8 + (lane >> 3);
+      const int row = tile_row((wid * kBSegs + j) * 8 + (lane >> 3));
       ob[j] = (uint32_t)(wrow(row) * Kd + ((slot ^ (row & 7)) << 4));
     }
   }
@@ -186,19 +187,27 @@ __global__ __launch_bounds__(C::kThreads, 1) void grouped_gemm_fp8_kernel(
   const float* sb_row = sbt + ((wn * 64) / kGroup) * ksb;
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_ptr_t)smem;
 
+  // Wave-uniform LDS destinations of this wave's DMA segments, computed once
+  // into scalar registers so that issuing a DMA in the K loop costs no
+  // VALU -> SGPR round trip.  DMA q of a stage: q = 0 the activation scales
+  // (waves below kSWaves), then kASegs A segments, then kBSegs B segments.
+  const uint32_t s_lds = __builtin_amdgcn_readfirstlane(lds0 + kABytes + kBBytes + wid * 256);
+  const uint32_t a_lds = __builtin_amdgcn_readfirstlane(lds0 + wid * kASegs * 1024);
+  const uint32_t b_lds = __builtin_amdgcn_readfirstlane(lds0 + kABytes + wid * kBSegs * 1024);
+  constexpr int kDma = 1 + kASegs + kBSegs;
+  auto issue_one = [&](int q, int kb, int buf) {
+    const uint32_t st = buf * kStage;
+    if (q == 0) {
+      if (wid < C::kSWaves) dma4(s_base + kb, os, s_lds + st);
+    } else if (q <= kASegs) {
+      dma16(a_base + (size_t)kb * kBK, oa[q - 1], a_lds + st + (q - 1) * 1024);
+    } else {
+      dma16(b_base + (size_t)kb * kBK, ob[q - 1 - kASegs], b_lds + st + (q - 1 - kASegs) * 1024);
+    }
+  };
   auto issue = [&](int kb, int buf) {
-    const uint32_t st = lds0 + buf * kStage;
-    const uint8_t* ab = a_base + (size_t)kb * kBK;
-    const uint8_t* bb = b_base + (size_t)kb * kBK;
 #pragma unroll
-    for (int j = 0; j < kASegs; ++j)
-      dma16(ab, oa[j], __builtin_amdgcn_readfirstlane(st + (wid * kASegs + j) * 1024));
-#pragma unroll
-    for (int j = 0; j < kBSegs; ++j)
-      dma16(bb, ob[j],
-            __builtin_amdgcn_readfirstlane(st + kABytes + (wid * kBSegs + j) * 1024));
-    if (wid < C::kSWaves)
-      dma4(s_base + kb, os, __builtin_amdgcn_readfirstlane(st + kABytes + kBBytes + wid * 256));
+    for (int q = 0; q < kDma; ++q) issue_one(q, kb, buf);
   };
   // loads one stage leaves outstanding per wave (waves 0-3 also load scales)
   const bool scale_wave = wid < C::kSWaves;

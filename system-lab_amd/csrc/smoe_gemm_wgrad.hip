@@ -49,28 +49,29 @@ __global__ __launch_bounds__(kWThreads, 1) void grouped_gemm_fp8_wgrad_kernel(
   const int slot = lane & 7;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int row = (wid * 4 + j) * 8 + (lane >> 3);
+    const int row = tile_row((wid * 4 + j) * 8 + (lane >> 3));
     oa[j] = (uint32_t)(min(row, nrows - 1) * ld + ((slot ^ (row & 7)) << 4));
     ob[j] = (uint32_t)(min(row, krows - 1) * ld + ((slot ^ (row & 7)) << 4));
   }
   const int srow = (wid & 3) * 64 + lane;
   const uint32_t os = (uint32_t)(min(srow, (wid < 4 ? nrows : krows) - 1) * sld) * 4u;
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_ptr_t)smem;
+  // wave-uniform LDS destinations, computed once into scalar registers
+  const uint32_t a_lds = __builtin_amdgcn_readfirstlane(lds0 + wid * 4 * 1024);
+  const uint32_t b_lds = __builtin_amdgcn_readfirstlane(lds0 + kWA + wid * 4 * 1024);
+  const uint32_t s_lds = __builtin_amdgcn_readfirstlane(
+      lds0 + kWA + kWB + (wid < 4 ? 0 : kWN * 4) + (wid & 3) * 256);
+  const float* sbase = uniform_ptr(wid < 4 ? aTs + (size_t)n0 * sld : bTs + (size_t)k0 * sld);
   auto issue = [&](int st_idx, int buf) {
-    const uint32_t st = lds0 + buf * kWStage;
+    const uint32_t st = buf * kWStage;
     const int r0 = g0 + st_idx * kGroup;
     const uint8_t* ab = aT + (size_t)n0 * ld + r0;
     const uint8_t* bb = bT + (size_t)k0 * ld + r0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      dma16(ab, oa[j], __builtin_amdgcn_readfirstlane(st + (wid * 4 + j) * 1024));
+    for (int j = 0; j < 4; ++j) dma16(ab, oa[j], a_lds + st + j * 1024);
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      dma16(bb, ob[j], __builtin_amdgcn_readfirstlane(st + kWA + (wid * 4 + j) * 1024));
-    const float* sbase = wid < 4 ? aTs + (size_t)n0 * sld : bTs + (size_t)k0 * sld;
-    dma4(uniform_ptr(sbase + r0 / kGroup), os,
-         __builtin_amdgcn_readfirstlane(st + kWA + kWB + (wid < 4 ? 0 : kWN * 4) +
-                                        (wid & 3) * 256));
+    for (int j = 0; j < 4; ++j) dma16(bb, ob[j], b_lds + st + j * 1024);
+    dma4(sbase + r0 / kGroup, os, s_lds + st);
   };
 
   const int wk = wid >> 2, wn = wid & 3;  // wave's k half and n quarter

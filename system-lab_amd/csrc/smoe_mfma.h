@@ -50,8 +50,24 @@ __device__ __forceinline__ const T* uniform_ptr(const T* p) {
   return (const T*)(uintptr_t)(((uint64_t)hi << 32) | lo);
 }
 
+// LDS tile layout.  ds_read_b128 serves a wave in 16-lane groups, and within
+// a group lanes 0-7 and lanes 8-15 are each conflict-free only when their
+// eight 16-byte accesses fall in one 128-byte half of the 64-bank array
+// (address bit 7 constant) at eight distinct positions (measured with the
+// LDS bank-conflict counter on gfx950).  A fragment read gives lane l tile
+// row base + l%16, so tile rows r and r+8 of each 16-row group share one
+// 256-byte line: row r sits at row position 2*(r&7) + (r>>3 & 1), which puts
+// rows 0-7 in the low halves and rows 8-15 in the high halves; within a row
+// the 16-byte chunk c is stored at slot c ^ (r & 7).
+__device__ __forceinline__ int lds_row(int r) {
+  return (r & ~15) | ((r & 7) << 1) | ((r >> 3) & 1);
+}
+// Inverse of lds_row: the tile row held at row position p.
+__device__ __forceinline__ int tile_row(int p) {
+  return (p & ~15) | ((p & 1) << 3) | ((p & 15) >> 1);
+}
 __device__ __forceinline__ int swz(int row, int chunk) {
-  return row * kRow + ((chunk ^ (row & 7)) << 4);
+  return lds_row(row) * kRow + ((chunk ^ (row & 7)) << 4);
 }
 
 __device__ __forceinline__ v4f mfma16(v8i a, v8i b, v4f c) {
