@@ -171,20 +171,6 @@ __global__ __launch_bounds__(C::kThreads, 1) void grouped_gemm_fp8_kernel(
   }
   const uint32_t os = (uint32_t)(min((wid % C::kSWaves) * 64 + lane, rows - 1) * ksb) * 4u;
   const int wr = wid / C::kWN, wn = wid % C::kWN;
-  // The tile's weight-block scales (kBN/128 blocks x ksb) move to LDS before
-  // the K loop, into the expert table's space (dead from here on): a
-  // compiler-visible global load inside the loop would make the compiler drain
-  // vmcnt to zero, i.e. wait for every DMA stage in flight.
-  constexpr int kNB128 = kBN / kGroup;
-  float* sbt = (float*)mstart;
-  __syncthreads();
-  for (int i = tid; i < kNB128 * ksb; i += kThreads) {
-    const int nb = i / ksb, kb = i - nb * ksb;
-    const int blk = kSwiGLU ? (nb == 0 ? nt : I / kGroup + nt) : min(n0 / kGroup + nb, N / kGroup - 1);
-    sbt[i] = bs[((size_t)e * (N / kGroup) + blk) * ksb + kb];
-  }
-  __syncthreads();
-  const float* sb_row = sbt + ((wn * 64) / kGroup) * ksb;
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_ptr_t)smem;
 
   // Wave-uniform LDS destinations of this wave's DMA segments, computed once
@@ -225,6 +211,20 @@ __global__ __launch_bounds__(C::kThreads, 1) void grouped_gemm_fp8_kernel(
 #pragma unroll
   for (int s = 0; s < kStages - 1; ++s)
     if (s < ksb) issue(s, s);
+  // While the first stages fly, the tile's weight-block scales (kBN/128
+  // blocks x ksb) move to LDS, into the expert table's space (dead from here
+  // on): a compiler-visible global load inside the K loop would make the
+  // compiler drain vmcnt to zero, i.e. wait for every DMA stage in flight.
+  constexpr int kNB128 = kBN / kGroup;
+  float* sbt = (float*)mstart;
+  __syncthreads();
+  for (int i = tid; i < kNB128 * ksb; i += kThreads) {
+    const int nb = i / ksb, kb = i - nb * ksb;
+    const int blk = kSwiGLU ? (nb == 0 ? nt : I / kGroup + nt) : min(n0 / kGroup + nb, N / kGroup - 1);
+    sbt[i] = bs[((size_t)e * (N / kGroup) + blk) * ksb + kb];
+  }
+  __syncthreads();
+  const float* sb_row = sbt + ((wn * 64) / kGroup) * ksb;
   if (kStages > 2 && ksb > 1) {
     if (scale_wave) wait_vm_lgkm0<kASegs + kBSegs + 1>();
     else wait_vm_lgkm0<kASegs + kBSegs>();
