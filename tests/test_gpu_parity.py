@@ -154,6 +154,35 @@ def test_permute_quant_bit_exact(dev, T, H, E, K, outl):
     assert np.array_equal(xs.cpu().numpy().view(np.uint32), rs.view(np.uint32))
 
 
+@pytest.mark.parametrize("T,K,E,mode", [(1000, 3, 16, "rand"), (700, 6, 64, "skew"),
+                                        (300, 7, 1024, "rand"), (160, 32, 64, "rand"),
+                                        (2000, 5, 8, "one"), (1, 1, 1, "rand"),
+                                        (4099, 8, 256, "skew")])
+def test_dispatch_matches_sort(dev, T, K, E, mode):
+    """smoe_dispatch_quant end to end.  K values that do not divide the
+    512-pair sort segment make tokens straddle segments; skewed and
+    single-expert loads stress the per-expert scan.  Maps, counts, offsets,
+    fp8 bytes and scales must equal the oracle's sort + permute."""
+    say("dispatch", T, K, E, mode)
+    rng = np.random.default_rng(T * K + E)
+    if mode == "one":
+        idx = np.full((T, K), E - 1, np.int32)
+    elif mode == "skew":
+        idx = np.minimum(rng.zipf(1.2, (T, K)) - 1, E - 1).astype(np.int32)
+    else:
+        idx = rng.integers(0, E, (T, K)).astype(np.int32)
+    H = 256
+    x = W.tokens(T, H, outliers=True)
+    xq, xs, rm, im, cnt, off = ops.permute_quant(x.to(dev), torch.from_numpy(idx).to(dev), E)
+    r_rm, r_im, r_cnt, r_off = O.route_sort(idx, E)
+    for got, ref, n in zip((rm, im, cnt, off), (r_rm, r_im, r_cnt, r_off),
+                           ("row_map", "inv_map", "counts", "offsets")):
+        assert np.array_equal(got.cpu().numpy(), ref), n
+    rq, rs = O.permute_quant(np_u16(x), r_im, K)
+    assert np.array_equal(np_u8(xq), rq)
+    assert np.array_equal(xs.cpu().numpy().view(np.uint32), rs.view(np.uint32))
+
+
 def test_permute_quant_zero_and_saturating_groups(dev):
     say("permute_quant zero/sat groups")
     T, H = 8, 256
