@@ -3,28 +3,32 @@
 //
 //   c[r,n] = bf16( sum_kb as[r,kb] * bs[e,n/128,kb] * sum_{k in kb} a[r,k]*b[e,n,k] )
 //
-// Tiling.  A workgroup of 256 threads (4 waves) owns a 256-row x 128-column
-// output tile of one expert; wave w owns rows (w>>1)*128 .. +128 and columns
-// (w&1)*64 .. +64, i.e. 8 x 4 blocks of the 16x16 fp8 MFMA with K = 128
+// Tiling.  A workgroup of 512 threads (8 waves) owns a 256-row x 256-column
+// output tile of one expert; wave w owns rows (w/4)*128 .. +128 and columns
+// (w%4)*64 .. +64, i.e. 8 x 4 blocks of the 16x16 fp8 MFMA with K = 128
 // (v_mfma_f32_16x16x128_f8f6f4).  One MFMA covers a whole 128-wide scale
 // block, so each block's partial sum is scaled by as[r,kb]*bs[e,nb,kb] and
 // added to the fp32 accumulator right away (4 FMAs per MFMA).  Weight rows
 // feed the MFMA's A operand and activation rows its B operand: an output lane
 // holds one activation row (lane % 16), so the activation scale is per lane
-// and the weight scale (one 128-column block per tile) is wave-uniform.
+// and the weight scale (a wave's 64 columns lie in one 128-column block) is
+// wave-uniform.
 //
 // Data movement.  Each K step stages a 256x128-byte activation tile, a
-// 128x128-byte weight tile and the 256 activation scales in LDS with direct
-// global->LDS loads (global_load_lds_dwordx4 / _dword: no VGPR round trip).
-// A lane's 16-byte chunk c of row i lands at chunk position c ^ (i & 7), so
-// the 128-bit fragment reads of 8 consecutive rows hit distinct banks.  Three
-// LDS stages: the loads of step kb+2 are issued before the MFMAs of step kb;
-// the step's single barrier waits only for step kb+1's loads.
+// 256x128-byte weight tile and the 256 activation scales in LDS with direct
+// global->LDS loads (global_load_lds_dwordx4 / _dword: no VGPR round trip),
+// two stages deep: the loads of step kb+1 are issued before the MFMAs of step
+// kb, and the step's single barrier waits for them.  The LDS row layout
+// (lds_row / swz) makes the 128-bit fragment reads conflict-free.  The tile's
+// weight-block scales are copied to LDS once, before the K loop.
 //
-// Scheduling.  The grid covers an upper bound of m-tiles (ceil(R/256) + E)
-// times the n-tiles, remapped so each XCD (8 per device, blocks dealt round
-// robin) works on a contiguous range of tiles, ordered in groups of kGroupM
-// m-tiles that sweep the n-tiles together (weight reuse in L2).  Every
+// Scheduling.  The grid covers an upper bound of m-tiles (ceil(R/256) + E,
+// padded to kChipM) times the n-tiles.  Tiles are taken in chip-wide groups
+// of kChipM consecutive m-tiles x all n-tiles; within a group, XCD x (blocks
+// are dealt to the 8 XCDs round robin) takes m-tiles x*kChipM/8 .. +kChipM/8
+// and sweeps the n-tiles.  All XCDs then stream the same weight slices at
+// once (read from HBM once, the other XCDs hit the last-level cache), and
+// each XCD's L2 serves its own activation rows to all n-tiles.  Every
 // workgroup derives the per-expert m-tile prefix sum from offsets[] in LDS
 // (no host sync, no workspace) and leaves when its tile index is past the
 // real total.  Zero-token experts own no tiles; rows past an expert's end are
@@ -33,7 +37,7 @@
 
 namespace smoe {
 
-constexpr int kGroupM = 4;  // m-tiles per scheduling group
+constexpr int kChipM = 16;  // m-tiles per chip-wide scheduling group (2 per XCD)
 
 // Tile configuration: waves form a kWR (rows) x kWN (columns) grid; each wave
 // owns kRB 16-row blocks x 4 16-column blocks (kRB*16 rows x 64 columns).
@@ -114,16 +118,15 @@ __global__ __launch_bounds__(C::kThreads, 1) void grouped_gemm_fp8_kernel(
   __syncthreads();
   const int total_mt = mstart[E];
 
-  // ---- tile index: XCD-contiguous, then grouped-M order -----------------
-  const int nblk = gridDim.x;  // multiple of 8
+  // ---- tile index: chip-wide m-groups, kChipM/8 m-tiles per XCD ---------
   const int bid = blockIdx.x;
-  const int lin = (bid & 7) * (nblk >> 3) + (bid >> 3);
   const int I = N / 2;
   const int NT = kSwiGLU ? I / kGroup : (N + kBN - 1) / kBN;
-  const int grp = lin / (kGroupM * NT);
-  const int in_g = lin - grp * kGroupM * NT;
-  const int mt = grp * kGroupM + (in_g % kGroupM);
-  const int nt = in_g / kGroupM;
+  constexpr int kXM = kChipM / 8;  // m-tiles per XCD and group
+  const int xcd = bid & 7, kx = bid >> 3;
+  const int g = kx / (kXM * NT), rem = kx - g * (kXM * NT);
+  const int mt = g * kChipM + kXM * xcd + rem % kXM;
+  const int nt = rem / kXM;
   if (mt >= total_mt || mt >= mt_bound) return;
 
   int lo = 0, hi = E;  // largest e with mstart[e] <= mt
@@ -362,7 +365,7 @@ extern "C" int smoe_grouped_gemm_fp8(const uint8_t* a, const float* as, const ui
   const long long mt_bound = (R + C::kBM - 1) / C::kBM + E;
   const long long NT = (N + C::kBN - 1) / C::kBN;
   // pad the m-tile count to whole scheduling groups, the grid to a multiple of 8
-  const long long mt_pad = (mt_bound + kGroupM - 1) / kGroupM * kGroupM;
+  const long long mt_pad = (mt_bound + kChipM - 1) / kChipM * kChipM;
   long long nblk = mt_pad * NT;
   nblk = (nblk + 7) / 8 * 8;
   if (nblk > 0x7fffffffLL) return SMOE_EINVAL_DIM;
@@ -393,7 +396,7 @@ extern "C" int smoe_grouped_gemm_fp8_swiglu(const uint8_t* a, const float* as, c
   const int N = 2 * I;
   const long long mt_bound = (R + C::kBM - 1) / C::kBM + E;
   const long long NT = I / kGroup;
-  const long long mt_pad = (mt_bound + kGroupM - 1) / kGroupM * kGroupM;
+  const long long mt_pad = (mt_bound + kChipM - 1) / kChipM * kChipM;
   long long nblk = mt_pad * NT;
   nblk = (nblk + 7) / 8 * 8;
   if (nblk > 0x7fffffffLL) return SMOE_EINVAL_DIM;
