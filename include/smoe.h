@@ -113,6 +113,19 @@ int smoe_quantize_weight_blockwise(const uint16_t* w, int E, int N, int Kdim, ui
                                    float* ws, void* stream);
 
 /*
+ * Self-test of the division-free quantiser used for bf16 inputs (permute,
+ * row, column and weight quantisation).  It compares the e4m3 bytes of the
+ * IEEE-division rule, e4m3(clamp(x / s)), with the library's
+ * reciprocal-and-correction path for every finite bf16 x and every positive
+ * finite bf16 amax >= |x| (s = amax / 448), about 2^31 pairs, on the GPU.
+ * counts [2] u64 on the device, zeroed by the caller, receives the number of
+ * mismatching bytes and the number of pairs checked.  No counterpart in the
+ * reference: it is the proof that the faster quantiser keeps the bit-exact
+ * contract.
+ */
+int smoe_selftest_quant_division(unsigned long long* counts, void* stream);
+
+/*
  * Dropless fp8 grouped GEMM with blockwise scales.  For each expert e and each
  * row r in [offsets[e], offsets[e+1]):
  *   c[r,n] = bf16( sum_kb as[r,kb]*bs[e,n/128,kb] * sum_{k in kb} a[r,k]*b[e,n,k] )

@@ -69,27 +69,24 @@ __global__ __launch_bounds__(1024) void pad_offsets_kernel(const int32_t* __rest
 // --------------------------------------------- 128x1 column quantisation
 // One 256-thread workgroup per (128-row group, 128-column slab).  The group's
 // rows (an expert's rows split into 128-row groups from its first row; short
-// last groups are zero-padded) are loaded with 8 128-bit non-temporal loads
-// per thread (16 threads per 256-byte row slice), optionally gathered through
-// src = gather[r] / gather_div, and staged as bf16 in LDS.  Thread t then owns
-// column t % 128 and rows (t / 128) * 64 .. +64, so the two halves of a
-// column sit in different waves and every wave reads 64 consecutive columns
-// of one row at a time (conflict-free).  A first pass over LDS finds the
-// half-column amax (the halves meet in LDS), a second quantises; keeping the
-// values in LDS rather than registers leaves room for more resident waves.
-// Each thread writes its 64 fp8 bytes as 4 128-bit stores into the transposed
-// output row (ld bytes apart); the two halves of a row chunk merge in L2.
+// last groups are zero-padded) are loaded with non-temporal 128-bit loads,
+// optionally gathered through src = gather[r] / gather_div.  Thread t owns 8
+// columns (t % 16) * 8 .. +8 of the 8 consecutive rows (t / 16) * 8 .. +8, so
+// everything stays in registers: the column amax is a local max over the 8
+// rows, an xor shuffle over the 4 row groups of a wave, and a 2 KB LDS
+// exchange over the 4 waves; then each thread quantises its 64 values with
+// the division-free bf16 quantiser and writes, per column, its 8 rows as one
+// 8-byte store into the transposed output (ld bytes per column).  The 16
+// stores that cover one column's 128 bytes merge in L2.
 constexpr int kQcCols = 128;
-constexpr int kQcPitch = kQcCols + 8;
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void quant_cols_kernel(
+__global__ __launch_bounds__(256) void quant_cols_kernel(
     const uint16_t* __restrict__ x, const int32_t* __restrict__ gather, int gather_div, int C,
     const int32_t* __restrict__ offsets, const int32_t* __restrict__ pad, int E, int ld,
     uint8_t* __restrict__ q, float* __restrict__ s) {
-  __shared__ __attribute__((aligned(16))) uint16_t tile[kGroup * kQcPitch];
   __shared__ int pad_l[SMOE_MAX_EXPERTS + 1];
-  __shared__ float hmax[2][kQcCols];
-  const int t = threadIdx.x;
+  __shared__ float wmax[4][kQcCols];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   for (int i = t; i <= E; i += 256) pad_l[i] = pad[i];
   __syncthreads();
   const int gpos = blockIdx.x * kGroup;  // position in the padded row space
@@ -104,51 +101,65 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
   const int row0 = offsets[e] + (gpos - pad_l[e]);
   const int valid = min(kGroup, offsets[e + 1] - row0);
   const int c0 = blockIdx.y * kQcCols;
-  const int cc = (t & 15) * 8;  // this thread's 8 columns of each row slice
+  const int cc = (t & 15) * 8;  // this thread's 8 columns
+  const int rg = t >> 4;        // this thread's rows rg*8 .. rg*8+7
   v4u v[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const int r = j * 16 + (t >> 4);
+    const int r = rg * 8 + j;
     v[j] = v4u{0u, 0u, 0u, 0u};
-    if (r < valid && c0 + cc < C) {
+    if (r < valid) {
       const int src = gather ? gather[row0 + r] / gather_div : row0 + r;
       v[j] = __builtin_nontemporal_load((const v4u*)(x + (size_t)src * C + c0 + cc));
     }
   }
+  // column amax: 8 rows here, then the 4 row groups of this wave, then waves
+  float cmax[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) cmax[i] = 0.0f;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const int r = j * 16 + (t >> 4);
-    *(v4u*)&tile[r * kQcPitch + cc] = v[j];
-  }
-  __syncthreads();
-  const int col = t & (kQcCols - 1), half = t >> 7;
-  const uint16_t* tcol = tile + half * 64 * kQcPitch + col;
-  float amax = 0.0f;
-#pragma unroll 16
-  for (int i = 0; i < 64; ++i)
-    amax = fmaxf(amax, fabsf(__uint_as_float((uint32_t)tcol[i * kQcPitch] << 16)));
-  hmax[half][col] = amax;
-  __syncthreads();
-  if (c0 + col >= C) return;
-  amax = fmaxf(hmax[0][col], hmax[1][col]);
-  const float sc = group_scale(amax);
-  uint8_t* dst = q + (size_t)(c0 + col) * ld + gpos + half * 64;
-#pragma unroll 1
-  for (int i0 = 0; i0 < 64; i0 += 16) {
-    uint32_t w[4];
+    const uint32_t wd[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      uint32_t b = 0;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const float f = __uint_as_float((uint32_t)tcol[(i0 + 4 * i + k) * kQcPitch] << 16);
-        b |= quant_one(f, sc) << (8 * k);
-      }
-      w[i] = b;
+      cmax[2 * i] = fmaxf(cmax[2 * i], fabsf(__uint_as_float(wd[i] << 16)));
+      cmax[2 * i + 1] = fmaxf(cmax[2 * i + 1], fabsf(__uint_as_float(wd[i] & 0xffff0000u)));
     }
-    *(uint4*)(dst + i0) = make_uint4(w[0], w[1], w[2], w[3]);
   }
-  if (half == 0) s[(size_t)(c0 + col) * (ld / kGroup) + gpos / kGroup] = sc;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    cmax[i] = fmaxf(cmax[i], __shfl_xor(cmax[i], 16, kWave));
+    cmax[i] = fmaxf(cmax[i], __shfl_xor(cmax[i], 32, kWave));
+  }
+  if (lane < 16) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) wmax[w][cc + i] = cmax[i];
+  }
+  __syncthreads();
+  float sc[8];
+  QDiv d[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int c = cc + i;
+    sc[i] = group_scale(fmaxf(fmaxf(wmax[0][c], wmax[1][c]), fmaxf(wmax[2][c], wmax[3][c])));
+    d[i] = qdiv_setup(sc[i]);
+  }
+  // column c0+cc+i gets bytes for rows gpos + rg*8 .. +8
+  uint8_t* dst = q + (size_t)(c0 + cc) * ld + gpos + rg * 8;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    uint32_t b[2] = {0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t wd = (i & 1) ? (v[j][i >> 1] & 0xffff0000u) : (v[j][i >> 1] << 16);
+      b[j >> 2] |= quant_one_bf16(__uint_as_float(wd), d[i]) << (8 * (j & 3));
+    }
+    *(uint2*)(dst + (size_t)i * ld) = make_uint2(b[0], b[1]);
+  }
+  if (rg == 0) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s[(size_t)(c0 + cc + i) * (ld / kGroup) + gpos / kGroup] = sc[i];
+  }
 }
 
 // ------------------------------------------------------- SwiGLU backward

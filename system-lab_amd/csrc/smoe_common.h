@@ -41,13 +41,10 @@ __device__ __forceinline__ uint32_t e4m3_encode(float v) {
   uint32_t sign = (u >> 24) & 0x80u;
   uint32_t a = u & 0x7fffffffu;
   float af = __uint_as_float(a);
-  uint32_t q;
-  if (af < 0.015625f) {
-    q = (uint32_t)__builtin_rintf(af * 512.0f);
-  } else {
-    q = ((a + 0x7ffffu + ((a >> 20) & 1u)) >> 20) - (120u << 3);
-  }
-  return q | sign;
+  // both ranges are evaluated and one is selected (no divergent branch)
+  const uint32_t q_sub = (uint32_t)__builtin_rintf(af * 512.0f);
+  const uint32_t q_nrm = ((a + 0x7ffffu + ((a >> 20) & 1u)) >> 20) - (120u << 3);
+  return (af < 0.015625f ? q_sub : q_nrm) | sign;
 }
 
 // q = e4m3(clamp(x / s, +-448)).  x / s is an IEEE fp32 division.
@@ -60,6 +57,37 @@ __device__ __forceinline__ uint32_t quant_one(float x, float s) {
 // s = amax / 448 (fp32 RN), 1 when amax == 0.
 __device__ __forceinline__ float group_scale(float amax) {
   return amax == 0.0f ? 1.0f : amax / kE4M3Max;
+}
+
+// Division-free quantiser for bf16 inputs.  With s = m * 2^e (m in [0.5, 1))
+// and r = RN(1/m) computed once per group, each element takes
+//   xs = x * 2^-e (exact), q0 = RN(xs * r), d = fma(-q0, m, xs),
+//   q = fma(d, r, q0) with the sign of x,
+// i.e. a reciprocal-based quotient with one residual correction.  The
+// quotient itself can differ from the IEEE quotient x / s in its last bit,
+// but e4m3(clamp(q)) equals e4m3(clamp(x / s)) for every finite bf16 x and
+// every bf16 amax >= |x| with s = group_scale(amax): this is checked
+// exhaustively over that whole domain (about 2^31 pairs) on the GPU by
+// smoe_selftest_quant_division.  Inputs that are not bf16 (SwiGLU's fp32 h)
+// use quant_one.
+struct QDiv {
+  float m, r;
+  int e;
+};
+__device__ __forceinline__ QDiv qdiv_setup(float s) {
+  QDiv d;
+  d.m = __builtin_frexpf(s, &d.e);
+  d.r = 1.0f / d.m;
+  return d;
+}
+__device__ __forceinline__ uint32_t quant_one_bf16(float x, const QDiv& d) {
+  const float xs = __builtin_ldexpf(x, -d.e);
+  const float q0 = xs * d.r;
+  const float res = __builtin_fmaf(-q0, d.m, xs);
+  float y = __builtin_fmaf(res, d.r, q0);
+  y = __uint_as_float((__float_as_uint(y) & 0x7fffffffu) | (__float_as_uint(x) & 0x80000000u));
+  y = fminf(fmaxf(y, -kE4M3Max), kE4M3Max);
+  return e4m3_encode(y);
 }
 
 // ---------------------------------------------------------------- exp -----
@@ -129,6 +157,26 @@ __device__ __forceinline__ Q16 quant16(const float (&f)[16]) {
     w[i] = quant_one(f[4 * i], s) | (quant_one(f[4 * i + 1], s) << 8) |
            (quant_one(f[4 * i + 2], s) << 16) |
            (quant_one(f[4 * i + 3], s) << 24);
+  }
+  Q16 r;
+  r.q = make_uint4(w[0], w[1], w[2], w[3]);
+  r.scale = s;
+  return r;
+}
+
+// As quant16, for bf16 inputs (the division-free quantiser).
+__device__ __forceinline__ Q16 quant16_bf16(const float (&f)[16]) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(f[i]));
+  amax = group_max<8>(amax);
+  const float s = group_scale(amax);
+  const QDiv d = qdiv_setup(s);
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    w[i] = quant_one_bf16(f[4 * i], d) | (quant_one_bf16(f[4 * i + 1], d) << 8) |
+           (quant_one_bf16(f[4 * i + 2], d) << 16) | (quant_one_bf16(f[4 * i + 3], d) << 24);
   }
   Q16 r;
   r.q = make_uint4(w[0], w[1], w[2], w[3]);

@@ -62,7 +62,7 @@ __global__ __launch_bounds__(256) void permute_quant_kernel(
       float f[16];
       unpack_bf16x8(v[u][0], f);
       unpack_bf16x8(v[u][1], f + 8);
-      q[u] = quant16(f);
+      q[u] = quant16_bf16(f);
     }
     for (int k = 0; k < K; ++k) {
       const int r = __shfl(my_r, k, kWave);
@@ -167,22 +167,62 @@ __global__ __launch_bounds__(256) void quant_weight_kernel(const uint16_t* __res
   __syncthreads();
   amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
   const float s = group_scale(amax);
+  const QDiv d = qdiv_setup(s);
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int ch = j * 256 + threadIdx.x;
     const int row = ch >> 4, col = (ch & 15) * 8;
-    uint32_t lo = quant_one(f[j][0], s) | (quant_one(f[j][1], s) << 8) |
-                  (quant_one(f[j][2], s) << 16) | (quant_one(f[j][3], s) << 24);
-    uint32_t hi = quant_one(f[j][4], s) | (quant_one(f[j][5], s) << 8) |
-                  (quant_one(f[j][6], s) << 16) | (quant_one(f[j][7], s) << 24);
+    uint32_t lo = quant_one_bf16(f[j][0], d) | (quant_one_bf16(f[j][1], d) << 8) |
+                  (quant_one_bf16(f[j][2], d) << 16) | (quant_one_bf16(f[j][3], d) << 24);
+    uint32_t hi = quant_one_bf16(f[j][4], d) | (quant_one_bf16(f[j][5], d) << 8) |
+                  (quant_one_bf16(f[j][6], d) << 16) | (quant_one_bf16(f[j][7], d) << 24);
     *(uint2*)(wq + base + (size_t)row * Kd + col) = make_uint2(lo, hi);
   }
   if (threadIdx.x == 0) ws[((size_t)e * nb + bn) * kb + bk] = s;
 }
 
+// Exhaustive check of the division-free quantiser: for every positive finite
+// bf16 amax (blockIdx.y) and every finite bf16 x with |x| <= amax (both
+// signs), compare e4m3(clamp(x / s)) with quant_one_bf16(x) for
+// s = group_scale(amax).  counts[0] accumulates mismatching bytes and
+// counts[1] the number of pairs checked.
+__global__ __launch_bounds__(256) void selftest_quant_division_kernel(
+    unsigned long long* __restrict__ counts) {
+  const uint32_t abits = blockIdx.y + 1;  // 0x0001 .. 0x7f7f
+  const float amax = __uint_as_float(abits << 16);
+  const float s = group_scale(amax);
+  const QDiv d = qdiv_setup(s);
+  unsigned long long bad = 0, n = 0;
+  for (uint32_t xb = blockIdx.x * blockDim.x + threadIdx.x; xb <= abits;
+       xb += gridDim.x * blockDim.x) {
+#pragma unroll
+    for (int sg = 0; sg < 2; ++sg) {
+      const float x = __uint_as_float((xb << 16) | (sg ? 0x80000000u : 0u));
+      bad += quant_one(x, s) != quant_one_bf16(x, d);
+      ++n;
+    }
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    bad += __shfl_xor(bad, o, kWave);
+    n += __shfl_xor(n, o, kWave);
+  }
+  if ((threadIdx.x & 63) == 0) {
+    atomicAdd(&counts[0], bad);
+    atomicAdd(&counts[1], n);
+  }
+}
+
 }  // namespace smoe
 
 using namespace smoe;
+
+extern "C" int smoe_selftest_quant_division(unsigned long long* counts, void* stream) {
+  if (!counts) return SMOE_EINVAL_NULL;
+  if ((uintptr_t)counts & 7u) return SMOE_EINVAL_PTRALIGN;
+  selftest_quant_division_kernel<<<dim3(64, 0x7f7f), dim3(256), 0, (hipStream_t)stream>>>(
+      counts);
+  SMOE_RETURN_LAUNCH();
+}
 
 extern "C" int smoe_permute_quant(const uint16_t* x, const int32_t* inv_map, int T, int H, int K,
                                   uint8_t* xq, float* xs, void* stream) {

@@ -137,6 +137,21 @@ def test_permute_quant_every_bf16_value(dev):
     assert (rs == 1.0).all()
 
 
+def test_division_free_quantiser_exhaustive(dev):
+    """The bf16 kernels (permute, row, column and weight quantisation) divide
+    by the group scale with a reciprocal and one residual correction instead
+    of an IEEE division.  The library's self-test compares the e4m3 bytes of
+    both for every finite bf16 x and every positive finite bf16 amax >= |x|
+    (s = amax / 448): the whole input domain of those kernels."""
+    say("division-free quantiser exhaustive")
+    counts = torch.zeros(2, dtype=torch.int64, device=dev)
+    smoe._C.call("smoe_selftest_quant_division", counts.data_ptr(),
+                 torch.cuda.current_stream().cuda_stream)
+    bad, n = counts.cpu().tolist()
+    assert n == sum(2 * (a + 1) for a in range(1, 0x7f80))
+    assert bad == 0
+
+
 @pytest.mark.parametrize("T,H,E,K,outl", [(2048, 1024, 8, 2, False), (1024, 7168, 256, 8, True),
                                           (333, 4096, 8, 2, False), (512, 2048, 128, 8, False),
                                           (5, 1152, 4, 3, True), (64, 9216, 16, 4, True)])
