@@ -222,12 +222,13 @@ int smoe_transpose_blockwise_fp8(const uint8_t* wq, const float* ws, int E, int 
  * Transposed 128x1 column quantisation of x [R,C] bf16 whose rows are the
  * expert segments offsets[E+1].  When gather is not NULL, row r of the
  * operand is x[gather[r] / gather_div] (e.g. row_map and K: the sorted
- * tokens of the forward, gathered on the fly).  Each expert's rows are split into 128-row
- * groups from its first row (short last groups zero-padded); group g of
- * expert e is column block pad[e]/128 + g of the output.  -> xTq [C, ld] u8,
+ * tokens of the forward, gathered on the fly).  Each expert's rows are split
+ * into 128-row groups from its first row (short last groups zero-padded);
+ * group g of expert e is column block pad[e]/128 + g of the output.
+ * -> xTq [C, ld] u8,
  * xTs [C, ld/128] f32, pad [E+1] i32 (pad[e+1] = pad[e] + ceil(count/128)*128).
  * ld must be >= smoe_quant_cols_ld(R, E) (an upper bound known on the host;
- * columns past pad[E] are left untouched).
+ * columns past pad[E] are left untouched) and ld/128 <= 65535.
  */
 int smoe_quant_cols_ld(int R, int E);
 int smoe_quant_cols_128x1(const uint16_t* x, const int32_t* gather, int gather_div, int R, int C,

@@ -89,7 +89,7 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   for (int i = t; i <= E; i += 256) pad_l[i] = pad[i];
   __syncthreads();
-  const int gpos = blockIdx.x * kGroup;  // position in the padded row space
+  const int gpos = blockIdx.y * kGroup;  // position in the padded row space
   if (gpos >= pad_l[E]) return;          // whole workgroup leaves together
   int lo = 0, hi = E;                    // largest e with pad[e] <= gpos
   while (hi - lo > 1) {
@@ -100,7 +100,7 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(
   const int e = lo;
   const int row0 = offsets[e] + (gpos - pad_l[e]);
   const int valid = min(kGroup, offsets[e + 1] - row0);
-  const int c0 = blockIdx.y * kQcCols;
+  const int c0 = blockIdx.x * kQcCols;
   const int cc = (t & 15) * 8;  // this thread's 8 columns
   const int rg = t >> 4;        // this thread's rows rg*8 .. rg*8+7
   v4u v[8];
@@ -296,13 +296,15 @@ extern "C" int smoe_quant_cols_128x1(const uint16_t* x, const int32_t* gather, i
   if (E <= 0 || E > SMOE_MAX_EXPERTS) return SMOE_EINVAL_EXPERTS;
   if (C % kGroup) return SMOE_EINVAL_ALIGN128;
   if (ld < smoe_quant_cols_ld(R, E) || ld % kGroup) return SMOE_EINVAL_DIM;
+  if (ld / kGroup > 65535) return SMOE_EINVAL_DIM;  // 128-row groups are grid.y
   SMOE_CHECK_PTR(x);
   SMOE_CHECK_PTR(xTq);
   if (!offsets || !xTs || !pad) return SMOE_EINVAL_NULL;
   if (((uintptr_t)offsets | (uintptr_t)xTs | (uintptr_t)pad) & 3u) return SMOE_EINVAL_PTRALIGN;
   hipStream_t s = (hipStream_t)stream;
   pad_offsets_kernel<<<1, 1024, 0, s>>>(offsets, E, pad);
-  quant_cols_kernel<<<dim3(ld / kGroup, (C + kQcCols - 1) / kQcCols), dim3(256), 0, s>>>(
+  // column slabs vary fastest, so the workgroups in flight read whole rows
+  quant_cols_kernel<<<dim3((C + kQcCols - 1) / kQcCols, ld / kGroup), dim3(256), 0, s>>>(
       x, gather, gather ? gather_div : 1, C, offsets, pad, E, ld, xTq, xTs);
   SMOE_RETURN_LAUNCH();
 }
