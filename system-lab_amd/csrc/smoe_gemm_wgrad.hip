@@ -121,19 +121,38 @@ __global__ __launch_bounds__(kWThreads, 1) void grouped_gemm_fp8_wgrad_kernel(
     asm volatile("" ::: "memory");
   }
 
-  // lane holds k = (lane%16) of each 16-row block i, n = (lane/16)*4 + v
+  // Epilogue: the fp32 tile leaves through LDS in two 128-row halves (the
+  // stage buffers are free after the K loop's last barrier).  Lane (i, j, v)
+  // holds dW row n = wn*64 + j*16 + (lane/16)*4 + v, column k = wk*128 +
+  // i*16 + lane%16; with a row pitch of 260 floats the 4 lane groups of a
+  // write land 16 banks apart, so the writes are conflict-free.  Then each
+  // wave stores whole 1 KB rows, 16 bytes per lane, non-temporally (dW is
+  // written once here and read by a later kernel).
+  float* ct = (float*)smem;
+  constexpr int kPitch = kWK + 4;
+  static_assert(128 * kPitch * 4 <= 2 * kWStage, "epilogue half-tile fits the stage buffers");
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int kl = wk * 128 + i * 16 + frow;
-    if (kl >= krows) continue;
+  for (int half = 0; half < 2; ++half) {
+    if ((wn >> 1) == half) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+      for (int i = 0; i < 8; ++i)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int nl = wn * 64 + j * 16 + (lane >> 4) * 4 + v;
-        if (nl < nrows) dW[((size_t)e * N + n0 + nl) * Kd + k0 + kl] = acc[i][j][v];
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int row = (wn & 1) * 64 + j * 16 + (lane >> 4) * 4 + v;
+            ct[row * kPitch + wk * 128 + i * 16 + frow] = acc[i][j][v];
+          }
+    }
+    __syncthreads();
+    for (int r = wid; r < 128; r += 8) {
+      const int nl = half * 128 + r;
+      if (nl < nrows && lane * 4 < krows) {
+        const v4f val = *(const v4f*)(ct + r * kPitch + lane * 4);
+        __builtin_nontemporal_store(val, (v4f*)(dW + ((size_t)e * N + n0 + nl) * Kd + k0 + lane * 4));
       }
     }
+    __syncthreads();
   }
 }
 
