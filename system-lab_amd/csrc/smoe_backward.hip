@@ -235,10 +235,15 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(
       d[2 * i] = __uint_as_float(d4[i] << 16);
       d[2 * i + 1] = __uint_as_float(d4[i] & 0xffff0000u);
     }
+    // all K rows' loads are issued before any arithmetic or store
+    uint4 vyk[kMaxK];
+#pragma unroll
+    for (int k = 0; k < kMaxK; ++k)
+      if (k < K && (unsigned)r[k] < (unsigned)R) vyk[k] = *(const uint4*)(y + (size_t)r[k] * H + col);
 #pragma unroll
     for (int k = 0; k < kMaxK; ++k) {
       if (k >= K || (unsigned)r[k] >= (unsigned)R) continue;
-      const uint4 vy = *(const uint4*)(y + (size_t)r[k] * H + col);
+      const uint4 vy = vyk[k];
       const uint32_t y4[4] = {vy.x, vy.y, vy.z, vy.w};
       uint32_t o[4];
 #pragma unroll
