@@ -33,7 +33,7 @@ sys.path.insert(0, os.path.join(ROOT, "system-lab_amd"))
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per permute_quant launch at config 2 from rocprofv3 FETCH_SIZE
 # (x2.0 copy calibration) + WRITE_SIZE (x1.0): profiles/permute_quant_cfg2.md
-PERMUTE_TRAFFIC_BYTES = 1_212_500_000
+PERMUTE_TRAFFIC_BYTES = 1_211_621_376
 FP8_PEAK_TFLOPS = 5000.0
 
 
