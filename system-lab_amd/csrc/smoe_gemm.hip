@@ -28,7 +28,8 @@
 // are dealt to the 8 XCDs round robin) takes m-tiles x*kChipM/8 .. +kChipM/8
 // and sweeps the n-tiles.  All XCDs then stream the same weight slices at
 // once (read from HBM once, the other XCDs hit the last-level cache), and
-// each XCD's L2 serves its own activation rows to all n-tiles.  Every
+// each XCD's L2 serves its own activation rows to all n-tiles.  A last,
+// partial group's tiles are split evenly over the 8 XCDs instead.  Every
 // workgroup derives the per-expert m-tile prefix sum from offsets[] in LDS
 // (no host sync, no workspace) and leaves when its tile index is past the
 // real total.  Zero-token experts own no tiles; rows past an expert's end are
@@ -124,10 +125,24 @@ __global__ __launch_bounds__(C::kThreads, 1) void grouped_gemm_fp8_kernel(
   const int NT = kSwiGLU ? I / kGroup : (N + kBN - 1) / kBN;
   constexpr int kXM = kChipM / 8;  // m-tiles per XCD and group
   const int xcd = bid & 7, kx = bid >> 3;
-  const int g = kx / (kXM * NT), rem = kx - g * (kXM * NT);
-  const int mt = g * kChipM + kXM * xcd + rem % kXM;
-  const int nt = rem / kXM;
-  if (mt >= total_mt || mt >= mt_bound) return;
+  const int m_all = min(total_mt, mt_bound);
+  const int full = m_all / kChipM;     // complete chip-wide groups
+  const int m_last = m_all - full * kChipM;  // m-tiles of the last, partial group
+  int mt, nt;
+  if (kx < full * kXM * NT) {
+    const int g = kx / (kXM * NT), rem = kx - g * (kXM * NT);
+    mt = g * kChipM + kXM * xcd + rem % kXM;
+    nt = rem / kXM;
+  } else {
+    // the partial group's m_last x NT tiles, m fastest, split into 8 equal
+    // contiguous chunks so that every XCD gets a share
+    const int chunk = (m_last * NT + 7) / 8;
+    const int j = kx - full * kXM * NT;
+    const int tl = xcd * chunk + j;
+    if (j >= chunk || tl >= m_last * NT) return;
+    mt = full * kChipM + tl % m_last;
+    nt = tl / m_last;
+  }
 
   int lo = 0, hi = E;  // largest e with mstart[e] <= mt
   while (hi - lo > 1) {
