@@ -113,17 +113,19 @@ int smoe_quantize_weight_blockwise(const uint16_t* w, int E, int N, int Kdim, ui
                                    float* ws, void* stream);
 
 /*
- * Self-test of the division-free quantiser used for bf16 inputs (permute,
- * row, column and weight quantisation).  It compares the e4m3 bytes of the
- * IEEE-division rule, e4m3(clamp(x / s)), with the library's
- * reciprocal-and-correction path for every finite bf16 x and every positive
- * finite bf16 amax >= |x| (s = amax / 448), about 2^31 pairs, on the GPU.
- * counts [2] u64 on the device, zeroed by the caller, receives the number of
- * mismatching bytes and the number of pairs checked.  No counterpart in the
- * reference: it is the proof that the faster quantiser keeps the bit-exact
- * contract.
+ * Self-test of the fast quantisation path (no counterpart in the reference:
+ * it proves that the faster kernels keep the bit-exact contract).  The
+ * contract's rule is e4m3(clamp(x / s)) with an IEEE division and an RNE
+ * encoder.  The kernels instead divide bf16 inputs with a reciprocal and one
+ * correction, and encode with the hardware conversion.  Checked on the GPU,
+ * exhaustively: (1) the bytes of the bf16 path for every finite bf16 x and
+ * every positive finite bf16 amax >= |x| (s = amax / 448), about 1.07e9
+ * pairs; (2) the hardware encoder for every fp32 with |v| <= 448, about
+ * 2.28e9 values.  counts [4] u64 on the device, zeroed by the caller,
+ * receives: mismatches (1), pairs checked (1), mismatches (2), values
+ * checked (2).
  */
-int smoe_selftest_quant_division(unsigned long long* counts, void* stream);
+int smoe_selftest_quant(unsigned long long* counts, void* stream);
 
 /*
  * Dropless fp8 grouped GEMM with blockwise scales.  For each expert e and each

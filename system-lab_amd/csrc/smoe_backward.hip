@@ -148,12 +148,14 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(
   uint8_t* dst = q + (size_t)(c0 + cc) * ld + gpos + rg * 8;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    uint32_t b[2] = {0u, 0u};
+    float qv[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const uint32_t wd = (i & 1) ? (v[j][i >> 1] & 0xffff0000u) : (v[j][i >> 1] << 16);
-      b[j >> 2] |= quant_one_bf16(__uint_as_float(wd), d[i]) << (8 * (j & 3));
+      qv[j] = quot_bf16(__uint_as_float(wd), d[i]);
     }
+    const uint32_t b[2] = {e4m3_pack4(qv[0], qv[1], qv[2], qv[3]),
+                           e4m3_pack4(qv[4], qv[5], qv[6], qv[7])};
     *(uint2*)(dst + (size_t)i * ld) = make_uint2(b[0], b[1]);
   }
   if (rg == 0) {

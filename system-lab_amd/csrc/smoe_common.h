@@ -31,27 +31,43 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
 }
 
 // ---------------------------------------------------------------- e4m3 ----
-// OCP e4m3fn encode of |v| <= 448 with round-to-nearest-even.
-// Subnormal range |v| < 2^-6: code = rint(|v| * 2^9) (the product is exact;
-// a result of 8 is the smallest normal, 0x08, which is the correct code).
-// Normal range: RNE to 3 mantissa bits on the fp32 pattern, then rebias the
-// exponent 127 -> 7 (subtract 120 << 3 from the combined exponent|mantissa).
-__device__ __forceinline__ uint32_t e4m3_encode(float v) {
+// Reference OCP e4m3fn encode of |v| <= 448 with round-to-nearest-even, in
+// software.  Subnormal range |v| < 2^-6: code = rint(|v| * 2^9) (the product
+// is exact; a result of 8 is the smallest normal, 0x08, which is the correct
+// code).  Normal range: RNE to 3 mantissa bits on the fp32 pattern, then
+// rebias the exponent 127 -> 7 (subtract 120 << 3 from the combined
+// exponent|mantissa).  The kernels use the hardware conversion below; this
+// is what smoe_selftest_quant checks it against.
+__device__ __forceinline__ uint32_t e4m3_encode_sw(float v) {
   uint32_t u = __float_as_uint(v);
   uint32_t sign = (u >> 24) & 0x80u;
   uint32_t a = u & 0x7fffffffu;
   float af = __uint_as_float(a);
-  // both ranges are evaluated and one is selected (no divergent branch)
   const uint32_t q_sub = (uint32_t)__builtin_rintf(af * 512.0f);
   const uint32_t q_nrm = ((a + 0x7ffffu + ((a >> 20) & 1u)) >> 20) - (120u << 3);
   return (af < 0.015625f ? q_sub : q_nrm) | sign;
 }
 
-// q = e4m3(clamp(x / s, +-448)).  x / s is an IEEE fp32 division.
+// Four values (each |v| <= 448) to four e4m3 bytes, a in the low byte, with
+// gfx950's v_cvt_pk_fp8_f32 (OCP e4m3fn, round to nearest even): identical
+// to e4m3_encode_sw for every fp32 with |v| <= 448, which smoe_selftest_quant
+// checks exhaustively.  It does not saturate (464 and above become NaN), so
+// its inputs are clamped or bounded by construction.
+__device__ __forceinline__ uint32_t e4m3_pack4(float a, float b, float c, float d) {
+  const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true);
+}
+
+// clamp(x / s, +-448) with an IEEE fp32 division: the quotient the
+// quantisation rule is defined on.
+__device__ __forceinline__ float quot_ieee(float x, float s) {
+  const float y = x / s;
+  return fminf(fmaxf(y, -kE4M3Max), kE4M3Max);
+}
+
+// Reference rule for one value: e4m3(clamp(x / s)).
 __device__ __forceinline__ uint32_t quant_one(float x, float s) {
-  float y = x / s;
-  y = fminf(fmaxf(y, -kE4M3Max), kE4M3Max);
-  return e4m3_encode(y);
+  return e4m3_encode_sw(quot_ieee(x, s));
 }
 
 // s = amax / 448 (fp32 RN), 1 when amax == 0.
@@ -59,17 +75,17 @@ __device__ __forceinline__ float group_scale(float amax) {
   return amax == 0.0f ? 1.0f : amax / kE4M3Max;
 }
 
-// Division-free quantiser for bf16 inputs.  With s = m * 2^e (m in [0.5, 1))
+// Division-free quotient for bf16 inputs.  With s = m * 2^e (m in [0.5, 1))
 // and r = RN(1/m) computed once per group, each element takes
 //   xs = x * 2^-e (exact), q0 = RN(xs * r), d = fma(-q0, m, xs),
 //   q = fma(d, r, q0) with the sign of x,
 // i.e. a reciprocal-based quotient with one residual correction.  The
-// quotient itself can differ from the IEEE quotient x / s in its last bit,
-// but e4m3(clamp(q)) equals e4m3(clamp(x / s)) for every finite bf16 x and
-// every bf16 amax >= |x| with s = group_scale(amax): this is checked
-// exhaustively over that whole domain (about 2^31 pairs) on the GPU by
-// smoe_selftest_quant_division.  Inputs that are not bf16 (SwiGLU's fp32 h)
-// use quant_one.
+// quotient can differ from the IEEE quotient x / s in its last bit, but its
+// e4m3 byte equals e4m3(clamp(x / s)) for every finite bf16 x and every bf16
+// amax >= |x| with s = group_scale(amax), with no clamp needed (|q| stays
+// below the 464 rounding boundary): smoe_selftest_quant checks this
+// exhaustively over that whole domain on the GPU.  Inputs that are not bf16
+// (SwiGLU's fp32 h) use quot_ieee.
 struct QDiv {
   float m, r;
   int e;
@@ -80,14 +96,12 @@ __device__ __forceinline__ QDiv qdiv_setup(float s) {
   d.r = 1.0f / d.m;
   return d;
 }
-__device__ __forceinline__ uint32_t quant_one_bf16(float x, const QDiv& d) {
+__device__ __forceinline__ float quot_bf16(float x, const QDiv& d) {
   const float xs = __builtin_ldexpf(x, -d.e);
   const float q0 = xs * d.r;
   const float res = __builtin_fmaf(-q0, d.m, xs);
-  float y = __builtin_fmaf(res, d.r, q0);
-  y = __uint_as_float((__float_as_uint(y) & 0x7fffffffu) | (__float_as_uint(x) & 0x80000000u));
-  y = fminf(fmaxf(y, -kE4M3Max), kE4M3Max);
-  return e4m3_encode(y);
+  const float y = __builtin_fmaf(res, d.r, q0);
+  return __uint_as_float((__float_as_uint(y) & 0x7fffffffu) | (__float_as_uint(x) & 0x80000000u));
 }
 
 // ---------------------------------------------------------------- exp -----
@@ -153,11 +167,9 @@ __device__ __forceinline__ Q16 quant16(const float (&f)[16]) {
   const float s = group_scale(amax);
   uint32_t w[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    w[i] = quant_one(f[4 * i], s) | (quant_one(f[4 * i + 1], s) << 8) |
-           (quant_one(f[4 * i + 2], s) << 16) |
-           (quant_one(f[4 * i + 3], s) << 24);
-  }
+  for (int i = 0; i < 4; ++i)
+    w[i] = e4m3_pack4(quot_ieee(f[4 * i], s), quot_ieee(f[4 * i + 1], s),
+                      quot_ieee(f[4 * i + 2], s), quot_ieee(f[4 * i + 3], s));
   Q16 r;
   r.q = make_uint4(w[0], w[1], w[2], w[3]);
   r.scale = s;
@@ -174,10 +186,9 @@ __device__ __forceinline__ Q16 quant16_bf16(const float (&f)[16]) {
   const QDiv d = qdiv_setup(s);
   uint32_t w[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    w[i] = quant_one_bf16(f[4 * i], d) | (quant_one_bf16(f[4 * i + 1], d) << 8) |
-           (quant_one_bf16(f[4 * i + 2], d) << 16) | (quant_one_bf16(f[4 * i + 3], d) << 24);
-  }
+  for (int i = 0; i < 4; ++i)
+    w[i] = e4m3_pack4(quot_bf16(f[4 * i], d), quot_bf16(f[4 * i + 1], d),
+                      quot_bf16(f[4 * i + 2], d), quot_bf16(f[4 * i + 3], d));
   Q16 r;
   r.q = make_uint4(w[0], w[1], w[2], w[3]);
   r.scale = s;
@@ -193,7 +204,6 @@ __device__ __forceinline__ void unpack_bf16x8(const uint4& v, float* f) {
   }
 }
 
-// ---------------------------------------------------------- permute_quant
 }  // namespace smoe
 
 // ------------------------------------------------------ host validation ----

@@ -172,21 +172,22 @@ __global__ __launch_bounds__(256) void quant_weight_kernel(const uint16_t* __res
   for (int j = 0; j < 8; ++j) {
     const int ch = j * 256 + threadIdx.x;
     const int row = ch >> 4, col = (ch & 15) * 8;
-    uint32_t lo = quant_one_bf16(f[j][0], d) | (quant_one_bf16(f[j][1], d) << 8) |
-                  (quant_one_bf16(f[j][2], d) << 16) | (quant_one_bf16(f[j][3], d) << 24);
-    uint32_t hi = quant_one_bf16(f[j][4], d) | (quant_one_bf16(f[j][5], d) << 8) |
-                  (quant_one_bf16(f[j][6], d) << 16) | (quant_one_bf16(f[j][7], d) << 24);
+    const uint32_t lo = e4m3_pack4(quot_bf16(f[j][0], d), quot_bf16(f[j][1], d),
+                                   quot_bf16(f[j][2], d), quot_bf16(f[j][3], d));
+    const uint32_t hi = e4m3_pack4(quot_bf16(f[j][4], d), quot_bf16(f[j][5], d),
+                                   quot_bf16(f[j][6], d), quot_bf16(f[j][7], d));
     *(uint2*)(wq + base + (size_t)row * Kd + col) = make_uint2(lo, hi);
   }
   if (threadIdx.x == 0) ws[((size_t)e * nb + bn) * kb + bk] = s;
 }
 
-// Exhaustive check of the division-free quantiser: for every positive finite
-// bf16 amax (blockIdx.y) and every finite bf16 x with |x| <= amax (both
-// signs), compare e4m3(clamp(x / s)) with quant_one_bf16(x) for
-// s = group_scale(amax).  counts[0] accumulates mismatching bytes and
-// counts[1] the number of pairs checked.
-__global__ __launch_bounds__(256) void selftest_quant_division_kernel(
+// Exhaustive checks of the fast quantisation path against the reference
+// rule e4m3_encode_sw(clamp(x / s)) with an IEEE division.
+// (1) For every positive finite bf16 amax (blockIdx.y) and every finite bf16
+// x with |x| <= amax (both signs), s = group_scale(amax): the byte of the
+// division-free quotient converted by v_cvt_pk_fp8_f32.  counts[0] gets the
+// mismatches, counts[1] the pairs checked.
+__global__ __launch_bounds__(256) void selftest_quant_bf16_kernel(
     unsigned long long* __restrict__ counts) {
   const uint32_t abits = blockIdx.y + 1;  // 0x0001 .. 0x7f7f
   const float amax = __uint_as_float(abits << 16);
@@ -198,7 +199,8 @@ __global__ __launch_bounds__(256) void selftest_quant_division_kernel(
 #pragma unroll
     for (int sg = 0; sg < 2; ++sg) {
       const float x = __uint_as_float((xb << 16) | (sg ? 0x80000000u : 0u));
-      bad += quant_one(x, s) != quant_one_bf16(x, d);
+      const uint32_t fast = e4m3_pack4(quot_bf16(x, d), 0.0f, 0.0f, 0.0f) & 0xffu;
+      bad += quant_one(x, s) != fast;
       ++n;
     }
   }
@@ -212,15 +214,41 @@ __global__ __launch_bounds__(256) void selftest_quant_division_kernel(
   }
 }
 
+// (2) For every fp32 v with |v| <= 448 (both signs): the hardware conversion
+// against e4m3_encode_sw.  counts[2] gets the mismatches, counts[3] the
+// values checked.
+__global__ __launch_bounds__(256) void selftest_e4m3_kernel(unsigned long long* __restrict__ counts) {
+  const uint32_t lim = __float_as_uint(kE4M3Max);
+  unsigned long long bad = 0, n = 0;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i <= lim;
+       i += (uint64_t)gridDim.x * blockDim.x) {
+#pragma unroll
+    for (int sg = 0; sg < 2; ++sg) {
+      const float v = __uint_as_float((uint32_t)i | (sg ? 0x80000000u : 0u));
+      bad += e4m3_encode_sw(v) != (e4m3_pack4(v, 0.0f, 0.0f, 0.0f) & 0xffu);
+      ++n;
+    }
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    bad += __shfl_xor(bad, o, kWave);
+    n += __shfl_xor(n, o, kWave);
+  }
+  if ((threadIdx.x & 63) == 0) {
+    atomicAdd(&counts[2], bad);
+    atomicAdd(&counts[3], n);
+  }
+}
+
 }  // namespace smoe
 
 using namespace smoe;
 
-extern "C" int smoe_selftest_quant_division(unsigned long long* counts, void* stream) {
+extern "C" int smoe_selftest_quant(unsigned long long* counts, void* stream) {
   if (!counts) return SMOE_EINVAL_NULL;
   if ((uintptr_t)counts & 7u) return SMOE_EINVAL_PTRALIGN;
-  selftest_quant_division_kernel<<<dim3(64, 0x7f7f), dim3(256), 0, (hipStream_t)stream>>>(
-      counts);
+  hipStream_t st = (hipStream_t)stream;
+  selftest_quant_bf16_kernel<<<dim3(64, 0x7f7f), dim3(256), 0, st>>>(counts);
+  selftest_e4m3_kernel<<<dim3(4096), dim3(256), 0, st>>>(counts);
   SMOE_RETURN_LAUNCH();
 }
 

@@ -137,19 +137,21 @@ def test_permute_quant_every_bf16_value(dev):
     assert (rs == 1.0).all()
 
 
-def test_division_free_quantiser_exhaustive(dev):
+def test_fast_quantiser_exhaustive(dev):
     """The bf16 kernels (permute, row, column and weight quantisation) divide
     by the group scale with a reciprocal and one residual correction instead
-    of an IEEE division.  The library's self-test compares the e4m3 bytes of
-    both for every finite bf16 x and every positive finite bf16 amax >= |x|
-    (s = amax / 448): the whole input domain of those kernels."""
-    say("division-free quantiser exhaustive")
-    counts = torch.zeros(2, dtype=torch.int64, device=dev)
-    smoe._C.call("smoe_selftest_quant_division", counts.data_ptr(),
-                 torch.cuda.current_stream().cuda_stream)
-    bad, n = counts.cpu().tolist()
-    assert n == sum(2 * (a + 1) for a in range(1, 0x7f80))
-    assert bad == 0
+    of an IEEE division, and every kernel encodes with the hardware fp8
+    conversion instead of the software RNE encoder.  The library's self-test
+    compares both with the reference rule exhaustively: every finite bf16 x
+    against every positive finite bf16 amax >= |x| (s = amax / 448), and every
+    fp32 with |v| <= 448 through the encoder."""
+    say("fast quantiser exhaustive")
+    counts = torch.zeros(4, dtype=torch.int64, device=dev)
+    smoe._C.call("smoe_selftest_quant", counts.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    bad_div, n_div, bad_enc, n_enc = counts.cpu().tolist()
+    assert n_div == sum(2 * (a + 1) for a in range(1, 0x7f80))
+    assert n_enc == 2 * (0x43e00000 + 1)
+    assert bad_div == 0 and bad_enc == 0
 
 
 @pytest.mark.parametrize("T,H,E,K,outl", [(2048, 1024, 8, 2, False), (1024, 7168, 256, 8, True),
