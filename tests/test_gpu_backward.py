@@ -86,6 +86,50 @@ def test_quant_cols_bit_exact(dev, counts, C):
     assert np.array_equal(s.cpu().numpy()[:, :Rp // 128], rs)
 
 
+def _special_values(R, C, seed):
+    """bf16 matrix mixing the values the fast quantiser treats specially:
+    all-zero columns and rows (s = 1), -0.0, denormals (alone and next to
+    normals), values near the bf16 maximum, and an all-denormal column."""
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((R, C)) * np.exp2(rng.integers(-30, 30, (R, C)))).astype(np.float32)
+    x[:, 0] = 0.0
+    x[:, 1] = -0.0
+    x[:, 2] = rng.choice([1e-39, -3e-40, 5e-41, 0.0], R)       # all denormal / zero
+    x[:, 3] = rng.choice([3.0e38, -2.9e38, 1.0, -1e-39], R)    # huge next to tiny
+    x[: R // 2, 4] = 1e-40
+    x[3, :] = 0.0
+    x[5, :] = -0.0
+    return O.f32_to_bf16(x)
+
+
+@pytest.mark.parametrize("counts,C", [([200, 57], 256), ([129], 384)])
+def test_quant_cols_special_values(dev, counts, C):
+    say("quant_cols special values", counts, C)
+    off = _offsets(counts)
+    R = int(off[-1])
+    xb = _special_values(R, C, R + C)
+    q, s, pad, ld = ops.quant_cols(torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16).to(dev),
+                                   torch.from_numpy(off).to(dev))
+    rq, rs, rpad = O.quant_cols_128x1(O.bf16_to_f32(xb), off)
+    Rp = int(rpad[-1])
+    assert np.array_equal(u8(q)[:, :Rp], rq)
+    assert np.array_equal(s.cpu().numpy()[:, :Rp // 128].view(np.uint32), rs.view(np.uint32))
+
+
+def test_quant_rows_and_weights_special_values(dev):
+    say("quant_rows / weight quant special values")
+    xb = _special_values(256, 512, 7)
+    xt = torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16).to(dev)
+    q, s = ops.quant_rows(xt)
+    rq, rs = O.quant_1x128(O.bf16_to_f32(xb))
+    assert np.array_equal(u8(q), rq)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), rs.view(np.uint32))
+    wq, ws = ops.quantize_weight_blockwise(xt.reshape(2, 128, 512))
+    rwq, rws = O.quantize_weight_blockwise(xb.reshape(2, 128, 512))
+    assert np.array_equal(u8(wq), rwq)
+    assert np.array_equal(ws.cpu().numpy().view(np.uint32), rws.view(np.uint32))
+
+
 def test_quant_cols_gather_bit_exact(dev):
     say("quant_cols gather")
     rng = np.random.default_rng(3)
