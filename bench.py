@@ -10,8 +10,9 @@ HBM.  ``value`` is the algorithmic HBM traffic of that step
 Also reported on the same line:
   roofline      the dominant kernel (permute_quant) timed alone with HIP
                 events on the launch stream, algorithmic bytes / duration;
-  cpu_baseline  the numpy oracle (route sort + permute-quantise) on a bounded
-                sample of the same workload, on this host's cores;
+  cpu_baseline  the PyTorch-CPU restatement of the same dispatch step
+                (oracle/cpu_torch.py) on a bounded sample of the same
+                workload, multi-threaded on this host's CPU share;
   extra         fp8 grouped GEMM TFLOPS on benchmark config 4 (DeepSeek-V3
                 local experts, Zipf loads, fc1 + fc2), the combine GB/s at
                 config-2 size, the whole SimpleMoE forward of config 3 and the
@@ -67,25 +68,33 @@ def permute_kernel_bytes(T, H, K):
 
 
 def cpu_baseline(c, budget_s=12.0):
+    """The dispatch step on the host: the PyTorch-CPU restatement of route
+    sort + permute + 1x128 quantisation (oracle/cpu_torch.py, byte-identical
+    to the numpy oracle), multi-threaded on this host's CPU share, on a
+    bounded sample of the config-2 tokens."""
     import numpy as np
-    from oracle import smoe_oracle as O
+    import torch
+    from oracle import cpu_torch, smoe_oracle as O
     from smoe import workloads as W
-    Ts = 1024
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    torch.set_num_threads(threads)
+    Ts = 4096
     x = W.tokens(Ts, c.H, outliers=True)
-    xn = x.view(__import__("torch").int16).numpy().view(np.uint16)
-    idx = O.router_topk(W.logits(Ts, c.E).numpy(), c.K, W.router_bias(c.E).numpy())[0]
+    idx = torch.from_numpy(O.router_topk(W.logits(Ts, c.E).numpy(), c.K,
+                                         W.router_bias(c.E).numpy())[0])
+    cpu_torch.dispatch_quant(x, idx, c.E)  # warm-up
     times = []
     t_end = time.time() + budget_s
-    while time.time() < t_end or not times:
+    while time.time() < t_end or len(times) < 3:
         t0 = time.perf_counter()
-        _, inv, _, _ = O.route_sort(idx, c.E)
-        O.permute_quant(xn, inv, c.K)
+        cpu_torch.dispatch_quant(x, idx, c.E)
         times.append(time.perf_counter() - t0)
     t = float(np.median(times))
     gbs = dispatch_bytes(Ts, c.H, c.E, c.K) / t / 1e9
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"numpy oracle route_sort+permute_quant on {Ts} of {c.T} tokens "
-                      f"(H={c.H}, E={c.E}, top-{c.K}), median of {len(times)} runs, "
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"PyTorch-CPU route sort + permute + 1x128 quantisation (oracle/cpu_torch.py, "
+                      f"byte-identical to the oracle) on {Ts} of {c.T} tokens (H={c.H}, E={c.E}, "
+                      f"top-{c.K}), {threads} threads, median of {len(times)} runs, "
                       f"{t * 1e3:.1f} ms each"}
 
 

@@ -400,3 +400,26 @@ def test_moe_backward_against_float64_autograd():
     assert rel(b["dW1"], W1.grad.numpy()) < 0.1
     assert rel(b["dW2"], W2.grad.numpy()) < 0.1
     assert rel(b["dw"], wts.grad.numpy()) < 0.08
+
+
+def test_cpu_torch_dispatch_matches_oracle():
+    """The multi-threaded PyTorch-CPU dispatch that bench.py times as its CPU
+    baseline computes exactly the oracle's sort, maps and fp8 bytes/scales."""
+    from oracle import cpu_torch
+    rng = np.random.default_rng(11)
+    for T, H, E, K in ((512, 1024, 64, 8), (97, 384, 5, 3), (1, 128, 1, 1)):
+        x = (rng.standard_normal((T, H)) * np.exp2(rng.integers(-8, 8, (T, H)))).astype(np.float32)
+        x[0, :128] = 0.0
+        if T > 2:
+            x[1, 5] = 3.0e38
+            x[2, :] = 1e-40
+        xb = O.f32_to_bf16(x)
+        idx = rng.integers(0, E, (T, K)).astype(np.int32)
+        xt = torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16)
+        xq, xs, rm, im, cnt, off = cpu_torch.dispatch_quant(xt, torch.from_numpy(idx), E)
+        r_rm, r_im, r_cnt, r_off = O.route_sort(idx, E)
+        rq, rs = O.permute_quant(xb, r_im, K)
+        assert np.array_equal(rm.numpy(), r_rm) and np.array_equal(im.numpy(), r_im)
+        assert np.array_equal(cnt.numpy(), r_cnt) and np.array_equal(off.numpy(), r_off)
+        assert np.array_equal(xq.numpy(), rq)
+        assert np.array_equal(xs.numpy().view(np.uint32), rs.view(np.uint32))
