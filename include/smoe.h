@@ -121,9 +121,12 @@ int smoe_quantize_weight_blockwise(const uint16_t* w, int E, int N, int Kdim, ui
  * exhaustively: (1) the bytes of the bf16 path for every finite bf16 x and
  * every positive finite bf16 amax >= |x| (s = amax / 448), about 1.07e9
  * pairs; (2) the hardware encoder for every fp32 with |v| <= 448, about
- * 2.28e9 values.  counts [4] u64 on the device, zeroed by the caller,
- * receives: mismatches (1), pairs checked (1), mismatches (2), values
- * checked (2).
+ * 2.28e9 values; (3) the hardware fp32 -> bf16 conversion the kernels
+ * use for bf16 outputs, against the software RNE rule, for every fp32 bit
+ * pattern (NaN only needs to stay a NaN of the same sign).  counts [6] u64
+ * on the device, zeroed by the caller, receives: mismatches (1), pairs
+ * checked (1), mismatches (2), values checked (2), mismatches (3), values
+ * checked (3).
  */
 int smoe_selftest_quant(unsigned long long* counts, void* stream);
 

@@ -184,7 +184,7 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(const uint16_t* __restr
     uint32_t og[4], ou[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      uint32_t gb[2], ub[2];
+      float gb[2], ub[2];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const float g = h ? __uint_as_float(g4[i] & 0xffff0000u) : __uint_as_float(g4[i] << 16);
@@ -193,11 +193,11 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(const uint16_t* __restr
         const float s = 1.0f / (1.0f + expf32(-g));
         const float silu = g * s;
         const float ds = s * (1.0f + g * (1.0f - s));
-        ub[h] = f32_to_bf16(d * silu);
-        gb[h] = f32_to_bf16((d * u) * ds);
+        ub[h] = d * silu;
+        gb[h] = (d * u) * ds;
       }
-      og[i] = gb[0] | (gb[1] << 16);
-      ou[i] = ub[0] | (ub[1] << 16);
+      og[i] = bf16_pack2(gb[0], gb[1]);
+      ou[i] = bf16_pack2(ub[0], ub[1]);
     }
     uint16_t* orow = dc1 + (size_t)r * 2 * I;
     *(uint4*)(orow + col) = make_uint4(og[0], og[1], og[2], og[3]);
@@ -254,7 +254,7 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(
         const float y1 = __uint_as_float(y4[i] & 0xffff0000u);
         part[k] = part[k] + d[2 * i] * y0;
         part[k] = part[k] + d[2 * i + 1] * y1;
-        o[i] = f32_to_bf16(wk[k] * d[2 * i]) | (f32_to_bf16(wk[k] * d[2 * i + 1]) << 16);
+        o[i] = bf16_pack2(wk[k] * d[2 * i], wk[k] * d[2 * i + 1]);
       }
       *(uint4*)(dy + (size_t)r[k] * H + col) = make_uint4(o[0], o[1], o[2], o[3]);
     }

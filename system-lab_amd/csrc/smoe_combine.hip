@@ -74,10 +74,10 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
         }
       }
       v4u ov;
-      ov.x = f32_to_bf16(acc[0]) | (f32_to_bf16(acc[1]) << 16);
-      ov.y = f32_to_bf16(acc[2]) | (f32_to_bf16(acc[3]) << 16);
-      ov.z = f32_to_bf16(acc[4]) | (f32_to_bf16(acc[5]) << 16);
-      ov.w = f32_to_bf16(acc[6]) | (f32_to_bf16(acc[7]) << 16);
+      ov.x = bf16_pack2(acc[0], acc[1]);
+      ov.y = bf16_pack2(acc[2], acc[3]);
+      ov.z = bf16_pack2(acc[4], acc[5]);
+      ov.w = bf16_pack2(acc[6], acc[7]);
       __builtin_nontemporal_store(ov, (v4u*)(out + (size_t)t * H + col));
     }
   }

@@ -23,11 +23,22 @@ __device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
   return __uint_as_float(bits16 << 16);
 }
 
-// Round-to-nearest-even fp32 -> bf16 bits; NaN stays a quiet NaN.
+// Round-to-nearest-even fp32 -> bf16 bits; NaN stays a quiet NaN.  The
+// software statement of the rule: kernels use bf16_pack2 below.
 __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
   uint32_t u = __float_as_uint(f);
   if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
   return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+// Two fp32 -> packed bf16 bits (lo in bits 0-15, hi in 16-31) with gfx950's
+// conversion instruction (v_cvt_pk_bf16_f32, round to nearest even): one
+// instruction per pair where f32_to_bf16's NaN test costs a branch per value.
+// smoe_selftest_quant checks it against f32_to_bf16 for every fp32 pattern.
+typedef __bf16 bf16x2_hw __attribute__((ext_vector_type(2)));
+typedef float f32x2_hw __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t bf16_pack2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_hw{lo, hi}, bf16x2_hw));
 }
 
 // ---------------------------------------------------------------- e4m3 ----

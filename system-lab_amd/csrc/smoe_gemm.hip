@@ -305,8 +305,8 @@ __global__ __launch_bounds__(C::kThreads, 1) void grouped_gemm_fp8_kernel(
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       uint2 o;
-      o.x = f32_to_bf16(acc[i][j][0]) | (f32_to_bf16(acc[i][j][1]) << 16);
-      o.y = f32_to_bf16(acc[i][j][2]) | (f32_to_bf16(acc[i][j][3]) << 16);
+      o.x = bf16_pack2(acc[i][j][0], acc[i][j][1]);
+      o.y = bf16_pack2(acc[i][j][2], acc[i][j][3]);
       *(uint2*)(ct + rl * kCPitch + (cl + j * 16) * 2) = o;
     }
   }

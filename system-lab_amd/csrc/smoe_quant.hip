@@ -124,7 +124,7 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const uint16_t* __res
       if (kSaveH && g < G) {
         uint32_t w[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) w[i] = f32_to_bf16(h[2 * i]) | (f32_to_bf16(h[2 * i + 1]) << 16);
+        for (int i = 0; i < 8; ++i) w[i] = bf16_pack2(h[2 * i], h[2 * i + 1]);
         uint16_t* hp = hb + (size_t)r * I + g * kGroup + sub * 16;
         *(uint4*)hp = make_uint4(w[0], w[1], w[2], w[3]);
         *(uint4*)(hp + 8) = make_uint4(w[4], w[5], w[6], w[7]);
@@ -239,6 +239,37 @@ __global__ __launch_bounds__(256) void selftest_e4m3_kernel(unsigned long long* 
   }
 }
 
+// (3) For every fp32 bit pattern: the hardware bf16 conversion (bf16_pack2)
+// against f32_to_bf16, in both halves of the pair.  Non-NaN values must give
+// the same bits; a NaN must stay a NaN of the same sign.  counts[4] gets the
+// mismatches, counts[5] the values checked.
+__device__ __forceinline__ bool bf16_same(float v, uint32_t hw) {
+  const uint32_t sw = f32_to_bf16(v);
+  if (v != v) return (hw & 0x7fffu) > 0x7f80u && (hw & 0x8000u) == (sw & 0x8000u);
+  return hw == sw;
+}
+__global__ __launch_bounds__(256) void selftest_bf16_kernel(unsigned long long* __restrict__ counts) {
+  unsigned long long bad = 0, n = 0;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i <= 0xffffffffull;
+       i += (uint64_t)gridDim.x * blockDim.x) {
+    const float v = __uint_as_float((uint32_t)i);
+    // partner for the other half: a different pattern on every lane
+    const float w = __uint_as_float((uint32_t)i ^ 0x9e3779b9u);
+    const uint32_t p = bf16_pack2(v, w);
+    bad += !bf16_same(v, p & 0xffffu);
+    bad += !bf16_same(w, p >> 16);
+    n += 2;
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    bad += __shfl_xor(bad, o, kWave);
+    n += __shfl_xor(n, o, kWave);
+  }
+  if ((threadIdx.x & 63) == 0) {
+    atomicAdd(&counts[4], bad);
+    atomicAdd(&counts[5], n);
+  }
+}
+
 }  // namespace smoe
 
 using namespace smoe;
@@ -249,6 +280,7 @@ extern "C" int smoe_selftest_quant(unsigned long long* counts, void* stream) {
   hipStream_t st = (hipStream_t)stream;
   selftest_quant_bf16_kernel<<<dim3(64, 0x7f7f), dim3(256), 0, st>>>(counts);
   selftest_e4m3_kernel<<<dim3(4096), dim3(256), 0, st>>>(counts);
+  selftest_bf16_kernel<<<dim3(8192), dim3(256), 0, st>>>(counts);
   SMOE_RETURN_LAUNCH();
 }
 

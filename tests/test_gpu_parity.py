@@ -144,14 +144,18 @@ def test_fast_quantiser_exhaustive(dev):
     conversion instead of the software RNE encoder.  The library's self-test
     compares both with the reference rule exhaustively: every finite bf16 x
     against every positive finite bf16 amax >= |x| (s = amax / 448), and every
-    fp32 with |v| <= 448 through the encoder."""
+    fp32 with |v| <= 448 through the encoder.  The bf16 outputs (GEMM
+    epilogue, combine, SwiGLU h, backward) use the hardware fp32 -> bf16
+    conversion, checked against the software RNE rule for all 2^32 fp32
+    patterns."""
     say("fast quantiser exhaustive")
-    counts = torch.zeros(4, dtype=torch.int64, device=dev)
+    counts = torch.zeros(6, dtype=torch.int64, device=dev)
     smoe._C.call("smoe_selftest_quant", counts.data_ptr(), torch.cuda.current_stream().cuda_stream)
-    bad_div, n_div, bad_enc, n_enc = counts.cpu().tolist()
+    bad_div, n_div, bad_enc, n_enc, bad_bf, n_bf = counts.cpu().tolist()
     assert n_div == sum(2 * (a + 1) for a in range(1, 0x7f80))
     assert n_enc == 2 * (0x43e00000 + 1)
-    assert bad_div == 0 and bad_enc == 0
+    assert n_bf == 2 * 2**32
+    assert bad_div == 0 and bad_enc == 0 and bad_bf == 0
 
 
 @pytest.mark.parametrize("T,H,E,K,outl", [(2048, 1024, 8, 2, False), (1024, 7168, 256, 8, True),
