@@ -58,6 +58,32 @@ def timed(fn, iters, warmup):
     return s.elapsed_time(e) / iters
 
 
+def timed_cold(fn, iters=20, warmup=5, flush_mib=1024):
+    """Median ms of ``iters`` single calls, each timed by its own HIP events
+    after a ``flush_mib`` MiB device read (larger than L2 plus the 256 MiB
+    last-level cache), so no call finds its inputs cached.  The flush reads
+    rather than writes: a write leaves dirty lines whose write-back would be
+    charged to the timed call."""
+    import numpy as np
+    import torch
+    flush = torch.ones(flush_mib << 18, dtype=torch.int32, device="cuda")
+    for _ in range(warmup):
+        flush.max()
+        fn()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    times = []
+    for _ in range(iters):
+        flush.max()
+        torch.cuda.synchronize()
+        s.record()
+        fn()
+        e.record()
+        torch.cuda.synchronize()
+        times.append(s.elapsed_time(e))
+    del flush
+    return float(np.median(times))
+
+
 def dispatch_bytes(T, H, E, K):
     return T * H * 2 + T * K * H + T * K * (H // 128) * 4 + T * K * 4 + T * K * 8 + (E + 1) * 4
 
@@ -148,11 +174,14 @@ def bench_combine(dev, c, steps, warmup):
     w = torch.rand((c.T, c.K), generator=g, device=dev)
     out = torch.empty((c.T, c.H), dtype=torch.bfloat16, device=dev)
     t = timed(lambda: ops.unpermute_combine(y, inv, w, out=out), steps, warmup)
+    tf = timed_cold(lambda: ops.unpermute_combine(y, inv, w, out=out))
     nb = R * c.H * 2 + R * 8 + c.T * c.H * 2
     del y, out
     torch.cuda.empty_cache()
     return {"ms": round(t, 4), "gbs": round(nb / (t * 1e-3) / 1e9, 1),
-            "roofline_frac": round(nb / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+            "roofline_frac": round(nb / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "ms_cold_median": round(tf, 4),
+            "gbs_cold_median": round(nb / (tf * 1e-3) / 1e9, 1)}
 
 
 def bench_layer(dev, steps, warmup):
@@ -293,13 +322,16 @@ def main():
     log(f"dispatch step {ms:.4f} ms  {value:.1f} GB/s")
 
     pk_ms = timed(permute_only, args.steps, 2)
+    pk_cold = timed_cold(permute_only)
     pk_bytes = permute_kernel_bytes(c.T, c.H, c.K)
     pk_gbs = pk_bytes / (pk_ms * 1e-3) / 1e9
     log(f"permute_quant kernel {pk_ms:.4f} ms  {pk_gbs:.1f} GB/s")
     roof = {"kernel": "smoe::permute_quant_kernel<4, true>", "bound": "hbm", "achieved": round(pk_gbs, 1),
             "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(pk_gbs / HBM_PEAK_GBS, 4),
             "traffic": PERMUTE_TRAFFIC_BYTES, "kernel_ms": round(pk_ms, 4),
-            "bytes_per_launch": pk_bytes}
+            "bytes_per_launch": pk_bytes,
+            "kernel_ms_cold_median": round(pk_cold, 4),
+            "frac_cold_median": round(pk_bytes / (pk_cold * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     del x, xq, xs
     torch.cuda.empty_cache()
 
