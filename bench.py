@@ -124,7 +124,40 @@ def cpu_baseline(c, budget_s=12.0):
                       f"{t * 1e3:.1f} ms each"}
 
 
-def bench_gemm(dev, steps, warmup):
+def cpu_gemm_baseline(xq, xs, w1q, w1s, c, rows=1024, experts=2, budget_s=8.0):
+    """The grouped GEMM on the host: fp32 dequantise + matmul per expert
+    (oracle/cpu_torch.py, within the GEMM tolerance of the float64 oracle),
+    multi-threaded, on a bounded sample of the config-4 fc1 shape: ``experts``
+    experts of ``rows`` rows each, K = H, N = 2I.  TFLOP/s counts the matmul
+    FLOP only; the time includes the dequantisation."""
+    import numpy as np
+    import torch
+    from oracle import cpu_torch
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    torch.set_num_threads(threads)
+    R = rows * experts
+    a = xq[:R].view(torch.uint8).cpu()
+    a_s = xs[:R].cpu()
+    w = w1q[:experts].view(torch.uint8).cpu()
+    w_s = w1s[:experts].cpu()
+    off = [i * rows for i in range(experts + 1)]
+    flop = 2.0 * R * w.shape[1] * w.shape[2]
+    cpu_torch.grouped_gemm_fp8(a, a_s, w, w_s, off)  # warm-up
+    times = []
+    t_end = time.time() + budget_s
+    while time.time() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        cpu_torch.grouped_gemm_fp8(a, a_s, w, w_s, off)
+        times.append(time.perf_counter() - t0)
+    t = float(np.median(times))
+    return {"value": round(flop / t / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"PyTorch-CPU fp32 dequantise + matmul (oracle/cpu_torch.py) on {experts} experts "
+                      f"x {rows} rows of the config-4 fc1 shape (K={c.H}, N={2 * c.I}), {flop:.3e} "
+                      f"FLOP per run, {threads} threads, median of {len(times)} runs, "
+                      f"{t * 1e3:.0f} ms each"}
+
+
+def bench_gemm(dev, steps, warmup, skip_cpu=True):
     import torch
     from smoe import ops, workloads as W
     c = W.CONFIGS["dsv3"]
@@ -158,6 +191,8 @@ def bench_gemm(dev, steps, warmup):
            "fc1_swiglu_fused_ms": round(t1s, 4), "fc1_then_swiglu_ms": round(t1 + t_sw, 4),
            "tflops": round(tf, 1), "roofline_frac": round(tf / FP8_PEAK_TFLOPS, 4),
            "peak_tflops": FP8_PEAK_TFLOPS}
+    if not skip_cpu:
+        out["cpu_baseline"] = cpu_gemm_baseline(xq, xs, w1q, w1s, c)
     del xq, xs, hq, hs, w1q, w1s, w2q, w2s, c1, y
     torch.cuda.empty_cache()
     return out
@@ -338,7 +373,7 @@ def main():
     extra = {}
     if not args.skip_extra:
         sx = max(5, args.steps // 5)
-        extra["grouped_gemm_fp8"] = bench_gemm(dev, sx, 2)
+        extra["grouped_gemm_fp8"] = bench_gemm(dev, sx, 2, skip_cpu=args.skip_cpu)
         log("gemm", extra["grouped_gemm_fp8"])
         extra["combine_cfg2"] = bench_combine(dev, c, sx, 2)
         log("combine", extra["combine_cfg2"])

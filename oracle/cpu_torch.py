@@ -1,15 +1,18 @@
-"""PyTorch-CPU restatement of the dispatch step — TEST INFRASTRUCTURE ONLY.
+"""PyTorch-CPU restatements of the hot path — TEST INFRASTRUCTURE ONLY.
 
-The CPU baseline that bench.py times next to the GPU path: the same route
-sort + permute + 1x128 quantisation semantics as ``smoe_oracle`` (C2, C3),
-written with vectorised torch CPU ops so that it runs multi-threaded on the
-host's cores.  Only ``tests/`` and bench.py's ``cpu_baseline`` leg use it;
-the product path never does.
+The CPU baselines that bench.py times next to the GPU path, written with
+vectorised torch CPU ops so that they run multi-threaded on the host's cores:
+  * ``dispatch_quant``: route sort + permute + 1x128 quantisation (C2, C3);
+  * ``grouped_gemm_fp8``: the blockwise-scaled grouped GEMM (C5) as fp32
+    dequantise + matmul per expert.
+Only ``tests/`` and bench.py's CPU baseline legs use them; the product path
+never does.
 
-Parity: ``tests/test_oracle.py`` holds it byte-for-byte to the numpy oracle
-(``smoe_oracle.route_sort`` + ``smoe_oracle.permute_quant``).  The e4m3
-encode is torch's own ``float8_e4m3fn`` cast after the +-448 clamp, which is
-the cast the oracle's software encoder is pinned against.
+Parity: ``tests/test_oracle.py`` holds ``dispatch_quant`` byte-for-byte to
+the numpy oracle (``smoe_oracle.route_sort`` + ``smoe_oracle.permute_quant``)
+and ``grouped_gemm_fp8`` to the float64 oracle within the GEMM tolerance.
+The e4m3 encode is torch's own ``float8_e4m3fn`` cast after the +-448 clamp,
+which is the cast the oracle's software encoder is pinned against.
 """
 import torch
 
@@ -43,3 +46,27 @@ def dispatch_quant(x: torch.Tensor, topk_idx: torch.Tensor, num_experts: int):
     tok = row_map // K
     return (q[tok], s[tok], row_map.to(torch.int32), inv_map.to(torch.int32),
             counts.to(torch.int32), offsets.to(torch.int32))
+
+
+def grouped_gemm_fp8(xq: torch.Tensor, xs: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor,
+                     offsets) -> torch.Tensor:
+    """C5 on the CPU: xq [R,K] u8 (e4m3 bytes), xs [R,K/128] f32, wq [E,N,K] u8,
+    ws [E,N/128,K/128] f32, offsets [E+1] -> fp32 [R,N].  Each operand is
+    dequantised to fp32 (value * its block scale) and expert e's rows
+    [offsets[e], offsets[e+1]) are multiplied by W[e]^T with torch.matmul
+    (summary/fp8_expert_gemm_optimization.md:89-95: fp8 dot -> fp32 acc ->
+    dequant; the scales are applied before the product here, which is the
+    same sum up to fp32 rounding)."""
+    R, Kd = xq.shape
+    E, N, _ = wq.shape
+    a = xq.view(torch.float8_e4m3fn).to(torch.float32).view(R, Kd // GROUP, GROUP)
+    a = (a * xs.unsqueeze(2)).view(R, Kd)
+    out = torch.zeros((R, N), dtype=torch.float32)
+    for e in range(E):
+        lo, hi = int(offsets[e]), int(offsets[e + 1])
+        if hi <= lo:
+            continue
+        w = wq[e].view(torch.float8_e4m3fn).to(torch.float32).view(N // GROUP, GROUP, Kd // GROUP, GROUP)
+        w = (w * ws[e][:, None, :, None]).view(N, Kd)
+        out[lo:hi] = a[lo:hi] @ w.T
+    return out
