@@ -80,59 +80,64 @@ __global__ __launch_bounds__(256) void permute_quant_kernel(
 }
 
 // ------------------------------------------------------------ swiglu_quant
-// kSaveH: also write h rounded to bf16 (the fc2 wgrad operand of the
-// backward pass), saving a recompute from c1.
+// Work is a flat list of (row, 128-column group) slots, slot = r * G + g, so
+// every 8-lane group of a wave is busy whatever I is (a row of I = 768 has 6
+// groups, which a wave-per-row mapping would leave 2 of 8 lane groups idle
+// on).  Wave w takes slots w * 8 * kUnroll .. +8 * kUnroll, 8 at a time; all
+// kUnroll batches' loads are issued before any arithmetic.  kSaveH: also
+// write h rounded to bf16 (the fc2 wgrad operand of the backward pass),
+// saving a recompute from c1.
 template <int kUnroll, bool kSaveH>
 __global__ __launch_bounds__(256) void swiglu_quant_kernel(const uint16_t* __restrict__ c1,
-                                                           int R, int I,
+                                                           uint32_t nslots, int I,
                                                            uint8_t* __restrict__ hq,
                                                            float* __restrict__ hs,
                                                            uint16_t* __restrict__ hb) {
   const int lane = threadIdx.x & 63;
-  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (r >= R) return;
-  const int G = I / kGroup;
+  const uint32_t G = (uint32_t)(I / kGroup);
   const int sub = lane & 7, gl = lane >> 3;
-  const uint16_t* gate = c1 + (size_t)r * 2 * I;
-  const uint16_t* up = gate + I;
-  for (int c0 = 0; c0 * 8 < G; c0 += kUnroll) {
-    uint4 vg[kUnroll][2], vu[kUnroll][2];
+  const uint32_t base = (blockIdx.x * 4u + (threadIdx.x >> 6)) * (8u * kUnroll);
+  uint4 vg[kUnroll][2], vu[kUnroll][2];
+  uint32_t rr[kUnroll], gg[kUnroll];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int g = (c0 + u) * 8 + gl;
-      if (g < G) {
-        const int col = g * kGroup + sub * 16;
-        vg[u][0] = *(const uint4*)(gate + col);
-        vg[u][1] = *(const uint4*)(gate + col + 8);
-        vu[u][0] = *(const uint4*)(up + col);
-        vu[u][1] = *(const uint4*)(up + col + 8);
-      } else {
-        vg[u][0] = vg[u][1] = vu[u][0] = vu[u][1] = make_uint4(0, 0, 0, 0);
-      }
+  for (int u = 0; u < kUnroll; ++u) {
+    const uint32_t slot = base + u * 8 + gl;
+    rr[u] = slot / G;
+    gg[u] = slot - rr[u] * G;
+    if (slot < nslots) {
+      const uint16_t* gate = c1 + (size_t)rr[u] * 2 * I + gg[u] * kGroup + sub * 16;
+      const uint16_t* up = gate + I;
+      vg[u][0] = *(const uint4*)gate;
+      vg[u][1] = *(const uint4*)(gate + 8);
+      vu[u][0] = *(const uint4*)up;
+      vu[u][1] = *(const uint4*)(up + 8);
+    } else {
+      vg[u][0] = vg[u][1] = vu[u][0] = vu[u][1] = make_uint4(0, 0, 0, 0);
     }
+  }
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      float fg[16], fu[16], h[16];
-      unpack_bf16x8(vg[u][0], fg);
-      unpack_bf16x8(vg[u][1], fg + 8);
-      unpack_bf16x8(vu[u][0], fu);
-      unpack_bf16x8(vu[u][1], fu + 8);
+  for (int u = 0; u < kUnroll; ++u) {
+    float fg[16], fu[16], h[16];
+    unpack_bf16x8(vg[u][0], fg);
+    unpack_bf16x8(vg[u][1], fg + 8);
+    unpack_bf16x8(vu[u][0], fu);
+    unpack_bf16x8(vu[u][1], fu + 8);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) h[i] = silu32(fg[i]) * fu[i];
-      const Q16 q = quant16(h);
-      const int g = (c0 + u) * 8 + gl;
-      if (kSaveH && g < G) {
+    for (int i = 0; i < 16; ++i) h[i] = silu32(fg[i]) * fu[i];
+    // the 8 lanes of a group share one slot, so the group's amax shuffle
+    // never mixes slots (or a valid slot with padding)
+    const Q16 q = quant16(h);
+    if (base + u * 8 + gl < nslots) {
+      const size_t off = (size_t)rr[u] * I + gg[u] * kGroup + sub * 16;
+      if (kSaveH) {
         uint32_t w[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) w[i] = bf16_pack2(h[2 * i], h[2 * i + 1]);
-        uint16_t* hp = hb + (size_t)r * I + g * kGroup + sub * 16;
-        *(uint4*)hp = make_uint4(w[0], w[1], w[2], w[3]);
-        *(uint4*)(hp + 8) = make_uint4(w[4], w[5], w[6], w[7]);
+        *(uint4*)(hb + off) = make_uint4(w[0], w[1], w[2], w[3]);
+        *(uint4*)(hb + off + 8) = make_uint4(w[4], w[5], w[6], w[7]);
       }
-      if (g < G) {
-        store16<true>(hq + (size_t)r * I + g * kGroup + sub * 16, q.q);
-        if (sub == 0) hs[(size_t)r * G + g] = q.scale;
-      }
+      store16<true>(hq + off, q.q);
+      if (sub == 0) hs[(size_t)rr[u] * G + gg[u]] = q.scale;
     }
   }
 }
@@ -355,18 +360,16 @@ extern "C" int smoe_swiglu_quant_h(const uint16_t* c1, int R, int I, uint8_t* hq
   SMOE_CHECK_PTR(hq);
   SMOE_CHECK_PTR(hs);
   if (h && ((uintptr_t)h & 15u)) return SMOE_EINVAL_PTRALIGN;
-  const int chunks = (I / kGroup + 7) / 8;
-  const dim3 grid((R + 3) / 4), block(256);
+  // slots (row, group) are 32-bit; the grid covers them 32 * kUnroll per block
+  const long long nslots = (long long)R * (I / kGroup);
+  constexpr int kU = 2;
+  if (nslots + 32LL * kU > 0xffffffffLL) return SMOE_EINVAL_DIM;
+  const dim3 grid((unsigned)((nslots + 32 * kU - 1) / (32 * kU))), block(256);
   hipStream_t s = (hipStream_t)stream;
-#define SMOE_SW(U)                                                                        \
-  do {                                                                                    \
-    if (h) swiglu_quant_kernel<U, true><<<grid, block, 0, s>>>(c1, R, I, hq, hs, h);      \
-    else swiglu_quant_kernel<U, false><<<grid, block, 0, s>>>(c1, R, I, hq, hs, nullptr); \
-  } while (0)
-  if (chunks <= 1) SMOE_SW(1);
-  else if (chunks <= 2) SMOE_SW(2);
-  else SMOE_SW(4);
-#undef SMOE_SW
+  if (h)
+    swiglu_quant_kernel<kU, true><<<grid, block, 0, s>>>(c1, (uint32_t)nslots, I, hq, hs, h);
+  else
+    swiglu_quant_kernel<kU, false><<<grid, block, 0, s>>>(c1, (uint32_t)nslots, I, hq, hs, nullptr);
   SMOE_RETURN_LAUNCH();
 }
 
