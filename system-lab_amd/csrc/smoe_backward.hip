@@ -74,8 +74,9 @@ __global__ __launch_bounds__(1024) void pad_offsets_kernel(const int32_t* __rest
 // columns (t % 16) * 8 .. +8 of the 8 consecutive rows (t / 16) * 8 .. +8, so
 // everything stays in registers: the column amax is a local max over the 8
 // rows, an xor shuffle over the 4 row groups of a wave, and a 2 KB LDS
-// exchange over the 4 waves; then each thread quantises its 64 values with
-// the division-free bf16 quantiser and writes, per column, its 8 rows as one
+// exchange over the 4 waves; one thread per column then derives the scale
+// and the quotient set-up for all, and each thread quantises its 64 values
+// with the division-free bf16 quantiser and writes, per column, its 8 rows as one
 // 8-byte store into the transposed output (ld bytes per column).  The 16
 // stores that cover one column's 128 bytes merge in L2.
 constexpr int kQcCols = 128;
@@ -86,6 +87,8 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(
     uint8_t* __restrict__ q, float* __restrict__ s) {
   __shared__ int pad_l[SMOE_MAX_EXPERTS + 1];
   __shared__ float wmax[4][kQcCols];
+  __shared__ float col_m[kQcCols], col_r[kQcCols];  // per-column quotient set-up
+  __shared__ int col_e[kQcCols];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   for (int i = t; i <= E; i += 256) pad_l[i] = pad[i];
   __syncthreads();
@@ -136,13 +139,24 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(
     for (int i = 0; i < 8; ++i) wmax[w][cc + i] = cmax[i];
   }
   __syncthreads();
-  float sc[8];
+  // one thread per column finishes the amax, derives the scale and the
+  // quotient set-up (two IEEE divisions) and shares them: the 16 threads
+  // that hold pieces of a column would otherwise repeat the divisions
+  if (t < kQcCols) {
+    const float sc = group_scale(fmaxf(fmaxf(wmax[0][t], wmax[1][t]), fmaxf(wmax[2][t], wmax[3][t])));
+    const QDiv qd = qdiv_setup(sc);
+    col_m[t] = qd.m;
+    col_r[t] = qd.r;
+    col_e[t] = qd.e;
+    s[(size_t)(c0 + t) * (ld / kGroup) + gpos / kGroup] = sc;
+  }
+  __syncthreads();
   QDiv d[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const int c = cc + i;
-    sc[i] = group_scale(fmaxf(fmaxf(wmax[0][c], wmax[1][c]), fmaxf(wmax[2][c], wmax[3][c])));
-    d[i] = qdiv_setup(sc[i]);
+    d[i].m = col_m[cc + i];
+    d[i].r = col_r[cc + i];
+    d[i].e = col_e[cc + i];
   }
   // column c0+cc+i gets bytes for rows gpos + rg*8 .. +8
   uint8_t* dst = q + (size_t)(c0 + cc) * ld + gpos + rg * 8;
@@ -157,10 +171,6 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(
     const uint32_t b[2] = {e4m3_pack4(qv[0], qv[1], qv[2], qv[3]),
                            e4m3_pack4(qv[4], qv[5], qv[6], qv[7])};
     *(uint2*)(dst + (size_t)i * ld) = make_uint2(b[0], b[1]);
-  }
-  if (rg == 0) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) s[(size_t)(c0 + cc + i) * (ld / kGroup) + gpos / kGroup] = sc[i];
   }
 }
 
