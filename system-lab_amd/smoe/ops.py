@@ -34,6 +34,10 @@ def _check(t: torch.Tensor, name: str, dtypes, ndim: int | None = None) -> None:
         raise TypeError(f"{name} must be a tensor")
     if t.device.type != "cuda":
         raise ValueError(f"{name} must be a GPU tensor (got {t.device}); the HIP kernels are the only path")
+    if t.device.index != torch.cuda.current_device():
+        # kernels launch on the current device's stream with raw pointers
+        raise ValueError(f"{name} is on {t.device} but the current device is "
+                         f"cuda:{torch.cuda.current_device()}")
     if t.dtype not in dtypes:
         raise TypeError(f"{name} has dtype {t.dtype}, expected one of {dtypes}")
     if ndim is not None and t.dim() != ndim:
