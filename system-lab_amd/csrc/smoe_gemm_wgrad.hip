@@ -13,7 +13,8 @@
 // one MFMA per 128-row group.  aT rows feed the MFMA's A operand and bT rows its B
 // operand, so an output lane holds one k (lane % 16) and four consecutive n.
 // Both scales vary per row and group, so each partial is multiplied by
-// sa[n,g]*sb[k,g] before accumulation.  Operands and both scale vectors of a
+// sa[n,g]*sb[k,g] before accumulation (the product is formed before the
+// MFMA result arrives, leaving one FMA per output after it).  Operands and both scale vectors of a
 // group are staged by direct global->LDS DMA, two stages deep, as in the
 // forward grouped GEMM.
 #include "smoe_mfma.h"
@@ -103,18 +104,32 @@ __global__ __launch_bounds__(kWThreads, 1) void grouped_gemm_fp8_wgrad_kernel(
       fa[j] = lds_frag(sA, wn * 64 + j * 16 + frow, fch);
       sa[j] = *(const v4f*)(sSa + wn * 64 + j * 16 + (lane >> 4) * 4);
     }
+    // the next row block's fragment and scale are read before this block's
+    // MFMAs are issued, so their LDS latency hides behind them
+    const int kr0 = wk * 128 + frow;
+    v8i fb = lds_frag(sB, kr0, fch);
+    float sb = sSb[kr0];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const int kr = wk * 128 + i * 16 + frow;
-      const v8i fb = lds_frag(sB, kr, fch);
-      const float sb = sSb[kr];
+      v8i fbn = fb;
+      float sbn = sb;
+      if (i + 1 < 8) {
+        fbn = lds_frag(sB, kr0 + (i + 1) * 16, fch);
+        sbn = sSb[kr0 + (i + 1) * 16];
+      }
+      // the scale products do not depend on the MFMA results: computing them
+      // first leaves one FMA per output after each MFMA
+      v4f sab[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sab[j] = sa[j] * sb;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const v4f p = mfma16(fa[j], fb, v4f{0.0f, 0.0f, 0.0f, 0.0f});
 #pragma unroll
-        for (int v = 0; v < 4; ++v)
-          acc[i][j][v] = __builtin_fmaf(p[v] * sa[j][v], sb, acc[i][j][v]);
+        for (int v = 0; v < 4; ++v) acc[i][j][v] = __builtin_fmaf(p[v], sab[j][v], acc[i][j][v]);
       }
+      fb = fbn;
+      sb = sbn;
     }
     __builtin_amdgcn_s_waitcnt(0);
     __builtin_amdgcn_s_barrier();
