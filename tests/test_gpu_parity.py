@@ -310,6 +310,38 @@ def test_gemm_skewed_experts(dev, counts, N, Kd):
     gemm_close(got, O.grouped_gemm_fp8(xq, xs, wq, ws, off), f"{counts}")
 
 
+def test_gemm_max_experts(dev):
+    """E = 1024 (the maximum): the per-workgroup expert scan covers two
+    experts per thread, many experts own no rows, the rest own 1..300."""
+    say("gemm 1024 experts")
+    rng = np.random.default_rng(1024)
+    E, N, Kd = 1024, 256, 256
+    counts = rng.integers(0, 40, E)
+    counts[rng.choice(E, 300, replace=False)] = 0
+    counts[5], counts[1023] = 300, 1
+    R = int(counts.sum())
+    xq, xs, wq, ws = _fp8_operands(rng, R, N, Kd, E)
+    off = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    got = _run_gemm(dev, xq, xs, wq, ws, off)
+    gemm_close(got, O.grouped_gemm_fp8(xq, xs, wq, ws, off), "E=1024")
+
+
+def test_gemm_max_kdim(dev):
+    """Kdim = 65536 (the maximum): 512 K blocks, so the tile's weight-scale
+    table in LDS is at its largest."""
+    say("gemm Kdim 65536")
+    rng = np.random.default_rng(65536)
+    counts = [3, 130]
+    E, N, Kd = len(counts), 256, 65536
+    R = sum(counts)
+    xq, xs, wq, ws = _fp8_operands(rng, R, N, Kd, E)
+    xs = (rng.random(xs.shape) + 0.5).astype(np.float32)
+    ws = (rng.random(ws.shape) + 0.5).astype(np.float32)
+    off = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    got = _run_gemm(dev, xq, xs, wq, ws, off)
+    gemm_close(got, O.grouped_gemm_fp8(xq, xs, wq, ws, off), "Kdim=65536")
+
+
 def test_gemm_dsv3_shape_sampled_rows(dev):
     """Benchmark config 4 at full size (R=65536, 32 experts, Zipf loads with
     zero-token experts, fc1 N=4096 K=7168 and fc2 N=7168 K=2048); the oracle
@@ -357,7 +389,8 @@ def test_swiglu_quant_bit_exact(dev, R, I):
 
 
 # --------------------------------------------------------------- combine
-@pytest.mark.parametrize("T,K,H", [(2048, 2, 1024), (1000, 8, 7168), (3, 1, 128), (17, 5, 1152)])
+@pytest.mark.parametrize("T,K,H", [(2048, 2, 1024), (1000, 8, 7168), (3, 1, 128), (17, 5, 1152),
+                                   (200, 16, 256), (77, 32, 384)])
 def test_combine_bit_exact(dev, T, K, H):
     say("combine", T, K, H)
     rng = np.random.default_rng(T * K + H)
