@@ -90,3 +90,35 @@ def test_forward_backward_graph_replays(dev):
         for name, got, want in zip(("out", "dx", "dw1", "dw2", "dtopk_w"), outs, ref):
             assert torch.equal(got.view(torch.uint8), want.view(torch.uint8)), \
                 f"replay {i}: {name} differs from the eager step"
+
+
+def test_two_streams_concurrent(dev):
+    """Calls on two streams at once (each with its own buffers and sort
+    workspace) give the same bytes as the same calls run one after the
+    other."""
+    say("two streams")
+    from smoe import ops
+    c = W.CONFIGS["tiny"]
+    m = _layer(dev, c)
+    w1q, w1s, _, _ = m.fp8_weights()
+    xs_ = [W.tokens(c.T, c.H, seed=s).to(dev) for s in (1, 2)]
+    idx = [ops.router_topk(W.logits(c.T, c.E, seed=s).to(dev), c.K)[0] for s in (3, 4)]
+
+    def work(i):
+        xq, xsc, rm, im, cnt, off = ops.permute_quant(xs_[i], idx[i], c.E)
+        return xq, xsc, rm, ops.grouped_gemm_fp8(xq, xsc, w1q, w1s, off)
+
+    serial = [[t.clone() for t in work(i)] for i in (0, 1)]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]  # default priority
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    res = [None, None]
+    for rep in range(3):
+        for i, s in enumerate(streams):
+            with torch.cuda.stream(s):
+                res[i] = work(i)
+        torch.cuda.synchronize()
+        for i in (0, 1):
+            for got, want in zip(res[i], serial[i]):
+                assert torch.equal(got.view(torch.uint8), want.view(torch.uint8)), f"stream {i} rep {rep}"
