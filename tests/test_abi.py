@@ -88,3 +88,53 @@ def test_ops_refuse_cpu_tensors():
     from smoe import ops
     with pytest.raises(ValueError, match="GPU tensor"):
         ops.router_topk(torch.zeros(4, 8), 2)
+
+
+def test_remaining_entry_points_reject():
+    """Every other entry point returns its documented code on the host for
+    malformed arguments (the checks run before any HIP call)."""
+    lib = _C.lib()
+    # fused fc1 + SwiGLU: I % 128, experts, 2*I*Kdim >= 2^31, hs NULL, misaligned c1
+    f = lib.smoe_grouped_gemm_fp8_swiglu
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 100, 192, 256, FAKE, FAKE, None, None) == -3
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 0, 100, 256, 256, FAKE, FAKE, None, None) == -4
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 100, 131072, 8192, FAKE, FAKE, None, None) == -2
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 100, 256, 256, FAKE, None, None, None) == -1
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 100, 256, 256, FAKE, FAKE, MIS, None) == -6
+    # dispatch: H % 128, T == 0, sort workspace missing
+    d = lib.smoe_dispatch_quant
+    assert d(FAKE, FAKE, 16, 200, 2, 8, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 1 << 20, None) == -3
+    assert d(FAKE, FAKE, 0, 256, 2, 8, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 1 << 20, None) == -2
+    assert d(FAKE, FAKE, 16, 256, 2, 8, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None, 0, None) == -5
+    # column quantiser: C % 128, experts, ld too small, gather_div, offsets NULL
+    q = lib.smoe_quant_cols_128x1
+    ld = lib.smoe_quant_cols_ld(1000, 4)
+    assert ld >= 1000 and ld % 128 == 0
+    assert q(FAKE, None, 1, 1000, 100, FAKE, 4, ld, FAKE, FAKE, FAKE, None) == -3
+    assert q(FAKE, None, 1, 1000, 128, FAKE, 0, ld, FAKE, FAKE, FAKE, None) == -4
+    assert q(FAKE, None, 1, 1000, 128, FAKE, 4, ld - 128, FAKE, FAKE, FAKE, None) == -2
+    assert q(FAKE, FAKE, 0, 1000, 128, FAKE, 4, ld, FAKE, FAKE, FAKE, None) == -2
+    assert q(FAKE, None, 1, 1000, 128, None, 4, ld, FAKE, FAKE, FAKE, None) == -1
+    # wgrad: N % 128, experts, ld <= 0, pad NULL
+    w = lib.smoe_grouped_gemm_fp8_wgrad
+    assert w(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 100, 256, 1024, FAKE, None) == -3
+    assert w(FAKE, FAKE, FAKE, FAKE, FAKE, 0, 256, 256, 1024, FAKE, None) == -4
+    assert w(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 256, 256, 0, FAKE, None) == -2
+    assert w(FAKE, FAKE, FAKE, FAKE, None, 4, 256, 256, 1024, FAKE, None) == -1
+    # SwiGLU backward, combine backward, transpose, row quantiser
+    assert lib.smoe_swiglu_bwd(FAKE, FAKE, 10, 100, FAKE, None) == -3
+    assert lib.smoe_swiglu_bwd(FAKE, FAKE, 0, 128, FAKE, None) == -2
+    cb = lib.smoe_unpermute_combine_bwd
+    assert cb(FAKE, FAKE, FAKE, FAKE, 4, 2, 130, FAKE, FAKE, None) == -3
+    assert cb(FAKE, FAKE, FAKE, FAKE, 4, 33, 128, FAKE, FAKE, None) == -7
+    assert cb(FAKE, FAKE, FAKE, None, 4, 2, 128, FAKE, FAKE, None) == -1
+    t = lib.smoe_transpose_blockwise_fp8
+    assert t(FAKE, FAKE, 2, 100, 128, FAKE, FAKE, None) == -3
+    assert t(FAKE, FAKE, 0, 128, 128, FAKE, FAKE, None) == -4
+    assert t(FAKE, None, 2, 128, 128, FAKE, FAKE, None) == -1
+    assert lib.smoe_quant_rows_1x128(FAKE, 10, 100, FAKE, FAKE, None) == -3
+    assert lib.smoe_quant_rows_1x128(FAKE, 0, 128, FAKE, FAKE, None) == -2
+    # SwiGLU with the bf16 h output: misaligned h; the quantiser self-test
+    assert lib.smoe_swiglu_quant_h(FAKE, 10, 128, FAKE, FAKE, MIS, None) == -6
+    assert lib.smoe_selftest_quant(None, None) == -1
+    assert lib.smoe_selftest_quant(MIS, None) == -6
