@@ -377,9 +377,9 @@ def main():
         log("gemm", extra["grouped_gemm_fp8"])
         extra["combine_cfg2"] = bench_combine(dev, c, sx, 2)
         log("combine", extra["combine_cfg2"])
-        extra["layer_mixtral"] = bench_layer(dev, 3, 1)
+        extra["layer_mixtral"] = bench_layer(dev, 10, 3)
         log("layer", extra["layer_mixtral"])
-        extra["layer_qwen3_fwd_bwd"] = bench_fwd_bwd(dev, 3, 1)
+        extra["layer_qwen3_fwd_bwd"] = bench_fwd_bwd(dev, 10, 3)
         log("fwd+bwd", extra["layer_qwen3_fwd_bwd"])
 
     cpu = None if args.skip_cpu else cpu_baseline(c)
