@@ -136,8 +136,10 @@ int smoe_selftest_quant(unsigned long long* counts, void* stream);
  *   c[r,n] = bf16( sum_kb as[r,kb]*bs[e,n/128,kb] * sum_{k in kb} a[r,k]*b[e,n,k] )
  * a [R,Kdim] u8, as [R,Kdim/128] f32, b [E,N,Kdim] u8, bs [E,N/128,Kdim/128] f32,
  * offsets [E+1] i32 on the device -> c [R,N] bf16.  Zero-token experts
- * produce no tiles.  ws may be NULL (smoe_grouped_gemm_fp8_workspace_size
- * returns 0).
+ * produce no tiles.  offsets[] is read on the device only; the kernel clamps
+ * every expert's range to rows [0, R), so malformed offsets (decreasing, or
+ * past R) never cause an access outside a, as or c.  ws may be NULL
+ * (smoe_grouped_gemm_fp8_workspace_size returns 0).
  * Replaces pt.ops.grouped_gemm_fp8(permuted, w1, tokens_per_expert, ...)
  * (notes/2026-04/2026-04-21_gptoss_10_moe_fp8_grouped_gemm_diagnosis.md:39) and
  * _fp8_fused_grouped_fwd(A_fp8, A_si, B_fp8, B_si, tpe)
@@ -233,7 +235,9 @@ int smoe_transpose_blockwise_fp8(const uint8_t* wq, const float* ws, int E, int 
  * -> xTq [C, ld] u8,
  * xTs [C, ld/128] f32, pad [E+1] i32 (pad[e+1] = pad[e] + ceil(count/128)*128).
  * ld must be >= smoe_quant_cols_ld(R, E) (an upper bound known on the host;
- * columns past pad[E] are left untouched) and ld/128 <= 65535.
+ * columns past pad[E] are left untouched) and ld/128 <= 65535.  Rows outside
+ * [0, R) are never read, whatever offsets[] holds; gather[] entries are
+ * trusted to index rows of x.
  */
 int smoe_quant_cols_ld(int R, int E);
 int smoe_quant_cols_128x1(const uint16_t* x, const int32_t* gather, int gather_div, int R, int C,

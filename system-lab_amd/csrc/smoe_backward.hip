@@ -82,8 +82,8 @@ __global__ __launch_bounds__(1024) void pad_offsets_kernel(const int32_t* __rest
 constexpr int kQcCols = 128;
 
 __global__ __launch_bounds__(256) void quant_cols_kernel(
-    const uint16_t* __restrict__ x, const int32_t* __restrict__ gather, int gather_div, int C,
-    const int32_t* __restrict__ offsets, const int32_t* __restrict__ pad, int E, int ld,
+    const uint16_t* __restrict__ x, const int32_t* __restrict__ gather, int gather_div, int R,
+    int C, const int32_t* __restrict__ offsets, const int32_t* __restrict__ pad, int E, int ld,
     uint8_t* __restrict__ q, float* __restrict__ s) {
   __shared__ int pad_l[SMOE_MAX_EXPERTS + 1];
   __shared__ float wmax[4][kQcCols];
@@ -102,7 +102,9 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(
   }
   const int e = lo;
   const int row0 = offsets[e] + (gpos - pad_l[e]);
-  const int valid = min(kGroup, offsets[e + 1] - row0);
+  // rows outside [0, R) are never read, whatever offsets[] holds (the group
+  // then quantises as zero padding)
+  const int valid = row0 < 0 ? 0 : min(kGroup, min(offsets[e + 1], R) - row0);
   const int c0 = blockIdx.x * kQcCols;
   const int cc = (t & 15) * 8;  // this thread's 8 columns
   const int rg = t >> 4;        // this thread's rows rg*8 .. rg*8+7
@@ -322,7 +324,7 @@ extern "C" int smoe_quant_cols_128x1(const uint16_t* x, const int32_t* gather, i
   pad_offsets_kernel<<<1, 1024, 0, s>>>(offsets, E, pad);
   // column slabs vary fastest, so the workgroups in flight read whole rows
   quant_cols_kernel<<<dim3((C + kQcCols - 1) / kQcCols, ld / kGroup), dim3(256), 0, s>>>(
-      x, gather, gather ? gather_div : 1, C, offsets, pad, E, ld, xTq, xTs);
+      x, gather, gather ? gather_div : 1, R, C, offsets, pad, E, ld, xTq, xTs);
   SMOE_RETURN_LAUNCH();
 }
 

@@ -74,8 +74,9 @@ struct Cfg {
 template <class C, bool kSwiGLU>
 __global__ __launch_bounds__(C::kThreads, 1) void grouped_gemm_fp8_kernel(
     const uint8_t* __restrict__ a, const float* __restrict__ as, const uint8_t* __restrict__ b,
-    const float* __restrict__ bs, const int32_t* __restrict__ offsets, int E, int N, int Kd,
-    int mt_bound, uint16_t* __restrict__ c, uint8_t* __restrict__ hq, float* __restrict__ hs) {
+    const float* __restrict__ bs, const int32_t* __restrict__ offsets, int E, int R, int N,
+    int Kd, int mt_bound, uint16_t* __restrict__ c, uint8_t* __restrict__ hq,
+    float* __restrict__ hs) {
   static_assert(!kSwiGLU || C::kBN == 256, "fused SwiGLU pairs 128 gate with 128 up columns");
   constexpr int kThreads = C::kThreads, kBM = C::kBM, kBN = C::kBN, kStage = C::kStage;
   constexpr int kStages = C::kStages, kABytes = C::kABytes, kBBytes = C::kBBytes;
@@ -152,7 +153,9 @@ __global__ __launch_bounds__(C::kThreads, 1) void grouped_gemm_fp8_kernel(
   }
   const int e = lo;
   const int row0 = offsets[e] + (mt - mstart[e]) * kBM;
-  const int rows = min(kBM, offsets[e + 1] - row0);
+  // rows outside [0, R) are never touched, whatever offsets[] holds
+  const int rows = min(kBM, min(offsets[e + 1], R) - row0);
+  if (row0 < 0 || rows <= 0) return;  // the whole workgroup leaves together
   const int n0 = nt * kBN;
   const int ksb = Kd / kBK;
 
@@ -386,7 +389,7 @@ extern "C" int smoe_grouped_gemm_fp8(const uint8_t* a, const float* as, const ui
   if (nblk > 0x7fffffffLL) return SMOE_EINVAL_DIM;
   grouped_gemm_fp8_kernel<C, false>
       <<<dim3((unsigned)nblk), dim3(C::kThreads), 0, (hipStream_t)stream>>>(
-          a, as, b, bs, offsets, E, N, Kdim, (int)mt_bound, c, nullptr, nullptr);
+          a, as, b, bs, offsets, E, R, N, Kdim, (int)mt_bound, c, nullptr, nullptr);
   SMOE_RETURN_LAUNCH();
 }
 
@@ -417,6 +420,6 @@ extern "C" int smoe_grouped_gemm_fp8_swiglu(const uint8_t* a, const float* as, c
   if (nblk > 0x7fffffffLL) return SMOE_EINVAL_DIM;
   grouped_gemm_fp8_kernel<C, true>
       <<<dim3((unsigned)nblk), dim3(C::kThreads), 0, (hipStream_t)stream>>>(
-          a, as, w1, w1s, offsets, E, N, Kdim, (int)mt_bound, c1, hq, hs);
+          a, as, w1, w1s, offsets, E, R, N, Kdim, (int)mt_bound, c1, hq, hs);
   SMOE_RETURN_LAUNCH();
 }

@@ -38,8 +38,9 @@ __global__ __launch_bounds__(kWThreads, 1) void grouped_gemm_fp8_wgrad_kernel(
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int e = blockIdx.z;
   const int n0 = blockIdx.y * kWN, k0 = blockIdx.x * kWK;
-  const int g0 = pad[e], g1 = pad[e + 1];
-  const int steps = (g1 - g0) / kGroup;
+  // operand columns outside [0, ld) are never read, whatever pad[] holds
+  const int g0 = max(pad[e], 0), g1 = min(pad[e + 1], ld);
+  const int steps = g1 > g0 ? (g1 - g0) / kGroup : 0;
   const int nrows = min(kWN, N - n0), krows = min(kWK, Kd - k0);
   const int sld = ld / kGroup;  // scale row length
 

@@ -342,6 +342,23 @@ def test_gemm_max_kdim(dev):
     gemm_close(got, O.grouped_gemm_fp8(xq, xs, wq, ws, off), "Kdim=65536")
 
 
+def test_gemm_malformed_offsets_stay_in_range(dev):
+    """offsets[] lives on the device and is not validated on the host, so the
+    kernel clamps every tile to rows [0, R): here expert 1's offsets decrease
+    (no tiles) and expert 2's run past R.  No access leaves the buffers; the
+    rows that belong to one expert only match the oracle."""
+    say("gemm malformed offsets")
+    rng = np.random.default_rng(77)
+    R, N, Kd, E = 1000, 256, 256, 3
+    xq, xs, wq, ws = _fp8_operands(rng, R, N, Kd, E)
+    bad = np.array([0, 400, 300, 1500], np.int32)
+    got = _run_gemm(dev, xq, xs, wq, ws, bad)
+    ref0 = O.grouped_gemm_fp8(xq, xs, wq, ws, np.array([0, 300, 300, 300], np.int32))
+    ref2 = O.grouped_gemm_fp8(xq, xs, wq, ws, np.array([0, 0, 0, R], np.int32))
+    gemm_close(got[:300], ref0[:300], "expert 0 rows")
+    gemm_close(got[400:], ref2[400:], "expert 2 rows, clamped at R")
+
+
 def test_gemm_dsv3_shape_sampled_rows(dev):
     """Benchmark config 4 at full size (R=65536, 32 experts, Zipf loads with
     zero-token experts, fc1 N=4096 K=7168 and fc2 N=7168 K=2048); the oracle
