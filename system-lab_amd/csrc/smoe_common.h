@@ -19,10 +19,6 @@ constexpr int kGroup = 128;  // quantisation group / weight block edge
 constexpr float kE4M3Max = 448.0f;
 
 // ---------------------------------------------------------------- bf16 ----
-__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
-  return __uint_as_float(bits16 << 16);
-}
-
 // Round-to-nearest-even fp32 -> bf16 bits; NaN stays a quiet NaN.  The
 // software statement of the rule: kernels use bf16_pack2 below.
 __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
