@@ -245,6 +245,21 @@ int smoe_quant_cols_128x1(const uint16_t* x, const int32_t* gather, int gather_d
                           int32_t* pad, void* stream);
 
 /*
+ * Both quantisations of one tensor from a single read: x [R,C] bf16 ->
+ * the 1x128 row quantisation xq [R,C] u8 + xs [R,C/128] f32 (the bytes of
+ * smoe_quant_rows_1x128) and the transposed 128x1 column quantisation
+ * xTq / xTs / pad of smoe_quant_cols_128x1 (no gather).  Rows are those of
+ * the expert segments offsets[E+1], which must cover [0, R) for every row
+ * of xq to be written.  The fp8 recipe quantises activation grads both
+ * ways, 1x128 for dgrad and 128x1 for wgrad
+ * (moe/MegatronCore_MoE_reading_notes.md:498-501); this replaces the two
+ * separate passes of the backward over dy and dc1.
+ */
+int smoe_quant_rows_cols(const uint16_t* x, int R, int C, const int32_t* offsets, int E, int ld,
+                         uint8_t* xq, float* xs, uint8_t* xTq, float* xTs, int32_t* pad,
+                         void* stream);
+
+/*
  * Variable-K grouped fp8 GEMM for weight gradients:
  *   dW[e][n][k] = sum over expert e's groups g of aTs[n,g]*bTs[k,g]*sum_r aT[n,r]*bT[k,r]
  * aT [N, ld] / bT [Kdim, ld] u8 and scales [*, ld/128] from

@@ -81,14 +81,21 @@ __global__ __launch_bounds__(1024) void pad_offsets_kernel(const int32_t* __rest
 // stores that cover one column's 128 bytes merge in L2.
 constexpr int kQcCols = 128;
 
+// kRows: also quantise the same tile 1x128 along rows (the dgrad operand),
+// written to qr [R, C] / sr [R, C/128] exactly as smoe_quant_rows_1x128 would,
+// so a tensor needed both ways is read once.
+template <bool kRows>
 __global__ __launch_bounds__(256) void quant_cols_kernel(
     const uint16_t* __restrict__ x, const int32_t* __restrict__ gather, int gather_div, int R,
     int C, const int32_t* __restrict__ offsets, const int32_t* __restrict__ pad, int E, int ld,
-    uint8_t* __restrict__ q, float* __restrict__ s) {
+    uint8_t* __restrict__ q, float* __restrict__ s, uint8_t* __restrict__ qr,
+    float* __restrict__ sr) {
   __shared__ int pad_l[SMOE_MAX_EXPERTS + 1];
   __shared__ float wmax[4][kQcCols];
   __shared__ float col_m[kQcCols], col_r[kQcCols];  // per-column quotient set-up
   __shared__ int col_e[kQcCols];
+  __shared__ float row_m[kQcCols], row_r[kQcCols];  // per-row set-up (kRows)
+  __shared__ int row_e[kQcCols];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   for (int i = t; i <= E; i += 256) pad_l[i] = pad[i];
   __syncthreads();
@@ -140,6 +147,35 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(
 #pragma unroll
     for (int i = 0; i < 8; ++i) wmax[w][cc + i] = cmax[i];
   }
+  if constexpr (kRows) {
+    // row amax of each 1x128 group: this thread's 8 columns, then the 16
+    // threads that share the row; lane j of the 16 derives row rg*8+j's set-up
+    float rmax[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t wd[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+      float m = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        m = fmaxf(m, fabsf(__uint_as_float(wd[i] << 16)));
+        m = fmaxf(m, fabsf(__uint_as_float(wd[i] & 0xffff0000u)));
+      }
+      rmax[j] = group_max<16>(m);
+    }
+    const int j = t & 15;
+    if (j < 8) {
+      float am = rmax[0];
+#pragma unroll
+      for (int i = 1; i < 8; ++i) am = (j == i) ? rmax[i] : am;
+      const float sc = group_scale(am);
+      const QDiv qd = qdiv_setup(sc);
+      const int r = rg * 8 + j;
+      row_m[r] = qd.m;
+      row_r[r] = qd.r;
+      row_e[r] = qd.e;
+      if (r < valid) sr[(size_t)(row0 + r) * (C / kGroup) + c0 / kGroup] = sc;
+    }
+  }
   __syncthreads();
   // one thread per column finishes the amax, derives the scale and the
   // quotient set-up (two IEEE divisions) and shares them: the 16 threads
@@ -173,6 +209,27 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(
     const uint32_t b[2] = {e4m3_pack4(qv[0], qv[1], qv[2], qv[3]),
                            e4m3_pack4(qv[4], qv[5], qv[6], qv[7])};
     *(uint2*)(dst + (size_t)i * ld) = make_uint2(b[0], b[1]);
+  }
+  if constexpr (kRows) {
+    // row r's 8 bytes at columns c0+cc .. +8 (16 threads cover the group)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int r = rg * 8 + j;
+      if (r >= valid) break;
+      QDiv rd;
+      rd.m = row_m[r];
+      rd.r = row_r[r];
+      rd.e = row_e[r];
+      float qv[8];
+      const uint32_t wd[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        qv[2 * i] = quot_bf16(__uint_as_float(wd[i] << 16), rd);
+        qv[2 * i + 1] = quot_bf16(__uint_as_float(wd[i] & 0xffff0000u), rd);
+      }
+      *(uint2*)(qr + (size_t)(row0 + r) * C + c0 + cc) =
+          make_uint2(e4m3_pack4(qv[0], qv[1], qv[2], qv[3]), e4m3_pack4(qv[4], qv[5], qv[6], qv[7]));
+    }
   }
 }
 
@@ -323,8 +380,30 @@ extern "C" int smoe_quant_cols_128x1(const uint16_t* x, const int32_t* gather, i
   hipStream_t s = (hipStream_t)stream;
   pad_offsets_kernel<<<1, 1024, 0, s>>>(offsets, E, pad);
   // column slabs vary fastest, so the workgroups in flight read whole rows
-  quant_cols_kernel<<<dim3((C + kQcCols - 1) / kQcCols, ld / kGroup), dim3(256), 0, s>>>(
-      x, gather, gather ? gather_div : 1, R, C, offsets, pad, E, ld, xTq, xTs);
+  quant_cols_kernel<false><<<dim3((C + kQcCols - 1) / kQcCols, ld / kGroup), dim3(256), 0, s>>>(
+      x, gather, gather ? gather_div : 1, R, C, offsets, pad, E, ld, xTq, xTs, nullptr, nullptr);
+  SMOE_RETURN_LAUNCH();
+}
+
+extern "C" int smoe_quant_rows_cols(const uint16_t* x, int R, int C, const int32_t* offsets, int E,
+                                    int ld, uint8_t* xq, float* xs, uint8_t* xTq, float* xTs,
+                                    int32_t* pad, void* stream) {
+  if (R <= 0 || C <= 0) return SMOE_EINVAL_DIM;
+  if (E <= 0 || E > SMOE_MAX_EXPERTS) return SMOE_EINVAL_EXPERTS;
+  if (C % kGroup) return SMOE_EINVAL_ALIGN128;
+  if (ld < smoe_quant_cols_ld(R, E) || ld % kGroup) return SMOE_EINVAL_DIM;
+  if (ld / kGroup > 65535) return SMOE_EINVAL_DIM;
+  SMOE_CHECK_PTR(x);
+  SMOE_CHECK_PTR(xTq);
+  if (!offsets || !xTs || !pad || !xs) return SMOE_EINVAL_NULL;
+  if (((uintptr_t)offsets | (uintptr_t)xTs | (uintptr_t)pad | (uintptr_t)xs) & 3u)
+    return SMOE_EINVAL_PTRALIGN;
+  if (!xq) return SMOE_EINVAL_NULL;
+  if ((uintptr_t)xq & 7u) return SMOE_EINVAL_PTRALIGN;
+  hipStream_t s = (hipStream_t)stream;
+  pad_offsets_kernel<<<1, 1024, 0, s>>>(offsets, E, pad);
+  quant_cols_kernel<true><<<dim3((C + kQcCols - 1) / kQcCols, ld / kGroup), dim3(256), 0, s>>>(
+      x, nullptr, 1, R, C, offsets, pad, E, ld, xTq, xTs, xq, xs);
   SMOE_RETURN_LAUNCH();
 }
 

@@ -86,9 +86,10 @@ class SimpleMoE(nn.Module):
         """Backward of one forward call given its intermediates
         (``forward(..., return_intermediates=True)``) and dout [T,H] bf16.
 
-        combine bwd -> dy 1x128 quant -> fc2 dgrad (W2^T) and fc2 wgrad
-        (128x1 dy, h) -> SwiGLU bwd -> dc1 quant -> fc1 dgrad (W1^T) and fc1
-        wgrad (128x1 dc1, sorted x) -> sum of the K replicas into dx.
+        combine bwd -> dy quant (1x128 rows and 128x1 columns, one pass) ->
+        fc2 dgrad (W2^T) and fc2 wgrad (128x1 dy, h) -> SwiGLU bwd -> dc1
+        quant (both ways, one pass) -> fc1 dgrad (W1^T) and fc1 wgrad (128x1
+        dc1, sorted x) -> sum of the K replicas into dx.
         Returns dx [T,H] bf16, dw1 [E,2I,H] f32, dw2 [E,H,I] f32 and the
         router-weight gradient dtopk_w [T,K] f32.  Every stage is a HIP kernel;
         nothing synchronises with the host."""
@@ -99,16 +100,16 @@ class SimpleMoE(nn.Module):
         off, inv = inter["offsets"], inter["inv_map"]
         K = self.top_k
         dy, dw = ops.unpermute_combine_bwd(dout.contiguous(), inter["y"], inv, inter["topk_w"])
-        dyq, dys = ops.quant_rows(dy)
+        # dy and dc1 are quantised both ways (1x128 rows for dgrad, 128x1
+        # columns for wgrad) from a single read each
+        dyq, dys, dyTq, dyTs, pad, ld = ops.quant_rows_cols(dy, off)
         dh = ops.grouped_gemm_fp8(dyq, dys, w2tq, w2ts, off)
         h = inter["h"]
-        dyTq, dyTs, pad, ld = ops.quant_cols(dy, off)
         hTq, hTs, _, _ = ops.quant_cols(h, off)
         dw2 = ops.grouped_gemm_fp8_wgrad(dyTq, dyTs, hTq, hTs, pad, ld)
         dc1 = ops.swiglu_bwd(inter["c1"], dh)
-        dcq, dcs = ops.quant_rows(dc1)
+        dcq, dcs, dcTq, dcTs, _, _ = ops.quant_rows_cols(dc1, off)
         dxs = ops.grouped_gemm_fp8(dcq, dcs, w1tq, w1ts, off)
-        dcTq, dcTs, _, _ = ops.quant_cols(dc1, off)
         # the sorted tokens x[row_map // K], gathered inside the quantiser
         xTq, xTs, _, _ = ops.quant_cols(inter["x"], off, gather=inter["row_map"], gather_div=K)
         dw1 = ops.grouped_gemm_fp8_wgrad(dcTq, dcTs, xTq, xTs, pad, ld)

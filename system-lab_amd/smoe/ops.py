@@ -289,6 +289,26 @@ def quant_cols(x: torch.Tensor, offsets: torch.Tensor, gather: torch.Tensor | No
     return xTq, xTs, pad, ld
 
 
+def quant_rows_cols(x: torch.Tensor, offsets: torch.Tensor):
+    """Both quantisations of x [R,C] bf16 from one read: the 1x128 rows of
+    ``quant_rows`` and the transposed 128x1 columns of ``quant_cols`` over
+    the expert segments ``offsets`` (which must cover all R rows).
+    -> (xq [R,C] fp8, xs [R,C/128], xTq [C,ld] fp8, xTs [C,ld/128], pad, ld)."""
+    _check(x, "x", (torch.bfloat16,), 2)
+    _check(offsets, "offsets", (torch.int32,), 1)
+    R, C = x.shape
+    E = offsets.numel() - 1
+    ld = int(_C.lib().smoe_quant_cols_ld(R, E))
+    xq = torch.empty((R, C), dtype=FP8, device=x.device)
+    xs = torch.empty((R, C // GROUP), dtype=torch.float32, device=x.device)
+    xTq = torch.empty((C, ld), dtype=FP8, device=x.device)
+    xTs = torch.empty((C, ld // GROUP), dtype=torch.float32, device=x.device)
+    pad = torch.empty(E + 1, dtype=torch.int32, device=x.device)
+    _C.call("smoe_quant_rows_cols", _ptr(x), R, C, _ptr(offsets), E, ld, _ptr(xq), _ptr(xs),
+            _ptr(xTq), _ptr(xTs), _ptr(pad), _stream())
+    return xq, xs, xTq, xTs, pad, ld
+
+
 def grouped_gemm_fp8_wgrad(aTq, aTs, bTq, bTs, pad, ld: int) -> torch.Tensor:
     """dW[e] = A_e^T B_e over each expert's rows from quant_cols operands:
     aT [N, ld], bT [K, ld] -> fp32 [E, N, K]."""

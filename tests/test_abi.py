@@ -134,6 +134,12 @@ def test_remaining_entry_points_reject():
     assert t(FAKE, None, 2, 128, 128, FAKE, FAKE, None) == -1
     assert lib.smoe_quant_rows_1x128(FAKE, 10, 100, FAKE, FAKE, None) == -3
     assert lib.smoe_quant_rows_1x128(FAKE, 0, 128, FAKE, FAKE, None) == -2
+    # one-read row + column quantiser: C % 128, experts, ld too small, xs NULL
+    rc = lib.smoe_quant_rows_cols
+    assert rc(FAKE, 1000, 100, FAKE, 4, ld, FAKE, FAKE, FAKE, FAKE, FAKE, None) == -3
+    assert rc(FAKE, 1000, 128, FAKE, 0, ld, FAKE, FAKE, FAKE, FAKE, FAKE, None) == -4
+    assert rc(FAKE, 1000, 128, FAKE, 4, ld - 128, FAKE, FAKE, FAKE, FAKE, FAKE, None) == -2
+    assert rc(FAKE, 1000, 128, FAKE, 4, ld, FAKE, None, FAKE, FAKE, FAKE, None) == -1
     # SwiGLU with the bf16 h output: misaligned h; the quantiser self-test
     assert lib.smoe_swiglu_quant_h(FAKE, 10, 128, FAKE, FAKE, MIS, None) == -6
     assert lib.smoe_selftest_quant(None, None) == -1

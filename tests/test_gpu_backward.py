@@ -130,6 +130,33 @@ def test_quant_rows_and_weights_special_values(dev):
     assert np.array_equal(ws.cpu().numpy().view(np.uint32), rws.view(np.uint32))
 
 
+@pytest.mark.parametrize("counts,C,special", [([130, 0, 5, 256, 1], 256, False),
+                                               ([1000, 24, 0, 2000], 768, False),
+                                               ([200, 57], 384, True), ([4096] * 2, 2048, False)])
+def test_quant_rows_cols_equals_separate_passes(dev, counts, C, special):
+    """The one-read quantiser gives exactly the bytes of quant_rows (1x128,
+    checked against the oracle) and of quant_cols (128x1, against the
+    oracle's transposed groups)."""
+    say("quant_rows_cols", counts, C, special)
+    off = _offsets(counts)
+    R = int(off[-1])
+    if special:
+        xb = _special_values(R, C, R + 3 * C)
+    else:
+        xb = O.f32_to_bf16(np.random.default_rng(R + C).standard_normal((R, C)).astype(np.float32))
+    xt = torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16).to(dev)
+    off_t = torch.from_numpy(off).to(dev)
+    q, s, qT, sT, pad, ld = ops.quant_rows_cols(xt, off_t)
+    rq, rs = O.quant_1x128(O.bf16_to_f32(xb))
+    assert np.array_equal(u8(q), rq)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), rs.view(np.uint32))
+    cq, cs, cpad, cld = ops.quant_cols(xt, off_t)
+    Rp = int(cpad[-1])
+    assert ld == cld and torch.equal(pad, cpad)
+    assert torch.equal(qT.view(torch.uint8)[:, :Rp], cq.view(torch.uint8)[:, :Rp])
+    assert torch.equal(sT[:, :Rp // 128].view(torch.int32), cs[:, :Rp // 128].view(torch.int32))
+
+
 def test_quant_cols_gather_bit_exact(dev):
     say("quant_cols gather")
     rng = np.random.default_rng(3)
