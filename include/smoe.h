@@ -260,6 +260,22 @@ int smoe_quant_rows_cols(const uint16_t* x, int R, int C, const int32_t* offsets
                          void* stream);
 
 /*
+ * SwiGLU backward fused into both quantisations of its output: computes
+ * dc1 [R,2I] = [dg | du] from c1 [R,2I] and dh [R,I] exactly as
+ * smoe_swiglu_bwd does (bf16-rounded), and writes the
+ * smoe_quant_rows_cols outputs of dc1 (dcq [R,2I] u8, dcs [R,2I/128],
+ * dcTq [2I,ld] u8, dcTs [2I,ld/128], pad) without storing dc1 itself,
+ * unless dc1 is not NULL.  Same bytes as smoe_swiglu_bwd followed by
+ * smoe_quant_rows_cols.  Replaces the "dexpert" activation backward and
+ * the requantisation of its gradient
+ * (moe/MoE_detailed_computation_dataflow.md:209-226;
+ * moe/MegatronCore_MoE_reading_notes.md:498-501).
+ */
+int smoe_swiglu_bwd_quant(const uint16_t* c1, const uint16_t* dh, int R, int I,
+                          const int32_t* offsets, int E, int ld, uint8_t* dcq, float* dcs,
+                          uint8_t* dcTq, float* dcTs, int32_t* pad, uint16_t* dc1, void* stream);
+
+/*
  * Variable-K grouped fp8 GEMM for weight gradients:
  *   dW[e][n][k] = sum over expert e's groups g of aTs[n,g]*bTs[k,g]*sum_r aT[n,r]*bT[k,r]
  * aT [N, ld] / bT [Kdim, ld] u8 and scales [*, ld/128] from

@@ -84,12 +84,19 @@ constexpr int kQcCols = 128;
 // kRows: also quantise the same tile 1x128 along rows (the dgrad operand),
 // written to qr [R, C] / sr [R, C/128] exactly as smoe_quant_rows_1x128 would,
 // so a tensor needed both ways is read once.
-template <bool kRows>
+// kSwigluBwd: the tiles are not read from x but computed: x is dc1 [R, 2I] =
+// [dg | du], the SwiGLU backward of c1 [R, 2I] and dh [R, I], with the same
+// fp32 operations and bf16 rounding as swiglu_bwd_kernel (C = 2I).  A
+// workgroup takes column block b of both halves, so slabs b (dg) and
+// I/128 + b (du) come from one sigmoid evaluation.  dc1 is written only when
+// not null.
+template <bool kRows, bool kSwigluBwd>
 __global__ __launch_bounds__(256) void quant_cols_kernel(
     const uint16_t* __restrict__ x, const int32_t* __restrict__ gather, int gather_div, int R,
     int C, const int32_t* __restrict__ offsets, const int32_t* __restrict__ pad, int E, int ld,
     uint8_t* __restrict__ q, float* __restrict__ s, uint8_t* __restrict__ qr,
-    float* __restrict__ sr) {
+    float* __restrict__ sr, const uint16_t* __restrict__ c1, const uint16_t* __restrict__ dh,
+    uint16_t* __restrict__ dc1) {
   __shared__ int pad_l[SMOE_MAX_EXPERTS + 1];
   __shared__ float wmax[4][kQcCols];
   __shared__ float col_m[kQcCols], col_r[kQcCols];  // per-column quotient set-up
@@ -112,124 +119,173 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(
   // rows outside [0, R) are never read, whatever offsets[] holds (the group
   // then quantises as zero padding)
   const int valid = row0 < 0 ? 0 : min(kGroup, min(offsets[e + 1], R) - row0);
-  const int c0 = blockIdx.x * kQcCols;
   const int cc = (t & 15) * 8;  // this thread's 8 columns
   const int rg = t >> 4;        // this thread's rows rg*8 .. rg*8+7
-  v4u v[8];
+  // quantise one 128x128 tile (v: this thread's 8 rows x 8 columns) whose
+  // columns start at c0, 128x1 along columns and (kRows) 1x128 along rows
+  auto quantize = [&](const v4u (&v)[8], const int c0) {
+    // column amax: 8 rows here, then the 4 row groups of this wave, then waves
+    float cmax[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int r = rg * 8 + j;
-    v[j] = v4u{0u, 0u, 0u, 0u};
-    if (r < valid) {
-      const int src = gather ? gather[row0 + r] / gather_div : row0 + r;
-      v[j] = __builtin_nontemporal_load((const v4u*)(x + (size_t)src * C + c0 + cc));
-    }
-  }
-  // column amax: 8 rows here, then the 4 row groups of this wave, then waves
-  float cmax[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) cmax[i] = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const uint32_t wd[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      cmax[2 * i] = fmaxf(cmax[2 * i], fabsf(__uint_as_float(wd[i] << 16)));
-      cmax[2 * i + 1] = fmaxf(cmax[2 * i + 1], fabsf(__uint_as_float(wd[i] & 0xffff0000u)));
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    cmax[i] = fmaxf(cmax[i], __shfl_xor(cmax[i], 16, kWave));
-    cmax[i] = fmaxf(cmax[i], __shfl_xor(cmax[i], 32, kWave));
-  }
-  if (lane < 16) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) wmax[w][cc + i] = cmax[i];
-  }
-  if constexpr (kRows) {
-    // row amax of each 1x128 group: this thread's 8 columns, then the 16
-    // threads that share the row; lane j of the 16 derives row rg*8+j's set-up
-    float rmax[8];
+    for (int i = 0; i < 8; ++i) cmax[i] = 0.0f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const uint32_t wd[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
-      float m = 0.0f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        m = fmaxf(m, fabsf(__uint_as_float(wd[i] << 16)));
-        m = fmaxf(m, fabsf(__uint_as_float(wd[i] & 0xffff0000u)));
+        cmax[2 * i] = fmaxf(cmax[2 * i], fabsf(__uint_as_float(wd[i] << 16)));
+        cmax[2 * i + 1] = fmaxf(cmax[2 * i + 1], fabsf(__uint_as_float(wd[i] & 0xffff0000u)));
       }
-      rmax[j] = group_max<16>(m);
     }
-    const int j = t & 15;
-    if (j < 8) {
-      float am = rmax[0];
 #pragma unroll
-      for (int i = 1; i < 8; ++i) am = (j == i) ? rmax[i] : am;
-      const float sc = group_scale(am);
+    for (int i = 0; i < 8; ++i) {
+      cmax[i] = fmaxf(cmax[i], __shfl_xor(cmax[i], 16, kWave));
+      cmax[i] = fmaxf(cmax[i], __shfl_xor(cmax[i], 32, kWave));
+    }
+    if (lane < 16) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) wmax[w][cc + i] = cmax[i];
+    }
+    if constexpr (kRows) {
+      // row amax of each 1x128 group: this thread's 8 columns, then the 16
+      // threads that share the row; lane j of the 16 derives row rg*8+j's set-up
+      float rmax[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t wd[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+        float m = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          m = fmaxf(m, fabsf(__uint_as_float(wd[i] << 16)));
+          m = fmaxf(m, fabsf(__uint_as_float(wd[i] & 0xffff0000u)));
+        }
+        rmax[j] = group_max<16>(m);
+      }
+      const int j = t & 15;
+      if (j < 8) {
+        float am = rmax[0];
+#pragma unroll
+        for (int i = 1; i < 8; ++i) am = (j == i) ? rmax[i] : am;
+        const float sc = group_scale(am);
+        const QDiv qd = qdiv_setup(sc);
+        const int r = rg * 8 + j;
+        row_m[r] = qd.m;
+        row_r[r] = qd.r;
+        row_e[r] = qd.e;
+        if (r < valid) sr[(size_t)(row0 + r) * (C / kGroup) + c0 / kGroup] = sc;
+      }
+    }
+    __syncthreads();
+    // one thread per column finishes the amax, derives the scale and the
+    // quotient set-up (two IEEE divisions) and shares them: the 16 threads
+    // that hold pieces of a column would otherwise repeat the divisions
+    if (t < kQcCols) {
+      const float sc = group_scale(fmaxf(fmaxf(wmax[0][t], wmax[1][t]), fmaxf(wmax[2][t], wmax[3][t])));
       const QDiv qd = qdiv_setup(sc);
-      const int r = rg * 8 + j;
-      row_m[r] = qd.m;
-      row_r[r] = qd.r;
-      row_e[r] = qd.e;
-      if (r < valid) sr[(size_t)(row0 + r) * (C / kGroup) + c0 / kGroup] = sc;
+      col_m[t] = qd.m;
+      col_r[t] = qd.r;
+      col_e[t] = qd.e;
+      s[(size_t)(c0 + t) * (ld / kGroup) + gpos / kGroup] = sc;
     }
-  }
-  __syncthreads();
-  // one thread per column finishes the amax, derives the scale and the
-  // quotient set-up (two IEEE divisions) and shares them: the 16 threads
-  // that hold pieces of a column would otherwise repeat the divisions
-  if (t < kQcCols) {
-    const float sc = group_scale(fmaxf(fmaxf(wmax[0][t], wmax[1][t]), fmaxf(wmax[2][t], wmax[3][t])));
-    const QDiv qd = qdiv_setup(sc);
-    col_m[t] = qd.m;
-    col_r[t] = qd.r;
-    col_e[t] = qd.e;
-    s[(size_t)(c0 + t) * (ld / kGroup) + gpos / kGroup] = sc;
-  }
-  __syncthreads();
-  QDiv d[8];
+    __syncthreads();
+    QDiv d[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    d[i].m = col_m[cc + i];
-    d[i].r = col_r[cc + i];
-    d[i].e = col_e[cc + i];
-  }
-  // column c0+cc+i gets bytes for rows gpos + rg*8 .. +8
-  uint8_t* dst = q + (size_t)(c0 + cc) * ld + gpos + rg * 8;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    float qv[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint32_t wd = (i & 1) ? (v[j][i >> 1] & 0xffff0000u) : (v[j][i >> 1] << 16);
-      qv[j] = quot_bf16(__uint_as_float(wd), d[i]);
+    for (int i = 0; i < 8; ++i) {
+      d[i].m = col_m[cc + i];
+      d[i].r = col_r[cc + i];
+      d[i].e = col_e[cc + i];
     }
-    const uint32_t b[2] = {e4m3_pack4(qv[0], qv[1], qv[2], qv[3]),
-                           e4m3_pack4(qv[4], qv[5], qv[6], qv[7])};
-    *(uint2*)(dst + (size_t)i * ld) = make_uint2(b[0], b[1]);
-  }
-  if constexpr (kRows) {
-    // row r's 8 bytes at columns c0+cc .. +8 (16 threads cover the group)
+    // column c0+cc+i gets bytes for rows gpos + rg*8 .. +8
+    uint8_t* dst = q + (size_t)(c0 + cc) * ld + gpos + rg * 8;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int r = rg * 8 + j;
-      if (r >= valid) break;
-      QDiv rd;
-      rd.m = row_m[r];
-      rd.r = row_r[r];
-      rd.e = row_e[r];
+    for (int i = 0; i < 8; ++i) {
       float qv[8];
-      const uint32_t wd[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        qv[2 * i] = quot_bf16(__uint_as_float(wd[i] << 16), rd);
-        qv[2 * i + 1] = quot_bf16(__uint_as_float(wd[i] & 0xffff0000u), rd);
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t wd = (i & 1) ? (v[j][i >> 1] & 0xffff0000u) : (v[j][i >> 1] << 16);
+        qv[j] = quot_bf16(__uint_as_float(wd), d[i]);
       }
-      *(uint2*)(qr + (size_t)(row0 + r) * C + c0 + cc) =
-          make_uint2(e4m3_pack4(qv[0], qv[1], qv[2], qv[3]), e4m3_pack4(qv[4], qv[5], qv[6], qv[7]));
+      const uint32_t b[2] = {e4m3_pack4(qv[0], qv[1], qv[2], qv[3]),
+                             e4m3_pack4(qv[4], qv[5], qv[6], qv[7])};
+      *(uint2*)(dst + (size_t)i * ld) = make_uint2(b[0], b[1]);
     }
+    if constexpr (kRows) {
+      // row r's 8 bytes at columns c0+cc .. +8 (16 threads cover the group)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int r = rg * 8 + j;
+        if (r >= valid) break;
+        QDiv rd;
+        rd.m = row_m[r];
+        rd.r = row_r[r];
+        rd.e = row_e[r];
+        float qv[8];
+        const uint32_t wd[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          qv[2 * i] = quot_bf16(__uint_as_float(wd[i] << 16), rd);
+          qv[2 * i + 1] = quot_bf16(__uint_as_float(wd[i] & 0xffff0000u), rd);
+        }
+        *(uint2*)(qr + (size_t)(row0 + r) * C + c0 + cc) =
+            make_uint2(e4m3_pack4(qv[0], qv[1], qv[2], qv[3]), e4m3_pack4(qv[4], qv[5], qv[6], qv[7]));
+      }
+    }
+  };
+
+  if constexpr (kSwigluBwd) {
+    // column block b of both halves: the sigmoid is computed once per (row,
+    // column) and gives dg (slab b) and du (slab I/128 + b)
+    const int I = C / 2, nI = I / kGroup;
+    const int col = (int)blockIdx.x * kGroup + cc;
+    v4u vG[8], vU[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int r = rg * 8 + j;
+      vG[j] = vU[j] = v4u{0u, 0u, 0u, 0u};
+      if (r < valid) {
+        const size_t row = (size_t)(row0 + r);
+        const v4u vg = __builtin_nontemporal_load((const v4u*)(c1 + row * 2 * I + col));
+        const v4u vu = __builtin_nontemporal_load((const v4u*)(c1 + row * 2 * I + I + col));
+        const v4u vd = __builtin_nontemporal_load((const v4u*)(dh + row * I + col));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float og[2], ou[2];
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const float g = h ? __uint_as_float(vg[i] & 0xffff0000u) : __uint_as_float(vg[i] << 16);
+            const float u = h ? __uint_as_float(vu[i] & 0xffff0000u) : __uint_as_float(vu[i] << 16);
+            const float d = h ? __uint_as_float(vd[i] & 0xffff0000u) : __uint_as_float(vd[i] << 16);
+            const float sg = 1.0f / (1.0f + expf32(-g));
+            const float silu = g * sg;
+            const float ds = sg * (1.0f + g * (1.0f - sg));
+            ou[h] = d * silu;
+            og[h] = (d * u) * ds;
+          }
+          vG[j][i] = bf16_pack2(og[0], og[1]);
+          vU[j][i] = bf16_pack2(ou[0], ou[1]);
+        }
+        if (dc1) {
+          *(v4u*)(dc1 + row * 2 * I + col) = vG[j];
+          *(v4u*)(dc1 + row * 2 * I + I + col) = vU[j];
+        }
+      }
+    }
+    quantize(vG, (int)blockIdx.x * kGroup);
+    __syncthreads();  // the second tile reuses the LDS exchange arrays
+    quantize(vU, (nI + (int)blockIdx.x) * kGroup);
+  } else {
+    v4u v[8];
+    const int c0 = blockIdx.x * kQcCols;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int r = rg * 8 + j;
+      v[j] = v4u{0u, 0u, 0u, 0u};
+      if (r < valid) {
+        const int src = gather ? gather[row0 + r] / gather_div : row0 + r;
+        v[j] = __builtin_nontemporal_load((const v4u*)(x + (size_t)src * C + c0 + cc));
+      }
+    }
+    quantize(v, c0);
   }
 }
 
@@ -380,8 +436,9 @@ extern "C" int smoe_quant_cols_128x1(const uint16_t* x, const int32_t* gather, i
   hipStream_t s = (hipStream_t)stream;
   pad_offsets_kernel<<<1, 1024, 0, s>>>(offsets, E, pad);
   // column slabs vary fastest, so the workgroups in flight read whole rows
-  quant_cols_kernel<false><<<dim3((C + kQcCols - 1) / kQcCols, ld / kGroup), dim3(256), 0, s>>>(
-      x, gather, gather ? gather_div : 1, R, C, offsets, pad, E, ld, xTq, xTs, nullptr, nullptr);
+  quant_cols_kernel<false, false><<<dim3((C + kQcCols - 1) / kQcCols, ld / kGroup), dim3(256), 0, s>>>(
+      x, gather, gather ? gather_div : 1, R, C, offsets, pad, E, ld, xTq, xTs, nullptr, nullptr,
+      nullptr, nullptr, nullptr);
   SMOE_RETURN_LAUNCH();
 }
 
@@ -402,8 +459,34 @@ extern "C" int smoe_quant_rows_cols(const uint16_t* x, int R, int C, const int32
   if ((uintptr_t)xq & 7u) return SMOE_EINVAL_PTRALIGN;
   hipStream_t s = (hipStream_t)stream;
   pad_offsets_kernel<<<1, 1024, 0, s>>>(offsets, E, pad);
-  quant_cols_kernel<true><<<dim3((C + kQcCols - 1) / kQcCols, ld / kGroup), dim3(256), 0, s>>>(
-      x, nullptr, 1, R, C, offsets, pad, E, ld, xTq, xTs, xq, xs);
+  quant_cols_kernel<true, false><<<dim3((C + kQcCols - 1) / kQcCols, ld / kGroup), dim3(256), 0, s>>>(
+      x, nullptr, 1, R, C, offsets, pad, E, ld, xTq, xTs, xq, xs, nullptr, nullptr, nullptr);
+  SMOE_RETURN_LAUNCH();
+}
+
+extern "C" int smoe_swiglu_bwd_quant(const uint16_t* c1, const uint16_t* dh, int R, int I,
+                                     const int32_t* offsets, int E, int ld, uint8_t* dcq,
+                                     float* dcs, uint8_t* dcTq, float* dcTs, int32_t* pad,
+                                     uint16_t* dc1, void* stream) {
+  if (R <= 0 || I <= 0) return SMOE_EINVAL_DIM;
+  if (E <= 0 || E > SMOE_MAX_EXPERTS) return SMOE_EINVAL_EXPERTS;
+  if (I % kGroup) return SMOE_EINVAL_ALIGN128;
+  if (ld < smoe_quant_cols_ld(R, E) || ld % kGroup) return SMOE_EINVAL_DIM;
+  if (ld / kGroup > 65535) return SMOE_EINVAL_DIM;
+  SMOE_CHECK_PTR(c1);
+  SMOE_CHECK_PTR(dh);
+  SMOE_CHECK_PTR(dcTq);
+  if (!offsets || !dcTs || !pad || !dcs || !dcq) return SMOE_EINVAL_NULL;
+  if (((uintptr_t)offsets | (uintptr_t)dcTs | (uintptr_t)pad | (uintptr_t)dcs) & 3u)
+    return SMOE_EINVAL_PTRALIGN;
+  if ((uintptr_t)dcq & 7u) return SMOE_EINVAL_PTRALIGN;
+  if (dc1 && ((uintptr_t)dc1 & 15u)) return SMOE_EINVAL_PTRALIGN;
+  const int C = 2 * I;
+  hipStream_t s = (hipStream_t)stream;
+  pad_offsets_kernel<<<1, 1024, 0, s>>>(offsets, E, pad);
+  // one workgroup per 128-column block of both halves (dg and du)
+  quant_cols_kernel<true, true><<<dim3(I / kQcCols, ld / kGroup), dim3(256), 0, s>>>(
+      nullptr, nullptr, 1, R, C, offsets, pad, E, ld, dcTq, dcTs, dcq, dcs, c1, dh, dc1);
   SMOE_RETURN_LAUNCH();
 }
 

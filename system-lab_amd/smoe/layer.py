@@ -87,8 +87,8 @@ class SimpleMoE(nn.Module):
         (``forward(..., return_intermediates=True)``) and dout [T,H] bf16.
 
         combine bwd -> dy quant (1x128 rows and 128x1 columns, one pass) ->
-        fc2 dgrad (W2^T) and fc2 wgrad (128x1 dy, h) -> SwiGLU bwd -> dc1
-        quant (both ways, one pass) -> fc1 dgrad (W1^T) and fc1 wgrad (128x1
+        fc2 dgrad (W2^T) and fc2 wgrad (128x1 dy, h) -> SwiGLU bwd fused with
+        both quantisations of dc1 -> fc1 dgrad (W1^T) and fc1 wgrad (128x1
         dc1, sorted x) -> sum of the K replicas into dx.
         Returns dx [T,H] bf16, dw1 [E,2I,H] f32, dw2 [E,H,I] f32 and the
         router-weight gradient dtopk_w [T,K] f32.  Every stage is a HIP kernel;
@@ -107,13 +107,14 @@ class SimpleMoE(nn.Module):
         h = inter["h"]
         hTq, hTs, _, _ = ops.quant_cols(h, off)
         dw2 = ops.grouped_gemm_fp8_wgrad(dyTq, dyTs, hTq, hTs, pad, ld)
-        dc1 = ops.swiglu_bwd(inter["c1"], dh)
-        dcq, dcs, dcTq, dcTs, _, _ = ops.quant_rows_cols(dc1, off)
+        # SwiGLU backward fused with both quantisations of dc1 (dc1 itself is
+        # never stored)
+        dcq, dcs, dcTq, dcTs, _, _ = ops.swiglu_bwd_quant(inter["c1"], dh, off)
         dxs = ops.grouped_gemm_fp8(dcq, dcs, w1tq, w1ts, off)
         # the sorted tokens x[row_map // K], gathered inside the quantiser
         xTq, xTs, _, _ = ops.quant_cols(inter["x"], off, gather=inter["row_map"], gather_div=K)
         dw1 = ops.grouped_gemm_fp8_wgrad(dcTq, dcTs, xTq, xTs, pad, ld)
         ones = torch.ones_like(inter["topk_w"])
         dx = ops.unpermute_combine(dxs, inv, ones)
-        return dict(dx=dx, dw1=dw1, dw2=dw2, dtopk_w=dw, dy=dy, dh=dh, dc1=dc1, dxs=dxs)
+        return dict(dx=dx, dw1=dw1, dw2=dw2, dtopk_w=dw, dy=dy, dh=dh, dxs=dxs)
 

@@ -309,6 +309,35 @@ def quant_rows_cols(x: torch.Tensor, offsets: torch.Tensor):
     return xq, xs, xTq, xTs, pad, ld
 
 
+def swiglu_bwd_quant(c1: torch.Tensor, dh: torch.Tensor, offsets: torch.Tensor,
+                     save_dc1: bool = False):
+    """SwiGLU backward fused with both quantisations of its output: the
+    bytes of ``quant_rows_cols(swiglu_bwd(c1, dh), offsets)`` without
+    storing dc1 (returned as the last element when ``save_dc1``).
+    c1 [R,2I], dh [R,I] bf16 -> (dcq [R,2I] fp8, dcs, dcTq [2I,ld] fp8, dcTs,
+    pad, ld[, dc1])."""
+    _check(c1, "c1", (torch.bfloat16,), 2)
+    _check(dh, "dh", (torch.bfloat16,), 2)
+    _check(offsets, "offsets", (torch.int32,), 1)
+    R, N = c1.shape
+    I = N // 2
+    if dh.shape != (R, I) or N != 2 * I:
+        raise ValueError("dh must be [R, I] for c1 [R, 2I]")
+    E = offsets.numel() - 1
+    ld = int(_C.lib().smoe_quant_cols_ld(R, E))
+    dev = c1.device
+    dcq = torch.empty((R, N), dtype=FP8, device=dev)
+    dcs = torch.empty((R, N // GROUP), dtype=torch.float32, device=dev)
+    dcTq = torch.empty((N, ld), dtype=FP8, device=dev)
+    dcTs = torch.empty((N, ld // GROUP), dtype=torch.float32, device=dev)
+    pad = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    dc1 = torch.empty((R, N), dtype=torch.bfloat16, device=dev) if save_dc1 else None
+    _C.call("smoe_swiglu_bwd_quant", _ptr(c1), _ptr(dh), R, I, _ptr(offsets), E, ld, _ptr(dcq),
+            _ptr(dcs), _ptr(dcTq), _ptr(dcTs), _ptr(pad), _ptr(dc1), _stream())
+    out = (dcq, dcs, dcTq, dcTs, pad, ld)
+    return out + (dc1,) if save_dc1 else out
+
+
 def grouped_gemm_fp8_wgrad(aTq, aTs, bTq, bTs, pad, ld: int) -> torch.Tensor:
     """dW[e] = A_e^T B_e over each expert's rows from quant_cols operands:
     aT [N, ld], bT [K, ld] -> fp32 [E, N, K]."""

@@ -140,6 +140,10 @@ def test_remaining_entry_points_reject():
     assert rc(FAKE, 1000, 128, FAKE, 0, ld, FAKE, FAKE, FAKE, FAKE, FAKE, None) == -4
     assert rc(FAKE, 1000, 128, FAKE, 4, ld - 128, FAKE, FAKE, FAKE, FAKE, FAKE, None) == -2
     assert rc(FAKE, 1000, 128, FAKE, 4, ld, FAKE, None, FAKE, FAKE, FAKE, None) == -1
+    sb = lib.smoe_swiglu_bwd_quant
+    assert sb(FAKE, FAKE, 1000, 100, FAKE, 4, ld, FAKE, FAKE, FAKE, FAKE, FAKE, None, None) == -3
+    assert sb(FAKE, FAKE, 1000, 128, FAKE, 0, ld, FAKE, FAKE, FAKE, FAKE, FAKE, None, None) == -4
+    assert sb(FAKE, FAKE, 1000, 128, FAKE, 4, ld, FAKE, FAKE, FAKE, FAKE, FAKE, MIS, None) == -6
     # SwiGLU with the bf16 h output: misaligned h; the quantiser self-test
     assert lib.smoe_swiglu_quant_h(FAKE, 10, 128, FAKE, FAKE, MIS, None) == -6
     assert lib.smoe_selftest_quant(None, None) == -1

@@ -157,6 +157,30 @@ def test_quant_rows_cols_equals_separate_passes(dev, counts, C, special):
     assert torch.equal(sT[:, :Rp // 128].view(torch.int32), cs[:, :Rp // 128].view(torch.int32))
 
 
+@pytest.mark.parametrize("counts,I", [([300, 0, 77, 512], 768), ([1000], 128), ([5, 129], 2048)])
+def test_swiglu_bwd_quant_equals_two_kernels(dev, counts, I):
+    """The fused SwiGLU backward + quantiser gives the bytes of swiglu_bwd
+    followed by quant_rows_cols, and its optional dc1 equals swiglu_bwd's."""
+    say("swiglu_bwd_quant", counts, I)
+    off = _offsets(counts)
+    R = int(off[-1])
+    rng = np.random.default_rng(R + I)
+    c1 = O.f32_to_bf16((rng.standard_normal((R, 2 * I)) * 3).astype(np.float32))
+    c1[0, :6] = O.f32_to_bf16(np.array([0, 100, -100, 88.5, -88.5, -87.2], np.float32))
+    dh = O.f32_to_bf16(rng.standard_normal((R, I)).astype(np.float32))
+    c1t, dht, off_t = bf(c1, dev), bf(dh, dev), torch.from_numpy(off).to(dev)
+    dc1 = ops.swiglu_bwd(c1t, dht)
+    ref = ops.quant_rows_cols(dc1, off_t)
+    got = ops.swiglu_bwd_quant(c1t, dht, off_t, save_dc1=True)
+    Rp = int(ref[4][-1])
+    assert torch.equal(got[6].view(torch.int16), dc1.view(torch.int16))
+    assert torch.equal(got[0].view(torch.uint8), ref[0].view(torch.uint8))
+    assert torch.equal(got[1].view(torch.int32), ref[1].view(torch.int32))
+    assert torch.equal(got[2].view(torch.uint8)[:, :Rp], ref[2].view(torch.uint8)[:, :Rp])
+    assert torch.equal(got[3][:, :Rp // 128].view(torch.int32), ref[3][:, :Rp // 128].view(torch.int32))
+    assert torch.equal(got[4], ref[4]) and got[5] == ref[5]
+
+
 def test_quant_cols_gather_bit_exact(dev):
     say("quant_cols gather")
     rng = np.random.default_rng(3)
