@@ -305,6 +305,24 @@ int smoe_unpermute_combine_bwd(const uint16_t* dout, const uint16_t* y, const in
                                const float* w, int T, int K, int H, uint16_t* dy, float* dw,
                                void* stream);
 
+/*
+ * Combine backward fused with both quantisations of dy: writes dw [T,K] f32
+ * as smoe_unpermute_combine_bwd does, and, without storing dy [T*K,H], the
+ * smoe_quant_rows_cols outputs of dy (dyq [T*K,H] u8, dys [T*K,H/128],
+ * dyTq [H,ld] u8, dyTs [H,ld/128], pad) over the expert segments offsets:
+ * row r of dy is rebuilt inside the quantiser as bf16(w[p]*dout[p/K]) with
+ * p = row_map[r] (row_map and inv_map inverse permutations of [0, T*K),
+ * as smoe_route_sort writes them).  Same bytes as smoe_unpermute_combine_bwd
+ * followed by smoe_quant_rows_cols.  Replaces dmerge and the requantisation
+ * of its gradient (moe/MoE_detailed_computation_dataflow.md:209-226;
+ * moe/MegatronCore_MoE_reading_notes.md:498-501).
+ */
+int smoe_unpermute_combine_bwd_quant(const uint16_t* dout, const uint16_t* y,
+                                     const int32_t* inv_map, const int32_t* row_map,
+                                     const float* w, int T, int K, int H, const int32_t* offsets,
+                                     int E, int ld, uint8_t* dyq, float* dys, uint8_t* dyTq,
+                                     float* dyTs, int32_t* pad, float* dw, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -70,7 +70,9 @@ __global__ __launch_bounds__(1024) void pad_offsets_kernel(const int32_t* __rest
 // One 256-thread workgroup per (128-row group, 128-column slab).  The group's
 // rows (an expert's rows split into 128-row groups from its first row; short
 // last groups are zero-padded) are loaded with non-temporal 128-bit loads,
-// optionally gathered through src = gather[r] / gather_div.  Thread t owns 8
+// optionally gathered through p = gather[r] as row p / gather_div and
+// optionally weighted by gather_w[p] (bf16(w * x)).  All 8 loads of a thread
+// are issued before any is used.  Thread t owns 8
 // columns (t % 16) * 8 .. +8 of the 8 consecutive rows (t / 16) * 8 .. +8, so
 // everything stays in registers: the column amax is a local max over the 8
 // rows, an xor shuffle over the 4 row groups of a wave, and a 2 KB LDS
@@ -92,8 +94,8 @@ constexpr int kQcCols = 128;
 // not null.
 template <bool kRows, bool kSwigluBwd>
 __global__ __launch_bounds__(256) void quant_cols_kernel(
-    const uint16_t* __restrict__ x, const int32_t* __restrict__ gather, int gather_div, int R,
-    int C, const int32_t* __restrict__ offsets, const int32_t* __restrict__ pad, int E, int ld,
+    const uint16_t* __restrict__ x, const int32_t* __restrict__ gather, int gather_div,
+    const float* __restrict__ gather_w, int R, int C, const int32_t* __restrict__ offsets, const int32_t* __restrict__ pad, int E, int ld,
     uint8_t* __restrict__ q, float* __restrict__ s, uint8_t* __restrict__ qr,
     float* __restrict__ sr, const uint16_t* __restrict__ c1, const uint16_t* __restrict__ dh,
     uint16_t* __restrict__ dc1) {
@@ -159,7 +161,7 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(
           m = fmaxf(m, fabsf(__uint_as_float(wd[i] << 16)));
           m = fmaxf(m, fabsf(__uint_as_float(wd[i] & 0xffff0000u)));
         }
-        rmax[j] = group_max<16>(m);
+        rmax[j] = row16_max(m);
       }
       const int j = t & 15;
       if (j < 8) {
@@ -237,37 +239,44 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(
     // column) and gives dg (slab b) and du (slab I/128 + b)
     const int I = C / 2, nI = I / kGroup;
     const int col = (int)blockIdx.x * kGroup + cc;
-    v4u vG[8], vU[8];
+    v4u vG[8], vU[8], vD[8];
+    // all 24 loads issued before any arithmetic (unconditional; rows outside
+    // the group re-read a valid row and are zeroed after)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const size_t row = valid > 0 ? (size_t)(row0 + min(rg * 8 + j, valid - 1)) : 0;
+      vG[j] = __builtin_nontemporal_load((const v4u*)(c1 + row * 2 * I + col));
+      vU[j] = __builtin_nontemporal_load((const v4u*)(c1 + row * 2 * I + I + col));
+      vD[j] = __builtin_nontemporal_load((const v4u*)(dh + row * I + col));
+    }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int r = rg * 8 + j;
-      vG[j] = vU[j] = v4u{0u, 0u, 0u, 0u};
-      if (r < valid) {
-        const size_t row = (size_t)(row0 + r);
-        const v4u vg = __builtin_nontemporal_load((const v4u*)(c1 + row * 2 * I + col));
-        const v4u vu = __builtin_nontemporal_load((const v4u*)(c1 + row * 2 * I + I + col));
-        const v4u vd = __builtin_nontemporal_load((const v4u*)(dh + row * I + col));
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float og[2], ou[2];
+      for (int i = 0; i < 4; ++i) {
+        float og[2], ou[2];
 #pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            const float g = h ? __uint_as_float(vg[i] & 0xffff0000u) : __uint_as_float(vg[i] << 16);
-            const float u = h ? __uint_as_float(vu[i] & 0xffff0000u) : __uint_as_float(vu[i] << 16);
-            const float d = h ? __uint_as_float(vd[i] & 0xffff0000u) : __uint_as_float(vd[i] << 16);
-            const float sg = 1.0f / (1.0f + expf32(-g));
-            const float silu = g * sg;
-            const float ds = sg * (1.0f + g * (1.0f - sg));
-            ou[h] = d * silu;
-            og[h] = (d * u) * ds;
-          }
-          vG[j][i] = bf16_pack2(og[0], og[1]);
-          vU[j][i] = bf16_pack2(ou[0], ou[1]);
+        for (int h = 0; h < 2; ++h) {
+          const float g = h ? __uint_as_float(vG[j][i] & 0xffff0000u) : __uint_as_float(vG[j][i] << 16);
+          const float u = h ? __uint_as_float(vU[j][i] & 0xffff0000u) : __uint_as_float(vU[j][i] << 16);
+          const float d = h ? __uint_as_float(vD[j][i] & 0xffff0000u) : __uint_as_float(vD[j][i] << 16);
+          const float sg = 1.0f / (1.0f + expf32(-g));
+          const float silu = g * sg;
+          const float ds = sg * (1.0f + g * (1.0f - sg));
+          ou[h] = d * silu;
+          og[h] = (d * u) * ds;
         }
+        vG[j][i] = bf16_pack2(og[0], og[1]);
+        vU[j][i] = bf16_pack2(ou[0], ou[1]);
+      }
+      if (r < valid) {
         if (dc1) {
+          const size_t row = (size_t)(row0 + r);
           *(v4u*)(dc1 + row * 2 * I + col) = vG[j];
           *(v4u*)(dc1 + row * 2 * I + I + col) = vU[j];
         }
+      } else {
+        vG[j] = vU[j] = v4u{0u, 0u, 0u, 0u};
       }
     }
     quantize(vG, (int)blockIdx.x * kGroup);
@@ -275,16 +284,54 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(
     quantize(vU, (nI + (int)blockIdx.x) * kGroup);
   } else {
     v4u v[8];
+    float wv[8];
     const int c0 = blockIdx.x * kQcCols;
+    // Loads are unconditional (out-of-group rows re-read the group's last
+    // row, or row 0 when the group is empty) and zeroed by selects after, so
+    // no control flow separates them and all 8 are in flight at once.
+    int src[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int r = rg * 8 + j;
-      v[j] = v4u{0u, 0u, 0u, 0u};
-      if (r < valid) {
-        const int src = gather ? gather[row0 + r] / gather_div : row0 + r;
-        v[j] = __builtin_nontemporal_load((const v4u*)(x + (size_t)src * C + c0 + cc));
+      src[j] = valid > 0 ? row0 + min(r, valid - 1) : 0;
+    }
+    bool ok[8];
+    if (gather) {
+      // gathered rows whose map entry lies outside [0, R) stay zero
+#pragma unroll
+      for (int j = 0; j < 8; ++j) src[j] = gather[src[j]];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        ok[j] = rg * 8 + j < valid && (unsigned)src[j] < (unsigned)R;
+        src[j] = (unsigned)src[j] < (unsigned)R ? src[j] : 0;
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = *(const v4u*)(x + (size_t)(src[j] / gather_div) * C + c0 + cc);
+      if (gather_w) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) wv[j] = gather_w[src[j]];
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        ok[j] = rg * 8 + j < valid;
+        v[j] = __builtin_nontemporal_load((const v4u*)(x + (size_t)src[j] * C + c0 + cc));
       }
     }
+    if (gather && gather_w) {
+      // the weighted rows bf16(w[p] * x[p / gather_div]), rounded as
+      // combine_bwd_kernel rounds dy
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          v[j][i] = bf16_pack2(wv[j] * __uint_as_float(v[j][i] << 16),
+                               wv[j] * __uint_as_float(v[j][i] & 0xffff0000u));
+    }
+    // rows outside the group are +0 (after the weights: w * +0 can be -0)
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (!ok[j]) v[j] = v4u{0u, 0u, 0u, 0u};
     quantize(v, c0);
   }
 }
@@ -334,11 +381,15 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(const uint16_t* __restr
 // One wave per token: reads dout[t] once, and for each of its K rows writes
 // dy[r] = bf16(w[t,k] * dout[t]) and reduces dw[t,k] = <dout[t], y[r]> in
 // fp32 (lane partials over the row, then a wave tree).
-template <int kMaxK>
+// kQuant: dy is not stored; its 1x128 row quantisation goes to dyq [T*K, H]
+// / dys [T*K, H/128] instead (the 16 lanes that hold a 128-column group
+// share its amax), the bytes smoe_quant_rows_1x128 would write from dy.
+template <int kMaxK, bool kQuant>
 __global__ __launch_bounds__(256) void combine_bwd_kernel(
     const uint16_t* __restrict__ dout, const uint16_t* __restrict__ y,
     const int32_t* __restrict__ inv_map, const float* __restrict__ w, int T, int K, int H,
-    uint16_t* __restrict__ dy, float* __restrict__ dw) {
+    uint16_t* __restrict__ dy, float* __restrict__ dw, uint8_t* __restrict__ dyq,
+    float* __restrict__ dys) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
@@ -381,7 +432,27 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(
         part[k] = part[k] + d[2 * i + 1] * y1;
         o[i] = bf16_pack2(wk[k] * d[2 * i], wk[k] * d[2 * i + 1]);
       }
-      *(uint4*)(dy + (size_t)r[k] * H + col) = make_uint4(o[0], o[1], o[2], o[3]);
+      if constexpr (kQuant) {
+        float m = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          m = fmaxf(m, fabsf(__uint_as_float(o[i] << 16)));
+          m = fmaxf(m, fabsf(__uint_as_float(o[i] & 0xffff0000u)));
+        }
+        const float sc = group_scale(row16_max(m));
+        const QDiv qd = qdiv_setup(sc);
+        float qv[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          qv[2 * i] = quot_bf16(__uint_as_float(o[i] << 16), qd);
+          qv[2 * i + 1] = quot_bf16(__uint_as_float(o[i] & 0xffff0000u), qd);
+        }
+        *(uint2*)(dyq + (size_t)r[k] * H + col) =
+            make_uint2(e4m3_pack4(qv[0], qv[1], qv[2], qv[3]), e4m3_pack4(qv[4], qv[5], qv[6], qv[7]));
+        if ((lane & 15) == 0) dys[(size_t)r[k] * (H / kGroup) + col / kGroup] = sc;
+      } else {
+        *(uint4*)(dy + (size_t)r[k] * H + col) = make_uint4(o[0], o[1], o[2], o[3]);
+      }
     }
   }
 #pragma unroll
@@ -437,7 +508,7 @@ extern "C" int smoe_quant_cols_128x1(const uint16_t* x, const int32_t* gather, i
   pad_offsets_kernel<<<1, 1024, 0, s>>>(offsets, E, pad);
   // column slabs vary fastest, so the workgroups in flight read whole rows
   quant_cols_kernel<false, false><<<dim3((C + kQcCols - 1) / kQcCols, ld / kGroup), dim3(256), 0, s>>>(
-      x, gather, gather ? gather_div : 1, R, C, offsets, pad, E, ld, xTq, xTs, nullptr, nullptr,
+      x, gather, gather ? gather_div : 1, nullptr, R, C, offsets, pad, E, ld, xTq, xTs, nullptr, nullptr,
       nullptr, nullptr, nullptr);
   SMOE_RETURN_LAUNCH();
 }
@@ -460,7 +531,7 @@ extern "C" int smoe_quant_rows_cols(const uint16_t* x, int R, int C, const int32
   hipStream_t s = (hipStream_t)stream;
   pad_offsets_kernel<<<1, 1024, 0, s>>>(offsets, E, pad);
   quant_cols_kernel<true, false><<<dim3((C + kQcCols - 1) / kQcCols, ld / kGroup), dim3(256), 0, s>>>(
-      x, nullptr, 1, R, C, offsets, pad, E, ld, xTq, xTs, xq, xs, nullptr, nullptr, nullptr);
+      x, nullptr, 1, nullptr, R, C, offsets, pad, E, ld, xTq, xTs, xq, xs, nullptr, nullptr, nullptr);
   SMOE_RETURN_LAUNCH();
 }
 
@@ -486,7 +557,7 @@ extern "C" int smoe_swiglu_bwd_quant(const uint16_t* c1, const uint16_t* dh, int
   pad_offsets_kernel<<<1, 1024, 0, s>>>(offsets, E, pad);
   // one workgroup per 128-column block of both halves (dg and du)
   quant_cols_kernel<true, true><<<dim3(I / kQcCols, ld / kGroup), dim3(256), 0, s>>>(
-      nullptr, nullptr, 1, R, C, offsets, pad, E, ld, dcTq, dcTs, dcq, dcs, c1, dh, dc1);
+      nullptr, nullptr, 1, nullptr, R, C, offsets, pad, E, ld, dcTq, dcTs, dcq, dcs, c1, dh, dc1);
   SMOE_RETURN_LAUNCH();
 }
 
@@ -516,10 +587,54 @@ extern "C" int smoe_unpermute_combine_bwd(const uint16_t* dout, const uint16_t* 
   const dim3 grid((T + 3) / 4), block(256);
   hipStream_t s = (hipStream_t)stream;
 #define SMOE_CBB(MK) \
-  combine_bwd_kernel<MK><<<grid, block, 0, s>>>(dout, y, inv_map, w, T, K, H, dy, dw)
+  combine_bwd_kernel<MK, false><<<grid, block, 0, s>>>(dout, y, inv_map, w, T, K, H, dy, dw, \
+                                                       nullptr, nullptr)
   if (K <= 2) SMOE_CBB(2);
   else if (K <= 8) SMOE_CBB(8);
   else SMOE_CBB(32);
 #undef SMOE_CBB
+  SMOE_RETURN_LAUNCH();
+}
+
+extern "C" int smoe_unpermute_combine_bwd_quant(const uint16_t* dout, const uint16_t* y,
+                                                const int32_t* inv_map, const int32_t* row_map,
+                                                const float* w, int T, int K, int H,
+                                                const int32_t* offsets, int E, int ld,
+                                                uint8_t* dyq, float* dys, uint8_t* dyTq,
+                                                float* dyTs, int32_t* pad, float* dw,
+                                                void* stream) {
+  if (T <= 0 || H <= 0) return SMOE_EINVAL_DIM;
+  if (H % kGroup) return SMOE_EINVAL_ALIGN128;
+  if (K <= 0 || K > 32) return SMOE_EINVAL_TOPK;
+  if ((long long)T * K > 0x7fffffffLL) return SMOE_EINVAL_DIM;
+  if (E <= 0 || E > SMOE_MAX_EXPERTS) return SMOE_EINVAL_EXPERTS;
+  const int R = T * K;
+  if (ld < smoe_quant_cols_ld(R, E) || ld % kGroup) return SMOE_EINVAL_DIM;
+  if (ld / kGroup > 65535) return SMOE_EINVAL_DIM;
+  SMOE_CHECK_PTR(dout);
+  SMOE_CHECK_PTR(y);
+  SMOE_CHECK_PTR(dyTq);
+  if (!inv_map || !row_map || !w || !dw || !offsets || !dys || !dyTs || !pad || !dyq)
+    return SMOE_EINVAL_NULL;
+  if (((uintptr_t)inv_map | (uintptr_t)row_map | (uintptr_t)w | (uintptr_t)dw |
+       (uintptr_t)offsets | (uintptr_t)dys | (uintptr_t)dyTs | (uintptr_t)pad) & 3u)
+    return SMOE_EINVAL_PTRALIGN;
+  if ((uintptr_t)dyq & 7u) return SMOE_EINVAL_PTRALIGN;
+  hipStream_t s = (hipStream_t)stream;
+  // dw and the 1x128 rows of dy; dy itself is never stored
+  const dim3 grid((T + 3) / 4), block(256);
+#define SMOE_CBB(MK) \
+  combine_bwd_kernel<MK, true><<<grid, block, 0, s>>>(dout, y, inv_map, w, T, K, H, nullptr, dw, \
+                                                      dyq, dys)
+  if (K <= 2) SMOE_CBB(2);
+  else if (K <= 8) SMOE_CBB(8);
+  else SMOE_CBB(32);
+#undef SMOE_CBB
+  pad_offsets_kernel<<<1, 1024, 0, s>>>(offsets, E, pad);
+  // 128x1 columns: row r of dy is rebuilt as bf16(w[p] * dout[p / K]) with
+  // p = row_map[r]
+  quant_cols_kernel<false, false><<<dim3(H / kQcCols, ld / kGroup), dim3(256), 0, s>>>(
+      dout, row_map, K, w, R, H, offsets, pad, E, ld, dyTq, dyTs, nullptr, nullptr, nullptr,
+      nullptr, nullptr);
   SMOE_RETURN_LAUNCH();
 }

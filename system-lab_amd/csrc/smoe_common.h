@@ -147,6 +147,17 @@ __device__ __forceinline__ float group_max(float v) {
   return v;
 }
 
+// Max over each row of 16 lanes with DPP lane moves (no LDS round trip):
+// swap neighbours, swap pairs, mirror within 8, mirror within 16.  Lanes
+// that are inactive contribute 0, so the inputs must be >= 0 (amax values).
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false)));
+  return v;
+}
+
 __device__ __forceinline__ float wave_sum_tree(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = v + __shfl_xor(v, o, kWave);

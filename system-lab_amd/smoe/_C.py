@@ -45,6 +45,8 @@ SIGNATURES = {
     "smoe_grouped_gemm_fp8_wgrad": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int, P, P]),
     "smoe_swiglu_bwd": (c_int, [P, P, c_int, c_int, P, P]),
     "smoe_unpermute_combine_bwd": (c_int, [P, P, P, P, c_int, c_int, c_int, P, P, P]),
+    "smoe_unpermute_combine_bwd_quant": (c_int, [P, P, P, P, P, c_int, c_int, c_int, P, c_int,
+                                                 c_int, P, P, P, P, P, P, P]),
 }
 
 

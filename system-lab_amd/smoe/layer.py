@@ -86,12 +86,14 @@ class SimpleMoE(nn.Module):
         """Backward of one forward call given its intermediates
         (``forward(..., return_intermediates=True)``) and dout [T,H] bf16.
 
-        combine bwd -> dy quant (1x128 rows and 128x1 columns, one pass) ->
+        combine bwd fused with both quantisations of dy (1x128 rows, 128x1
+        columns; dy never stored) ->
         fc2 dgrad (W2^T) and fc2 wgrad (128x1 dy, h) -> SwiGLU bwd fused with
         both quantisations of dc1 -> fc1 dgrad (W1^T) and fc1 wgrad (128x1
         dc1, sorted x) -> sum of the K replicas into dx.
         Returns dx [T,H] bf16, dw1 [E,2I,H] f32, dw2 [E,H,I] f32 and the
-        router-weight gradient dtopk_w [T,K] f32.  Every stage is a HIP kernel;
+        router-weight gradient dtopk_w [T,K] f32 (plus dy's 1x128 quantisation dyq,
+        dys and the intermediates dh, dxs).  Every stage is a HIP kernel;
         nothing synchronises with the host."""
         w1q, w1s, w2q, w2s = self.fp8_weights()
         if getattr(self, "_fp8_t", None) is None or self._fp8_t[0] is not w1q:
@@ -99,10 +101,10 @@ class SimpleMoE(nn.Module):
         _, w1tq, w1ts, w2tq, w2ts = self._fp8_t
         off, inv = inter["offsets"], inter["inv_map"]
         K = self.top_k
-        dy, dw = ops.unpermute_combine_bwd(dout.contiguous(), inter["y"], inv, inter["topk_w"])
-        # dy and dc1 are quantised both ways (1x128 rows for dgrad, 128x1
-        # columns for wgrad) from a single read each
-        dyq, dys, dyTq, dyTs, pad, ld = ops.quant_rows_cols(dy, off)
+        # combine backward fused with both quantisations of dy (1x128 rows for
+        # dgrad, 128x1 columns for wgrad); dy itself is never stored
+        dyq, dys, dyTq, dyTs, pad, ld, dw = ops.unpermute_combine_bwd_quant(
+            dout.contiguous(), inter["y"], inv, inter["row_map"], inter["topk_w"], off)
         dh = ops.grouped_gemm_fp8(dyq, dys, w2tq, w2ts, off)
         h = inter["h"]
         hTq, hTs, _, _ = ops.quant_cols(h, off)
@@ -116,5 +118,5 @@ class SimpleMoE(nn.Module):
         dw1 = ops.grouped_gemm_fp8_wgrad(dcTq, dcTs, xTq, xTs, pad, ld)
         ones = torch.ones_like(inter["topk_w"])
         dx = ops.unpermute_combine(dxs, inv, ones)
-        return dict(dx=dx, dw1=dw1, dw2=dw2, dtopk_w=dw, dy=dy, dh=dh, dxs=dxs)
+        return dict(dx=dx, dw1=dw1, dw2=dw2, dtopk_w=dw, dyq=dyq, dys=dys, dh=dh, dxs=dxs)
 

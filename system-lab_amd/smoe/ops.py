@@ -379,3 +379,38 @@ def unpermute_combine_bwd(dout: torch.Tensor, y: torch.Tensor, inv_map: torch.Te
     _C.call("smoe_unpermute_combine_bwd", _ptr(dout), _ptr(y), _ptr(inv_map), _ptr(topk_w), T, K,
             H, _ptr(dy), _ptr(dw), _stream())
     return dy, dw
+
+
+def unpermute_combine_bwd_quant(dout: torch.Tensor, y: torch.Tensor, inv_map: torch.Tensor,
+                                row_map: torch.Tensor, topk_w: torch.Tensor,
+                                offsets: torch.Tensor):
+    """Combine backward fused with both quantisations of dy: the bytes of
+    ``quant_rows_cols(unpermute_combine_bwd(...)[0], offsets)`` and dw,
+    without storing dy.  -> (dyq [T*K,H] fp8, dys, dyTq [H,ld] fp8, dyTs,
+    pad, ld, dw [T,K] f32)."""
+    _check(dout, "dout", (torch.bfloat16,), 2)
+    _check(y, "y", (torch.bfloat16,), 2)
+    _check(inv_map, "inv_map", (torch.int32,))
+    _check(row_map, "row_map", (torch.int32,))
+    _check(topk_w, "topk_w", (torch.float32,), 2)
+    _check(offsets, "offsets", (torch.int32,), 1)
+    T, K = topk_w.shape
+    H = dout.shape[1]
+    R = T * K
+    if dout.shape[0] != T or y.shape != (R, H):
+        raise ValueError("dout must be [T, H] and y [T*K, H] for topk_w [T, K]")
+    if inv_map.numel() != R or row_map.numel() != R:
+        raise ValueError("inv_map and row_map must hold T*K entries")
+    E = offsets.numel() - 1
+    ld = int(_C.lib().smoe_quant_cols_ld(R, E))
+    dev = dout.device
+    dyq = torch.empty((R, H), dtype=FP8, device=dev)
+    dys = torch.empty((R, H // GROUP), dtype=torch.float32, device=dev)
+    dyTq = torch.empty((H, ld), dtype=FP8, device=dev)
+    dyTs = torch.empty((H, ld // GROUP), dtype=torch.float32, device=dev)
+    pad = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    dw = torch.empty((T, K), dtype=torch.float32, device=dev)
+    _C.call("smoe_unpermute_combine_bwd_quant", _ptr(dout), _ptr(y), _ptr(inv_map),
+            _ptr(row_map), _ptr(topk_w), T, K, H, _ptr(offsets), E, ld, _ptr(dyq), _ptr(dys),
+            _ptr(dyTq), _ptr(dyTs), _ptr(pad), _ptr(dw), _stream())
+    return dyq, dys, dyTq, dyTs, pad, ld, dw

@@ -144,6 +144,16 @@ def test_remaining_entry_points_reject():
     assert sb(FAKE, FAKE, 1000, 100, FAKE, 4, ld, FAKE, FAKE, FAKE, FAKE, FAKE, None, None) == -3
     assert sb(FAKE, FAKE, 1000, 128, FAKE, 0, ld, FAKE, FAKE, FAKE, FAKE, FAKE, None, None) == -4
     assert sb(FAKE, FAKE, 1000, 128, FAKE, 4, ld, FAKE, FAKE, FAKE, FAKE, FAKE, MIS, None) == -6
+    # fused combine backward + quantiser: H % 128, top-k, experts, ld too small, row_map NULL
+    cq = lib.smoe_unpermute_combine_bwd_quant
+    ld2 = lib.smoe_quant_cols_ld(1000, 4)
+    args = lambda T=500, K=2, H=128, E=4, ld=ld2, rm=FAKE: (
+        FAKE, FAKE, FAKE, rm, FAKE, T, K, H, FAKE, E, ld, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None)
+    assert cq(*args(H=130)) == -3
+    assert cq(*args(K=33)) == -7
+    assert cq(*args(E=0)) == -4
+    assert cq(*args(ld=ld2 - 128)) == -2
+    assert cq(*args(rm=None)) == -1
     # SwiGLU with the bf16 h output: misaligned h; the quantiser self-test
     assert lib.smoe_swiglu_quant_h(FAKE, 10, 128, FAKE, FAKE, MIS, None) == -6
     assert lib.smoe_selftest_quant(None, None) == -1

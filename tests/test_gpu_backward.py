@@ -181,6 +181,41 @@ def test_swiglu_bwd_quant_equals_two_kernels(dev, counts, I):
     assert torch.equal(got[4], ref[4]) and got[5] == ref[5]
 
 
+@pytest.mark.parametrize("T,K,H,E", [(300, 3, 768, 5), (1024, 8, 2048, 128), (513, 1, 256, 4),
+                                     (64, 32, 128, 7)])
+def test_combine_bwd_quant_equals_two_kernels(dev, T, K, H, E):
+    """The fused combine backward + quantiser gives the bytes of
+    unpermute_combine_bwd followed by quant_rows_cols (dy never stored), the
+    same dw, and dy's 1x128 rows match the oracle's."""
+    say("combine_bwd_quant", T, K, H, E)
+    rng = np.random.default_rng(T * K + H)
+    idx = np.stack([rng.permutation(E)[:K] if K <= E else rng.integers(0, E, K)
+                    for _ in range(T)]).astype(np.int32)
+    row_map, inv_map, _, off = O.route_sort(idx, E)
+    R = T * K
+    dout = W.tokens(T, H, seed=21)
+    y = W.tokens(R, H, seed=22)
+    w = torch.from_numpy(rng.random((T, K)).astype(np.float32) * 2 - 0.5)
+    w[0, 0] = 0.0
+    dv, yv, wv = dout.to(dev), y.to(dev), w.to(dev)
+    rm, im, off_t = (torch.from_numpy(a).to(dev) for a in (row_map, inv_map, off))
+    dy, dw = ops.unpermute_combine_bwd(dv, yv, im, wv)
+    ref = ops.quant_rows_cols(dy, off_t)
+    got = ops.unpermute_combine_bwd_quant(dv, yv, im, rm, wv, off_t)
+    Rp = int(ref[4][-1])
+    assert torch.equal(got[0].view(torch.uint8), ref[0].view(torch.uint8))
+    assert torch.equal(got[1].view(torch.int32), ref[1].view(torch.int32))
+    assert torch.equal(got[2].view(torch.uint8)[:, :Rp], ref[2].view(torch.uint8)[:, :Rp])
+    assert torch.equal(got[3][:, :Rp // 128].view(torch.int32), ref[3][:, :Rp // 128].view(torch.int32))
+    assert torch.equal(got[4], ref[4]) and got[5] == ref[5]
+    assert torch.equal(got[6].view(torch.int32), dw.view(torch.int32))
+    # dy rows from the oracle's combine backward, quantised by the oracle
+    ody, odw = O.combine_bwd(u16(dout), u16(y), inv_map, w.numpy(), K)
+    rq, rs = O.quant_1x128(O.bf16_to_f32(ody))
+    assert np.array_equal(u8(got[0]), rq) and np.array_equal(got[1].cpu().numpy(), rs)
+    close(got[6].cpu().numpy(), odw, "dw")
+
+
 def test_quant_cols_gather_bit_exact(dev):
     say("quant_cols gather")
     rng = np.random.default_rng(3)
@@ -331,7 +366,8 @@ def test_layer_backward_end_to_end(dev, T, H, I, E, K):
     m, x, st, dout, fwd, r = _layer_case(dev, T, H, I, E, K)
     g = m.backward_from(st, dout.to(dev))
     f = lambda a: O.bf16_to_f32(a).astype(np.float64)
-    assert np.array_equal(u16(g["dy"]), r["dy"])
+    dyq, dys = O.quant_1x128(O.bf16_to_f32(r["dy"]))
+    assert np.array_equal(u8(g["dyq"]), dyq) and np.array_equal(g["dys"].cpu().numpy(), dys)
     close(g["dw2"].cpu().numpy(), r["dW2"], "dW2")
     close(g["dw1"].cpu().numpy(), r["dW1"], "dW1", mx_tol=2e-2)
     close(f(u16(g["dx"])), f(r["dx"]), "dx", mx_tol=2e-2)
