@@ -101,22 +101,43 @@ class SimpleMoE(nn.Module):
         _, w1tq, w1ts, w2tq, w2ts = self._fp8_t
         off, inv = inter["offsets"], inter["inv_map"]
         K = self.top_k
+        # The weight gradients are off the dx critical path.  They run on a
+        # second stream (default priority), so that a wgrad tile writing its
+        # fp32 output shares the chip with dgrad tiles that are MFMA-bound.
+        # Every side-stream segment starts by waiting for the main stream, and
+        # the main stream waits for the side stream before returning.
+        main = torch.cuda.current_stream()
+        side = self._side_stream(main.device)
+        ones = torch.ones_like(inter["topk_w"])
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            # the wgrad activation operands depend on the forward only: h, and
+            # the sorted tokens x[row_map // K] gathered inside the quantiser
+            hTq, hTs, _, _ = ops.quant_cols(inter["h"], off)
+            xTq, xTs, _, _ = ops.quant_cols(inter["x"], off, gather=inter["row_map"], gather_div=K)
         # combine backward fused with both quantisations of dy (1x128 rows for
         # dgrad, 128x1 columns for wgrad); dy itself is never stored
         dyq, dys, dyTq, dyTs, pad, ld, dw = ops.unpermute_combine_bwd_quant(
             dout.contiguous(), inter["y"], inv, inter["row_map"], inter["topk_w"], off)
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            dw2 = ops.grouped_gemm_fp8_wgrad(dyTq, dyTs, hTq, hTs, pad, ld)
         dh = ops.grouped_gemm_fp8(dyq, dys, w2tq, w2ts, off)
-        h = inter["h"]
-        hTq, hTs, _, _ = ops.quant_cols(h, off)
-        dw2 = ops.grouped_gemm_fp8_wgrad(dyTq, dyTs, hTq, hTs, pad, ld)
         # SwiGLU backward fused with both quantisations of dc1 (dc1 itself is
         # never stored)
         dcq, dcs, dcTq, dcTs, _, _ = ops.swiglu_bwd_quant(inter["c1"], dh, off)
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            dw1 = ops.grouped_gemm_fp8_wgrad(dcTq, dcTs, xTq, xTs, pad, ld)
         dxs = ops.grouped_gemm_fp8(dcq, dcs, w1tq, w1ts, off)
-        # the sorted tokens x[row_map // K], gathered inside the quantiser
-        xTq, xTs, _, _ = ops.quant_cols(inter["x"], off, gather=inter["row_map"], gather_div=K)
-        dw1 = ops.grouped_gemm_fp8_wgrad(dcTq, dcTs, xTq, xTs, pad, ld)
-        ones = torch.ones_like(inter["topk_w"])
         dx = ops.unpermute_combine(dxs, inv, ones)
+        main.wait_stream(side)
         return dict(dx=dx, dw1=dw1, dw2=dw2, dtopk_w=dw, dyq=dyq, dys=dys, dh=dh, dxs=dxs)
+
+    def _side_stream(self, device) -> torch.cuda.Stream:
+        s = getattr(self, "_side", None)
+        if s is None or s.device != device:
+            s = torch.cuda.Stream(device=device)  # default priority
+            self._side = s
+        return s
 
