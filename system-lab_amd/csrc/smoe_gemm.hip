@@ -26,7 +26,7 @@
 // padded to kChipM) times the n-tiles.  Tiles are taken in chip-wide groups
 // of kChipM consecutive m-tiles x all n-tiles; within a group, XCD x (blocks
 // are dealt to the 8 XCDs round robin) takes m-tiles x*kChipM/8 .. +kChipM/8
-// and sweeps the n-tiles.  All XCDs then stream the same weight slices at
+// and sweeps the n-tiles, m fastest.  All XCDs then stream the same weight slices at
 // once (read from HBM once, the other XCDs hit the last-level cache), and
 // each XCD's L2 serves its own activation rows to all n-tiles.  A last,
 // partial group's tiles are split evenly over the 8 XCDs instead.  Every
@@ -38,7 +38,9 @@
 
 namespace smoe {
 
-constexpr int kChipM = 16;  // m-tiles per chip-wide scheduling group (2 per XCD)
+// m-tiles per chip-wide scheduling group: 4 per XCD, so an XCD's 32 CUs run
+// 4 m-tiles x 8 n-tiles at once (12 distinct operand slices per K step)
+constexpr int kChipM = 32;
 
 // Tile configuration: waves form a kWR (rows) x kWN (columns) grid; each wave
 // owns kRB 16-row blocks x 4 16-column blocks (kRB*16 rows x 64 columns).

@@ -1,6 +1,6 @@
 """CPU model of the grouped GEMM's tile mapping and address arithmetic
 (system-lab_amd/csrc/smoe_gemm.hip, Cfg<2,4,8,2>: 256x256 tiles, chip-wide
-groups of 16 m-tiles, 8 waves loading 1 KiB segments).  It checks, without a
+groups of 32 m-tiles, 8 waves loading 1 KiB segments).  It checks, without a
 GPU, that every real (m-tile, n-tile) is produced by exactly one workgroup,
 and that every activation, scale, weight and output access of every lane
 stays inside its buffer, for valid offsets and for malformed ones
@@ -8,7 +8,7 @@ stays inside its buffer, for valid offsets and for malformed ones
 import numpy as np
 
 BM = BN = 256
-CHIP_M, XM, BK = 16, 2, 128
+CHIP_M, XM, BK = 32, 4, 128
 LANES = np.arange(64)
 
 
