@@ -90,7 +90,7 @@ def e4m3_encode(v: np.ndarray) -> np.ndarray:
     return (q | sign).astype(np.uint8)
 
 
-def e4m3_decode(q: np.ndarray) -> np.ndarray:
+def _e4m3_decode_formula(q: np.ndarray) -> np.ndarray:
     """OCP e4m3fn byte -> float32 (0x7f / 0xff -> NaN)."""
     q = np.asarray(q, dtype=np.uint8).astype(np.int32)
     s = np.where(q & 0x80, -1.0, 1.0)
@@ -100,6 +100,15 @@ def e4m3_decode(q: np.ndarray) -> np.ndarray:
     out = (s * mag).astype(np.float32)
     out[(q & 0x7F) == 0x7F] = np.nan
     return out
+
+
+_E4M3_TABLE = _e4m3_decode_formula(np.arange(256))
+
+
+def e4m3_decode(q: np.ndarray) -> np.ndarray:
+    """OCP e4m3fn byte -> float32 (0x7f / 0xff -> NaN): the formula above,
+    tabulated once for all 256 codes and applied by lookup."""
+    return _E4M3_TABLE[np.asarray(q, dtype=np.uint8)]
 
 
 def quant_rule(x: np.ndarray, s: np.ndarray) -> np.ndarray:

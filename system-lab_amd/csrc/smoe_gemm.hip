@@ -73,7 +73,7 @@ struct Cfg {
 // when not null.  h is computed from the bf16-rounded fc1 values exactly as
 // the stand-alone SwiGLU kernel does, so the fused path is bit-identical to
 // GEMM -> bf16 c1 -> swiglu_quant.
-template <class C, bool kSwiGLU>
+template <class C, bool kSwiGLU, bool kChunkS>
 __global__ __launch_bounds__(C::kThreads, 1) void grouped_gemm_fp8_kernel(
     const uint8_t* __restrict__ a, const float* __restrict__ as, const uint8_t* __restrict__ b,
     const float* __restrict__ bs, const int32_t* __restrict__ offsets, int E, int R, int N,
@@ -84,7 +84,15 @@ __global__ __launch_bounds__(C::kThreads, 1) void grouped_gemm_fp8_kernel(
   constexpr int kStages = C::kStages, kABytes = C::kABytes, kBBytes = C::kBBytes;
   constexpr int kASegs = C::kASegs, kBSegs = C::kBSegs, kRB = C::kRB;
   constexpr int kCPitch = kBN * 2 + 16;  // bytes per staged output row (+16: banks)
-  constexpr int kSmem = kStages * kStage > kBM * kCPitch ? kStages * kStage : kBM * kCPitch;
+  // kChunkS: the activation scales are staged kSChunk K steps at a time in a
+  // double-buffered area after the stages, instead of 256 words per step.
+  constexpr int kSChunk = 8;
+  constexpr int kSC0 = kStages * kStage;                 // scale chunk area
+  constexpr int kSCBytes = kBM * kSChunk * 4;            // one chunk
+  constexpr int kLoop = kSC0 + (kChunkS ? 2 * kSCBytes : 0);
+  constexpr int kSmem = kLoop > kBM * kCPitch ? kLoop : kBM * kCPitch;
+  static_assert(kSmem + 4200 <= 160 * 1024, "LDS budget");
+  static_assert(!kChunkS || kSCBytes == C::kWaves * 1024, "one 1 KiB scale DMA per wave and chunk");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kSmem];
   __shared__ int mstart[SMOE_MAX_EXPERTS + 1];
   __shared__ int wsum[kThreads / kWave];
@@ -193,6 +201,11 @@ __global__ __launch_bounds__(C::kThreads, 1) void grouped_gemm_fp8_kernel(
     }
   }
   const uint32_t os = (uint32_t)(min((wid % C::kSWaves) * 64 + lane, rows - 1) * ksb) * 4u;
+  // scale chunk DMA: lane l of wave w moves 16 bytes (4 K steps) of tile row
+  // w*32 + l/2 into LDS row-major [kBM][kSChunk]; with ksb a multiple of
+  // kSChunk every read stays inside its row.
+  const uint32_t osc =
+      (uint32_t)(min(wid * 32 + (lane >> 1), rows - 1) * ksb) * 4u + (uint32_t)(lane & 1) * 16u;
   const int wr = wid / C::kWN, wn = wid % C::kWN;
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_ptr_t)smem;
 
@@ -216,10 +229,14 @@ __global__ __launch_bounds__(C::kThreads, 1) void grouped_gemm_fp8_kernel(
   };
   auto issue = [&](int kb, int buf) {
 #pragma unroll
-    for (int q = 0; q < kDma; ++q) issue_one(q, kb, buf);
+    for (int q = kChunkS ? 1 : 0; q < kDma; ++q) issue_one(q, kb, buf);
+  };
+  const uint32_t sc_lds = __builtin_amdgcn_readfirstlane(lds0 + kSC0 + wid * 1024);
+  auto issue_sc = [&](int chunk) {
+    dma16(s_base + chunk * kSChunk, osc, sc_lds + (chunk & 1) * kSCBytes);
   };
   // loads one stage leaves outstanding per wave (waves 0-3 also load scales)
-  const bool scale_wave = wid < C::kSWaves;
+  const bool scale_wave = !kChunkS && wid < C::kSWaves;
 
   const int frow = lane & 15;
   const int fch = (lane >> 4) * 2;
@@ -231,6 +248,7 @@ __global__ __launch_bounds__(C::kThreads, 1) void grouped_gemm_fp8_kernel(
     for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 
   // prologue: stages 0 .. kStages-2 in flight, stage 0 landed
+  if constexpr (kChunkS) issue_sc(0);
 #pragma unroll
   for (int s = 0; s < kStages - 1; ++s)
     if (s < ksb) issue(s, s);
@@ -261,10 +279,14 @@ __global__ __launch_bounds__(C::kThreads, 1) void grouped_gemm_fp8_kernel(
   for (int kb = 0; kb < ksb; ++kb) {
     // refill the slot consumed in the previous step (free after its barrier)
     const int nxt = kb + kStages - 1;
+    // the next scale chunk goes out at the first step of the current one, into
+    // the half whose chunk was last read before the previous barrier
+    if (kChunkS && (kb & (kSChunk - 1)) == 0 && kb + kSChunk < ksb) issue_sc(kb / kSChunk + 1);
     if (nxt < ksb) issue(nxt, nxt % kStages);
     const uint8_t* sA = smem + buf * kStage;
     const uint8_t* sB = sA + kABytes;
     const float* sS = (const float*)(sB + kBBytes);
+    const float* sC = (const float*)(smem + kSC0 + ((kb / kSChunk) & 1) * kSCBytes) + (kb & (kSChunk - 1));
     const float sb = sb_row[kb];
     v8i fw[4];
 #pragma unroll
@@ -277,7 +299,7 @@ __global__ __launch_bounds__(C::kThreads, 1) void grouped_gemm_fp8_kernel(
     for (int i = 0; i < kRB; ++i) {
       v8i fxn = fx;
       if (i + 1 < kRB) fxn = lds_frag(sA, rbase + (i + 1) * 16, fch);
-      const float sc = sS[rbase + i * 16] * sb;
+      const float sc = (kChunkS ? sC[(rbase + i * 16) * kSChunk] : sS[rbase + i * 16]) * sb;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const v4f p = mfma16(fw[j], fx, v4f{0.0f, 0.0f, 0.0f, 0.0f});
@@ -389,9 +411,14 @@ extern "C" int smoe_grouped_gemm_fp8(const uint8_t* a, const float* as, const ui
   long long nblk = mt_pad * NT;
   nblk = (nblk + 7) / 8 * 8;
   if (nblk > 0x7fffffffLL) return SMOE_EINVAL_DIM;
-  grouped_gemm_fp8_kernel<C, false>
-      <<<dim3((unsigned)nblk), dim3(C::kThreads), 0, (hipStream_t)stream>>>(
-          a, as, b, bs, offsets, E, R, N, Kdim, (int)mt_bound, c, nullptr, nullptr);
+  if (Kdim % (kBK * 8) == 0)
+    grouped_gemm_fp8_kernel<C, false, true>
+        <<<dim3((unsigned)nblk), dim3(C::kThreads), 0, (hipStream_t)stream>>>(
+            a, as, b, bs, offsets, E, R, N, Kdim, (int)mt_bound, c, nullptr, nullptr);
+  else
+    grouped_gemm_fp8_kernel<C, false, false>
+        <<<dim3((unsigned)nblk), dim3(C::kThreads), 0, (hipStream_t)stream>>>(
+            a, as, b, bs, offsets, E, R, N, Kdim, (int)mt_bound, c, nullptr, nullptr);
   SMOE_RETURN_LAUNCH();
 }
 
@@ -420,8 +447,13 @@ extern "C" int smoe_grouped_gemm_fp8_swiglu(const uint8_t* a, const float* as, c
   long long nblk = mt_pad * NT;
   nblk = (nblk + 7) / 8 * 8;
   if (nblk > 0x7fffffffLL) return SMOE_EINVAL_DIM;
-  grouped_gemm_fp8_kernel<C, true>
-      <<<dim3((unsigned)nblk), dim3(C::kThreads), 0, (hipStream_t)stream>>>(
-          a, as, w1, w1s, offsets, E, R, N, Kdim, (int)mt_bound, c1, hq, hs);
+  if (Kdim % (kBK * 8) == 0)
+    grouped_gemm_fp8_kernel<C, true, true>
+        <<<dim3((unsigned)nblk), dim3(C::kThreads), 0, (hipStream_t)stream>>>(
+            a, as, w1, w1s, offsets, E, R, N, Kdim, (int)mt_bound, c1, hq, hs);
+  else
+    grouped_gemm_fp8_kernel<C, true, false>
+        <<<dim3((unsigned)nblk), dim3(C::kThreads), 0, (hipStream_t)stream>>>(
+            a, as, w1, w1s, offsets, E, R, N, Kdim, (int)mt_bound, c1, hq, hs);
   SMOE_RETURN_LAUNCH();
 }

@@ -284,10 +284,14 @@ def test_gemm_layout_one_hot(dev):
     assert bad.size == 0, f"{len(bad)} mismatches, first (r,n): {bad[:8].tolist()}"
 
 
-def test_gemm_scale_indexing(dev):
-    say("gemm scale indexing")
+@pytest.mark.parametrize("Kd", [512, 3072])
+def test_gemm_scale_indexing(dev, Kd):
+    """Distinct scales per (row, K block) and per (expert, n block, K block).
+    Kd = 3072 takes the kernel path that stages activation scales 8 K blocks
+    at a time (3 chunks: both halves of the chunk buffer and a reuse)."""
+    say("gemm scale indexing", Kd)
     rng = np.random.default_rng(21)
-    R, N, Kd, E = 200, 384, 512, 2
+    R, N, E = 200, 384, 2
     xq, xs, wq, ws = _fp8_operands(rng, R, N, Kd, E)
     xs = rng.random(xs.shape).astype(np.float32) + 0.5      # distinct per (r, kb)
     ws = rng.random(ws.shape).astype(np.float32) + 0.5      # distinct per (e, nb, kb)
@@ -299,7 +303,8 @@ def test_gemm_scale_indexing(dev):
 @pytest.mark.parametrize("counts,N,Kd", [([5, 0, 300, 1, 0, 129, 128, 17], 256, 512),
                                          ([0, 0, 1000], 512, 1024),
                                          ([1], 128, 128),
-                                         ([4096, 0, 0, 3], 1024, 2048)])
+                                         ([4096, 0, 0, 3], 1024, 2048),
+                                         ([700, 0, 33, 1], 384, 3072)])
 def test_gemm_skewed_experts(dev, counts, N, Kd):
     say("gemm skewed", counts, N, Kd)
     rng = np.random.default_rng(sum(counts) + N)
@@ -384,9 +389,10 @@ def test_gemm_dsv3_shape_sampled_rows(dev):
         aq_np, as_np = np_u8(a_q[torch.from_numpy(rows).to(dev)]), a_s[torch.from_numpy(rows).to(dev)].cpu().numpy()
         wq_np, ws_np = np_u8(wq), ws.cpu().numpy()
         ref = np.zeros_like(got)
-        for i, r in enumerate(rows):
-            e = int(np.searchsorted(offs, r, side="right") - 1)
-            ref[i] = O.dequant_rows(aq_np[i:i + 1], as_np[i:i + 1]) @ O.dequant_weight(wq_np[e], ws_np[e]).T
+        owner = np.searchsorted(offs, rows, side="right") - 1
+        for e in np.unique(owner):
+            sel = owner == e
+            ref[sel] = O.dequant_rows(aq_np[sel], as_np[sel]) @ O.dequant_weight(wq_np[e], ws_np[e]).T
         gemm_close(got, ref, f"dsv3 N={N} K={Kd}")
         del wq, ws, out
         torch.cuda.empty_cache()
