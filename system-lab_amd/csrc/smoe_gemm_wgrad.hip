@@ -14,27 +14,33 @@
 // operand, so an output lane holds one k (lane % 16) and four consecutive n.
 // Both scales vary per row and group, so each partial is multiplied by
 // sa[n,g]*sb[k,g] before accumulation (the product is formed before the
-// MFMA result arrives, leaving one FMA per output after it).  Operands and both scale vectors of a
-// group are staged by direct global->LDS DMA, two stages deep, as in the
-// forward grouped GEMM.
+// MFMA result arrives, leaving one FMA per output after it).  Operands are
+// staged by direct global->LDS DMA, two stages deep, as in the forward
+// grouped GEMM; both scale vectors are staged 8 row groups at a time.
 #include "smoe_mfma.h"
 
 namespace smoe {
 
 // Tile: 256 (n, aT rows) x 256 (k, bT rows) per workgroup of 8 waves in a
 // 2 (k) x 4 (n) grid; each wave owns 128 k x 64 n = 8 x 4 blocks of the
-// 16x16 MFMA.  Stage = aT tile | bT tile | aT scales | bT scales.
+// 16x16 MFMA.  Stage = aT tile | bT tile.
 constexpr int kWN = 256, kWK = 256;
 constexpr int kWThreads = 512;
 constexpr int kWA = kWN * kRow;  // 32 KiB of aT
 constexpr int kWB = kWK * kRow;  // 32 KiB of bT
-constexpr int kWStage = kWA + kWB + (kWN + kWK) * 4;
+constexpr int kWStage = kWA + kWB;
+// Both operands' 128x1 scales are staged kWChunk row groups at a time:
+// [kWN + kWK rows][kWChunk] fp32 per chunk, double-buffered after the stages.
+constexpr int kWChunk = 8;
+constexpr int kWSC = (kWN + kWK) * kWChunk * 4;  // 16 KiB per chunk
+constexpr int kWSmem = 2 * kWStage + 2 * kWSC;
+static_assert(kWSmem <= 160 * 1024, "LDS budget");
 
 __global__ __launch_bounds__(kWThreads, 1) void grouped_gemm_fp8_wgrad_kernel(
     const uint8_t* __restrict__ aT, const float* __restrict__ aTs, const uint8_t* __restrict__ bT,
     const float* __restrict__ bTs, const int32_t* __restrict__ pad, int N, int Kd, int ld,
     float* __restrict__ dW) {
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * kWStage];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kWSmem];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int e = blockIdx.z;
   const int n0 = blockIdx.y * kWN, k0 = blockIdx.x * kWK;
@@ -45,8 +51,7 @@ __global__ __launch_bounds__(kWThreads, 1) void grouped_gemm_fp8_wgrad_kernel(
   const int sld = ld / kGroup;  // scale row length
 
   // DMA per wave and stage: aT segments w*4..w*4+3, bT segments w*4..w*4+3
-  // (8 rows of 128 bytes each); waves 0-3 load 64 aT scales each, waves 4-7
-  // 64 bT scales each.
+  // (8 rows of 128 bytes each).
   uint32_t oa[4], ob[4];
   const int slot = lane & 7;
 #pragma unroll
@@ -55,15 +60,10 @@ __global__ __launch_bounds__(kWThreads, 1) void grouped_gemm_fp8_wgrad_kernel(
     oa[j] = (uint32_t)(min(row, nrows - 1) * ld + ((slot ^ (row & 7)) << 4));
     ob[j] = (uint32_t)(min(row, krows - 1) * ld + ((slot ^ (row & 7)) << 4));
   }
-  const int srow = (wid & 3) * 64 + lane;
-  const uint32_t os = (uint32_t)(min(srow, (wid < 4 ? nrows : krows) - 1) * sld) * 4u;
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_ptr_t)smem;
   // wave-uniform LDS destinations, computed once into scalar registers
   const uint32_t a_lds = __builtin_amdgcn_readfirstlane(lds0 + wid * 4 * 1024);
   const uint32_t b_lds = __builtin_amdgcn_readfirstlane(lds0 + kWA + wid * 4 * 1024);
-  const uint32_t s_lds = __builtin_amdgcn_readfirstlane(
-      lds0 + kWA + kWB + (wid < 4 ? 0 : kWN * 4) + (wid & 3) * 256);
-  const float* sbase = uniform_ptr(wid < 4 ? aTs + (size_t)n0 * sld : bTs + (size_t)k0 * sld);
   auto issue = [&](int st_idx, int buf) {
     const uint32_t st = buf * kWStage;
     const int r0 = g0 + st_idx * kGroup;
@@ -73,7 +73,24 @@ __global__ __launch_bounds__(kWThreads, 1) void grouped_gemm_fp8_wgrad_kernel(
     for (int j = 0; j < 4; ++j) dma16(ab, oa[j], a_lds + st + j * 1024);
 #pragma unroll
     for (int j = 0; j < 4; ++j) dma16(bb, ob[j], b_lds + st + j * 1024);
-    dma4(sbase + r0 / kGroup, os, s_lds + st);
+  };
+  // Scale chunk c (row groups g0/128 + 8c .. +8): waves 0-3 take aT rows
+  // (wid&3)*64 .., waves 4-7 bT rows; instruction i moves 8 rows x 8
+  // consecutive words (lane -> row i*8 + lane/8, group lane%8), so each
+  // instruction touches 8 short row segments instead of 64 rows.  Columns
+  // past the row end are clamped (their values are never used).
+  const float* sbase = uniform_ptr(wid < 4 ? aTs + (size_t)n0 * sld : bTs + (size_t)k0 * sld);
+  const int srows = wid < 4 ? nrows : krows;
+  const uint32_t sc_lds =
+      __builtin_amdgcn_readfirstlane(lds0 + 2 * kWStage + wid * 64 * kWChunk * 4);
+  auto issue_sc = [&](int chunk) {
+    const int col = min(g0 / kGroup + chunk * kWChunk + (lane & 7), sld - 1);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int row = min((wid & 3) * 64 + i * 8 + (lane >> 3), srows - 1);
+      dma4(sbase, (uint32_t)(row * sld + col) * 4u,
+           sc_lds + (chunk & 1) * kWSC + i * 8 * kWChunk * 4);
+    }
   };
 
   const int wk = wid >> 2, wn = wid & 3;  // wave's k half and n quarter
@@ -86,6 +103,7 @@ __global__ __launch_bounds__(kWThreads, 1) void grouped_gemm_fp8_wgrad_kernel(
     for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 
   if (steps > 0) {
+    issue_sc(0);
     issue(0, 0);
     __builtin_amdgcn_s_waitcnt(0);
     __builtin_amdgcn_s_barrier();
@@ -93,30 +111,36 @@ __global__ __launch_bounds__(kWThreads, 1) void grouped_gemm_fp8_wgrad_kernel(
   }
   for (int st = 0; st < steps; ++st) {
     const int buf = st & 1;
+    // the next scale chunk goes out at the first step of the current one,
+    // into the half whose chunk was last read before the previous barrier
+    if ((st & (kWChunk - 1)) == 0 && st + kWChunk < steps) issue_sc(st / kWChunk + 1);
     if (st + 1 < steps) issue(st + 1, buf ^ 1);
     const uint8_t* sA = smem + buf * kWStage;
     const uint8_t* sB = sA + kWA;
-    const float* sSa = (const float*)(sB + kWB);
-    const float* sSb = sSa + kWN;
+    const float* sSa = (const float*)(smem + 2 * kWStage + ((st / kWChunk) & 1) * kWSC) +
+                       (st & (kWChunk - 1));
+    const float* sSb = sSa + kWN * kWChunk;
     v8i fa[4];
     v4f sa[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       fa[j] = lds_frag(sA, wn * 64 + j * 16 + frow, fch);
-      sa[j] = *(const v4f*)(sSa + wn * 64 + j * 16 + (lane >> 4) * 4);
+      const int r = wn * 64 + j * 16 + (lane >> 4) * 4;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) sa[j][v] = sSa[(r + v) * kWChunk];
     }
     // the next row block's fragment and scale are read before this block's
     // MFMAs are issued, so their LDS latency hides behind them
     const int kr0 = wk * 128 + frow;
     v8i fb = lds_frag(sB, kr0, fch);
-    float sb = sSb[kr0];
+    float sb = sSb[kr0 * kWChunk];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       v8i fbn = fb;
       float sbn = sb;
       if (i + 1 < 8) {
         fbn = lds_frag(sB, kr0 + (i + 1) * 16, fch);
-        sbn = sSb[kr0 + (i + 1) * 16];
+        sbn = sSb[(kr0 + (i + 1) * 16) * kWChunk];
       }
       // the scale products do not depend on the MFMA results: computing them
       // first leaves one FMA per output after each MFMA
@@ -146,7 +170,7 @@ __global__ __launch_bounds__(kWThreads, 1) void grouped_gemm_fp8_wgrad_kernel(
   // written once here and read by a later kernel).
   float* ct = (float*)smem;
   constexpr int kPitch = kWK + 4;
-  static_assert(128 * kPitch * 4 <= 2 * kWStage, "epilogue half-tile fits the stage buffers");
+  static_assert(128 * kPitch * 4 <= kWSmem, "epilogue half-tile fits the LDS buffers");
 #pragma unroll
   for (int half = 0; half < 2; ++half) {
     if ((wn >> 1) == half) {
