@@ -84,8 +84,9 @@ __global__ __launch_bounds__(C::kThreads, 1) void grouped_gemm_fp8_kernel(
   constexpr int kStages = C::kStages, kABytes = C::kABytes, kBBytes = C::kBBytes;
   constexpr int kASegs = C::kASegs, kBSegs = C::kBSegs, kRB = C::kRB;
   constexpr int kCPitch = kBN * 2 + 16;  // bytes per staged output row (+16: banks)
-  // kChunkS: the activation scales are staged kSChunk K steps at a time in a
-  // double-buffered area after the stages, instead of 256 words per step.
+  // kChunkS (K a multiple of 512): the activation scales are staged kSChunk K
+  // steps at a time in a double-buffered area after the stages, instead of
+  // 256 words per step.
   constexpr int kSChunk = 8;
   constexpr int kSC0 = kStages * kStage;                 // scale chunk area
   constexpr int kSCBytes = kBM * kSChunk * 4;            // one chunk
@@ -202,10 +203,11 @@ __global__ __launch_bounds__(C::kThreads, 1) void grouped_gemm_fp8_kernel(
   }
   const uint32_t os = (uint32_t)(min((wid % C::kSWaves) * 64 + lane, rows - 1) * ksb) * 4u;
   // scale chunk DMA: lane l of wave w moves 16 bytes (4 K steps) of tile row
-  // w*32 + l/2 into LDS row-major [kBM][kSChunk]; with ksb a multiple of
-  // kSChunk every read stays inside its row.
-  const uint32_t osc =
-      (uint32_t)(min(wid * 32 + (lane >> 1), rows - 1) * ksb) * 4u + (uint32_t)(lane & 1) * 16u;
+  // w*32 + l/2 into LDS row-major [kBM][kSChunk].  ksb is a multiple of 4, so
+  // each 16-byte half of a chunk row lies wholly inside or wholly past the
+  // row's end; a half past the end (the last chunk when ksb % 8 == 4) re-reads
+  // the first half instead, and its values are never used.
+  const uint32_t osc = (uint32_t)(min(wid * 32 + (lane >> 1), rows - 1) * ksb) * 4u;
   const int wr = wid / C::kWN, wn = wid % C::kWN;
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_ptr_t)smem;
 
@@ -233,7 +235,8 @@ __global__ __launch_bounds__(C::kThreads, 1) void grouped_gemm_fp8_kernel(
   };
   const uint32_t sc_lds = __builtin_amdgcn_readfirstlane(lds0 + kSC0 + wid * 1024);
   auto issue_sc = [&](int chunk) {
-    dma16(s_base + chunk * kSChunk, osc, sc_lds + (chunk & 1) * kSCBytes);
+    const bool second = (lane & 1) && (chunk + 1) * kSChunk <= ksb;
+    dma16(s_base + chunk * kSChunk, osc + (second ? 16u : 0u), sc_lds + (chunk & 1) * kSCBytes);
   };
   // loads one stage leaves outstanding per wave (waves 0-3 also load scales)
   const bool scale_wave = !kChunkS && wid < C::kSWaves;
@@ -411,7 +414,7 @@ extern "C" int smoe_grouped_gemm_fp8(const uint8_t* a, const float* as, const ui
   long long nblk = mt_pad * NT;
   nblk = (nblk + 7) / 8 * 8;
   if (nblk > 0x7fffffffLL) return SMOE_EINVAL_DIM;
-  if (Kdim % (kBK * 8) == 0)
+  if (Kdim % (kBK * 4) == 0)
     grouped_gemm_fp8_kernel<C, false, true>
         <<<dim3((unsigned)nblk), dim3(C::kThreads), 0, (hipStream_t)stream>>>(
             a, as, b, bs, offsets, E, R, N, Kdim, (int)mt_bound, c, nullptr, nullptr);
@@ -447,7 +450,7 @@ extern "C" int smoe_grouped_gemm_fp8_swiglu(const uint8_t* a, const float* as, c
   long long nblk = mt_pad * NT;
   nblk = (nblk + 7) / 8 * 8;
   if (nblk > 0x7fffffffLL) return SMOE_EINVAL_DIM;
-  if (Kdim % (kBK * 8) == 0)
+  if (Kdim % (kBK * 4) == 0)
     grouped_gemm_fp8_kernel<C, true, true>
         <<<dim3((unsigned)nblk), dim3(C::kThreads), 0, (hipStream_t)stream>>>(
             a, as, w1, w1s, offsets, E, R, N, Kdim, (int)mt_bound, c1, hq, hs);

@@ -284,11 +284,13 @@ def test_gemm_layout_one_hot(dev):
     assert bad.size == 0, f"{len(bad)} mismatches, first (r,n): {bad[:8].tolist()}"
 
 
-@pytest.mark.parametrize("Kd", [512, 3072])
+@pytest.mark.parametrize("Kd", [384, 512, 1536, 3072])
 def test_gemm_scale_indexing(dev, Kd):
     """Distinct scales per (row, K block) and per (expert, n block, K block).
-    Kd = 3072 takes the kernel path that stages activation scales 8 K blocks
-    at a time (3 chunks: both halves of the chunk buffer and a reuse)."""
+    Kd = 384 reads the activation scales one K block at a time; the others
+    stage them 8 K blocks at a time: 512 (one chunk, its second half past the
+    row end), 1536 (two chunks, the last one half full) and 3072 (3 chunks:
+    both halves of the chunk buffer and a reuse)."""
     say("gemm scale indexing", Kd)
     rng = np.random.default_rng(21)
     R, N, E = 200, 384, 2
