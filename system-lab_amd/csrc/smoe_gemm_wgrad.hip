@@ -38,12 +38,21 @@ static_assert(kWSmem <= 160 * 1024, "LDS budget");
 
 __global__ __launch_bounds__(kWThreads, 1) void grouped_gemm_fp8_wgrad_kernel(
     const uint8_t* __restrict__ aT, const float* __restrict__ aTs, const uint8_t* __restrict__ bT,
-    const float* __restrict__ bTs, const int32_t* __restrict__ pad, int N, int Kd, int ld,
+    const float* __restrict__ bTs, const int32_t* __restrict__ pad, int E, int N, int Kd, int ld,
     float* __restrict__ dW) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kWSmem];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int e = blockIdx.z;
-  const int n0 = blockIdx.y * kWN, k0 = blockIdx.x * kWK;
+  // XCD-aware tile order: workgroups are dealt to the 8 XCDs round robin, so
+  // XCD x runs experts x, x+8, ... and all NT x KT tiles of one expert before
+  // the next.  An XCD's L2 then serves each aT and bT block to every tile of
+  // the expert that reads it (about 14 distinct 32 KiB slices per K step for
+  // its 32 CUs at config 5, against 37 when the k-tile was the fastest index).
+  const int KT = (Kd + kWK - 1) / kWK, NT = (N + kWN - 1) / kWN;
+  const int xcd = blockIdx.x & 7, tslot = blockIdx.x >> 3;
+  const int e = (tslot / (NT * KT)) * 8 + xcd;
+  if (e >= E) return;  // the whole workgroup leaves together
+  const int rem = tslot % (NT * KT);
+  const int n0 = (rem / KT) * kWN, k0 = (rem % KT) * kWK;
   // operand columns outside [0, ld) are never read, whatever pad[] holds
   const int g0 = max(pad[e], 0), g1 = min(pad[e + 1], ld);
   const int steps = g1 > g0 ? (g1 - g0) / kGroup : 0;
@@ -213,8 +222,11 @@ extern "C" int smoe_grouped_gemm_fp8_wgrad(const uint8_t* aT, const float* aTs,
   SMOE_CHECK_PTR(dW);
   if (!aTs || !bTs || !pad) return SMOE_EINVAL_NULL;
   if (((uintptr_t)aTs | (uintptr_t)bTs | (uintptr_t)pad) & 3u) return SMOE_EINVAL_PTRALIGN;
-  grouped_gemm_fp8_wgrad_kernel<<<dim3((Kdim + kWK - 1) / kWK, (N + kWN - 1) / kWN, E),
-                                  dim3(kWThreads), 0,
-                                  (hipStream_t)stream>>>(aT, aTs, bT, bTs, pad, N, Kdim, ld, dW);
+  // experts padded to a multiple of 8 (one per XCD in each round)
+  const long long nblk =
+      (long long)(E + 7) / 8 * 8 * ((Kdim + kWK - 1) / kWK) * ((N + kWN - 1) / kWN);
+  if (nblk > 0x7fffffffLL) return SMOE_EINVAL_DIM;
+  grouped_gemm_fp8_wgrad_kernel<<<dim3((unsigned)nblk), dim3(kWThreads), 0, (hipStream_t)stream>>>(
+      aT, aTs, bT, bTs, pad, E, N, Kdim, ld, dW);
   SMOE_RETURN_LAUNCH();
 }

@@ -232,7 +232,8 @@ def test_quant_cols_gather_bit_exact(dev):
 
 
 @pytest.mark.parametrize("counts,N,K", [([3, 0, 200, 129], 256, 384), ([1024] * 4, 768, 2048),
-                                        ([0, 0], 128, 128), ([5000, 17], 2048, 768)])
+                                        ([0, 0], 128, 128), ([5000, 17], 2048, 768),
+                                        ([7, 130, 0, 256, 1, 0, 300, 128, 129, 5, 64], 384, 640)])
 def test_wgrad_gemm(dev, counts, N, K):
     say("wgrad", counts, N, K)
     off = _offsets(counts)
