@@ -14,21 +14,25 @@
 // and the weight scale (a wave's 64 columns lie in one 128-column block) is
 // wave-uniform.
 //
-// Data movement.  Each K step stages a 256x128-byte activation tile, a
-// 256x128-byte weight tile and the 256 activation scales in LDS with direct
-// global->LDS loads (global_load_lds_dwordx4 / _dword: no VGPR round trip),
-// two stages deep: the loads of step kb+1 are issued before the MFMAs of step
-// kb, and the step's single barrier waits for them.  The LDS row layout
-// (lds_row / swz) makes the 128-bit fragment reads conflict-free.  The tile's
-// weight-block scales are copied to LDS once, before the K loop.
+// Data movement.  Each K step stages a 256x128-byte activation tile and a
+// 256x128-byte weight tile in LDS with direct global->LDS loads
+// (global_load_lds_dwordx4: no VGPR round trip), two stages deep: the loads of
+// step kb+1 are issued before the MFMAs of step kb, and the step's single
+// barrier waits for them.  The 256 activation scales of a step come either 8
+// K steps at a time (K a multiple of 512: one 16-byte DMA per wave per
+// chunk, double-buffered) or with each stage (one word from each of 256 rows,
+// _dword DMA).  The LDS row layout (lds_row / swz) makes the 128-bit fragment
+// reads conflict-free.  The tile's weight-block scales are copied to LDS once,
+// before the K loop.
 //
 // Scheduling.  The grid covers an upper bound of m-tiles (ceil(R/256) + E,
 // padded to kChipM) times the n-tiles.  Tiles are taken in chip-wide groups
 // of kChipM consecutive m-tiles x all n-tiles; within a group, XCD x (blocks
 // are dealt to the 8 XCDs round robin) takes m-tiles x*kChipM/8 .. +kChipM/8
-// and sweeps the n-tiles, m fastest.  All XCDs then stream the same weight slices at
-// once (read from HBM once, the other XCDs hit the last-level cache), and
-// each XCD's L2 serves its own activation rows to all n-tiles.  A last,
+// and sweeps the n-tiles, m fastest, so its 32 CUs run 4 m-tiles x 8 n-tiles
+// at once.  All XCDs then stream the same weight slices at once (read from
+// HBM once, the other XCDs hit the last-level cache), and each XCD's L2
+// serves its own activation rows to all n-tiles.  A last,
 // partial group's tiles are split evenly over the 8 XCDs instead.  Every
 // workgroup derives the per-expert m-tile prefix sum from offsets[] in LDS
 // (no host sync, no workspace) and leaves when its tile index is past the
