@@ -109,6 +109,12 @@ class SimpleMoE(nn.Module):
         main = torch.cuda.current_stream()
         side = self._side_stream(main.device)
         ones = torch.ones_like(inter["topk_w"])
+        # the returned weight gradients are allocated on the caller's stream,
+        # so the caching allocator never hands their memory to side-stream
+        # work while the caller still uses them
+        E, H, I = self.num_experts, self.hidden, self.intermediate
+        dw1 = torch.empty((E, 2 * I, H), dtype=torch.float32, device=dout.device)
+        dw2 = torch.empty((E, H, I), dtype=torch.float32, device=dout.device)
         side.wait_stream(main)
         with torch.cuda.stream(side):
             # the wgrad activation operands depend on the forward only: h, and
@@ -121,14 +127,14 @@ class SimpleMoE(nn.Module):
             dout.contiguous(), inter["y"], inv, inter["row_map"], inter["topk_w"], off)
         side.wait_stream(main)
         with torch.cuda.stream(side):
-            dw2 = ops.grouped_gemm_fp8_wgrad(dyTq, dyTs, hTq, hTs, pad, ld)
+            ops.grouped_gemm_fp8_wgrad(dyTq, dyTs, hTq, hTs, pad, ld, out=dw2)
         dh = ops.grouped_gemm_fp8(dyq, dys, w2tq, w2ts, off)
         # SwiGLU backward fused with both quantisations of dc1 (dc1 itself is
         # never stored)
         dcq, dcs, dcTq, dcTs, _, _ = ops.swiglu_bwd_quant(inter["c1"], dh, off)
         side.wait_stream(main)
         with torch.cuda.stream(side):
-            dw1 = ops.grouped_gemm_fp8_wgrad(dcTq, dcTs, xTq, xTs, pad, ld)
+            ops.grouped_gemm_fp8_wgrad(dcTq, dcTs, xTq, xTs, pad, ld, out=dw1)
         dxs = ops.grouped_gemm_fp8(dcq, dcs, w1tq, w1ts, off)
         dx = ops.unpermute_combine(dxs, inv, ones)
         main.wait_stream(side)

@@ -338,16 +338,22 @@ def swiglu_bwd_quant(c1: torch.Tensor, dh: torch.Tensor, offsets: torch.Tensor,
     return out + (dc1,) if save_dc1 else out
 
 
-def grouped_gemm_fp8_wgrad(aTq, aTs, bTq, bTs, pad, ld: int) -> torch.Tensor:
+def grouped_gemm_fp8_wgrad(aTq, aTs, bTq, bTs, pad, ld: int, out: torch.Tensor | None = None) -> torch.Tensor:
     """dW[e] = A_e^T B_e over each expert's rows from quant_cols operands:
-    aT [N, ld], bT [K, ld] -> fp32 [E, N, K]."""
+    aT [N, ld], bT [K, ld] -> fp32 [E, N, K] (into ``out`` when given)."""
     _check(aTq, "aTq", (FP8, torch.uint8), 2)
     _check(bTq, "bTq", (FP8, torch.uint8), 2)
     _check(pad, "pad", (torch.int32,), 1)
     N, K, E = aTq.shape[0], bTq.shape[0], pad.numel() - 1
     if aTq.shape[1] != ld or bTq.shape[1] != ld:
         raise ValueError("operands must share the padded row length ld")
-    dW = torch.empty((E, N, K), dtype=torch.float32, device=aTq.device)
+    if out is None:
+        dW = torch.empty((E, N, K), dtype=torch.float32, device=aTq.device)
+    else:
+        _check(out, "out", (torch.float32,), 3)
+        if tuple(out.shape) != (E, N, K):
+            raise ValueError(f"out must be [{E}, {N}, {K}] fp32")
+        dW = out
     _C.call("smoe_grouped_gemm_fp8_wgrad", _ptr(_bytes(aTq)), _ptr(aTs), _ptr(_bytes(bTq)),
             _ptr(bTs), _ptr(pad), E, N, K, ld, _ptr(dW), _stream())
     return dW

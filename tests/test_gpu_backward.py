@@ -262,6 +262,10 @@ def test_wgrad_gemm(dev, counts, N, K):
         if counts[e] == 0:
             assert not got[e].any()
     close(got, ref, f"wgrad {counts}")
+    # into a caller buffer that starts as NaN: every element is written
+    out = torch.full((E, N, K), float("nan"), dtype=torch.float32, device=dev)
+    assert ops.grouped_gemm_fp8_wgrad(aq, as_, bq, bs_, pad, ld, out=out) is out
+    assert torch.equal(out, dW)
 
 
 @pytest.mark.parametrize("R,I", [(1000, 768), (9, 2048), (300, 128)])
