@@ -158,15 +158,42 @@ __device__ __forceinline__ float row16_max(float v) {
   return v;
 }
 
+// The value of lane (l ^ kO) for every lane l of a fully active wave: DPP
+// quad permutes for 1 and 2, ds_swizzle's bit mode within 32 lanes for 4, 8
+// and 16, ds_bpermute for 32.  The same partner as __shfl_xor(v, kO), with
+// shorter exchange latency for the first five levels.
+template <int kO>
+__device__ __forceinline__ int xor_lanes(int v) {
+  static_assert(kO == 1 || kO == 2 || kO == 4 || kO == 8 || kO == 16 || kO == 32, "xor distance");
+  if constexpr (kO == 1) return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
+  else if constexpr (kO == 2) return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
+  else if constexpr (kO < 32) return __builtin_amdgcn_ds_swizzle(v, (kO << 10) | 0x1F);
+  else return __shfl_xor(v, 32, kWave);
+}
+template <int kO>
+__device__ __forceinline__ float xor_lanes(float v) {
+  return __int_as_float(xor_lanes<kO>(__float_as_int(v)));
+}
+
+// Sum over the wave as a fixed butterfly (partners at distance 32, 16, ...,
+// 1), the reduction tree the oracle restates.
 __device__ __forceinline__ float wave_sum_tree(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = v + __shfl_xor(v, o, kWave);
+  v = v + xor_lanes<32>(v);
+  v = v + xor_lanes<16>(v);
+  v = v + xor_lanes<8>(v);
+  v = v + xor_lanes<4>(v);
+  v = v + xor_lanes<2>(v);
+  v = v + xor_lanes<1>(v);
   return v;
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  v = fmaxf(v, xor_lanes<32>(v));
+  v = fmaxf(v, xor_lanes<16>(v));
+  v = fmaxf(v, xor_lanes<8>(v));
+  v = fmaxf(v, xor_lanes<4>(v));
+  v = fmaxf(v, xor_lanes<2>(v));
+  v = fmaxf(v, xor_lanes<1>(v));
   return v;
 }
 

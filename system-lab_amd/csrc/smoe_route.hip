@@ -24,6 +24,22 @@ namespace smoe {
 constexpr int kSeg = 512;  // pairs per segment (one wave)
 
 // ------------------------------------------------------------------ router
+// One butterfly level of the wave arg-max: the partner at distance kO wins
+// with a larger score, or an equal score and a lower id (0x7fffffff marks a
+// lane with no candidate).
+template <int kO>
+__device__ __forceinline__ void argmax_step(float& bs, int& bi, float& bp) {
+  const float os = xor_lanes<kO>(bs);
+  const int oi = xor_lanes<kO>(bi);
+  const float op = xor_lanes<kO>(bp);
+  const bool take = (oi != 0x7fffffff) && (bi == 0x7fffffff || os > bs || (os == bs && oi < bi));
+  if (take) {
+    bs = os;
+    bi = oi;
+    bp = op;
+  }
+}
+
 template <int NC>
 __global__ __launch_bounds__(256) void router_topk_kernel(
     const float* __restrict__ logits, const float* __restrict__ bias, int T, int E, int K,
@@ -74,19 +90,12 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
       }
     }
     // wave arg-max: larger score wins, equal scores -> lower id
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      float os = __shfl_xor(bs, o, kWave);
-      int oi = __shfl_xor(bi, o, kWave);
-      float op = __shfl_xor(bp, o, kWave);
-      bool take = (oi != 0x7fffffff) &&
-                  (bi == 0x7fffffff || os > bs || (os == bs && oi < bi));
-      if (take) {
-        bs = os;
-        bi = oi;
-        bp = op;
-      }
-    }
+    argmax_step<32>(bs, bi, bp);
+    argmax_step<16>(bs, bi, bp);
+    argmax_step<8>(bs, bi, bp);
+    argmax_step<4>(bs, bi, bp);
+    argmax_step<2>(bs, bi, bp);
+    argmax_step<1>(bs, bi, bp);
     // owner lane retires the winner
 #pragma unroll
     for (int c = 0; c < NC; ++c)
