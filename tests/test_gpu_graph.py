@@ -122,3 +122,35 @@ def test_two_streams_concurrent(dev):
         for i in (0, 1):
             for got, want in zip(res[i], serial[i]):
                 assert torch.equal(got.view(torch.uint8), want.view(torch.uint8)), f"stream {i} rep {rep}"
+
+
+def test_backward_on_a_caller_stream(dev):
+    """backward_from orders its weight-gradient stream after whatever stream
+    the caller runs on, and that stream after it: forward + backward on a
+    non-default stream, twice, with the caller's stream reading the results
+    right away (no host sync in between), give the default-stream bytes."""
+    say("backward on a caller stream")
+    c = W.CONFIGS["tiny"]
+    m = _layer(dev, c)
+    x, lg = W.tokens(c.T, c.H).to(dev), W.logits(c.T, c.E).to(dev)
+    dout = (W.tokens(c.T, c.H, seed=4).float() * 1e-3).to(torch.bfloat16).to(dev)
+
+    def step():
+        out, inter = m(x, lg, return_intermediates=True)
+        g = m.backward_from(inter, dout)
+        return [out, g["dx"], g["dw1"], g["dw2"], g["dtopk_w"]]
+
+    ref = [t.clone() for t in step()]
+    torch.cuda.synchronize()
+    user = torch.cuda.Stream()  # default priority
+    user.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(user):
+        for rep in range(2):
+            got = step()
+            # copies enqueued on the caller's stream straight after the call
+            snap = [t.clone() for t in got]
+            del got
+    torch.cuda.current_stream().wait_stream(user)
+    torch.cuda.synchronize()
+    for name, a, b in zip(("out", "dx", "dw1", "dw2", "dtopk_w"), snap, ref):
+        assert torch.equal(a.view(torch.uint8), b.view(torch.uint8)), f"{name} differs on a caller stream"
