@@ -5,15 +5,21 @@ Headline (benchmark config 2, the permute+quantise shape the metric is quoted on
 the dispatch of one batch — stable expert sort + fused permute/1x128 fp8
 quantisation — for T=16384 tokens, H=7168, E=256, top-8, inputs resident in
 HBM.  ``value`` is the algorithmic HBM traffic of that step
-(T*H*2 + T*K*H + T*K*(H/128)*4 + T*K*4 + T*K*8 + (E+1)*4 bytes) per second.
+(T*H*2 + T*K*H + T*K*(H/128)*4 + T*K*4 + T*K*8 + (E+1)*4 bytes) per second,
+from the median of K event-timed steps, each after a 1 GiB cache flush (the
+input is 235 MB, so back to back it would partly sit in the last-level
+cache).
 
 Also reported on the same line:
   roofline      the dominant kernel (permute_quant) timed alone with HIP
-                events on the launch stream, algorithmic bytes / duration;
+                events on the launch stream, algorithmic bytes / duration,
+                median of >= 20 flushed launches;
   cpu_baseline  the PyTorch-CPU restatement of the same dispatch step
                 (oracle/cpu_torch.py) on a bounded sample of the same
                 workload, multi-threaded on this host's CPU share;
-  extra         fp8 grouped GEMM TFLOPS on benchmark config 4 (DeepSeek-V3
+  extra         the HBM ceiling for the dispatch step's read:write mix
+                (smoe_bw_probe), the fused router + sort at config 2,
+                fp8 grouped GEMM TFLOPS on benchmark config 4 (DeepSeek-V3
                 local experts, Zipf loads, fc1 + fc2), the combine GB/s at
                 config-2 size, the whole SimpleMoE forward of config 3 and the
                 forward+backward step of config 5.
@@ -43,8 +49,10 @@ def log(*a):
 
 
 def timed(fn, iters, warmup):
-    """Mean ms per call over ``iters`` calls on the current stream, bracketed
-    by HIP events recorded on that stream (the stream the kernels use)."""
+    """Mean ms per call over ``iters`` back-to-back calls on the current
+    stream, bracketed by HIP events recorded on that stream (the stream the
+    kernels use).  Inputs may stay in L2 / the last-level cache between
+    calls: reported as the warm figure only."""
     import torch
     for _ in range(warmup):
         fn()
@@ -58,30 +66,52 @@ def timed(fn, iters, warmup):
     return s.elapsed_time(e) / iters
 
 
-def timed_cold(fn, iters=20, warmup=5, flush_mib=1024):
-    """Median ms of ``iters`` single calls, each timed by its own HIP events
-    after a ``flush_mib`` MiB device read (larger than L2 plus the 256 MiB
-    last-level cache), so no call finds its inputs cached.  The flush reads
-    rather than writes: a write leaves dirty lines whose write-back would be
-    charged to the timed call."""
+class Flush:
+    """A ``mib`` MiB device buffer whose read (a max-reduction) evicts L2 and
+    the 256 MiB last-level cache.  It reads rather than writes: a write
+    leaves dirty lines whose write-back would be charged to the next timed
+    call."""
+
+    def __init__(self, mib=1024):
+        import torch
+        self.buf = torch.ones(mib << 18, dtype=torch.int32, device="cuda")
+
+    def __call__(self):
+        self.buf.max()
+
+
+def timed_median(fn, iters=20, warmup=5, flush=None):
+    """Median ms of ``iters`` single calls, each bracketed by its own HIP
+    events on the current stream; with ``flush`` (a Flush), each call runs
+    after the caches were flushed, so no call finds its inputs cached.  The
+    benchmark contract's timing: median of >= 20 event-timed calls after 5
+    warm-ups, flushed for the HBM-bound kernels."""
     import numpy as np
     import torch
-    flush = torch.ones(flush_mib << 18, dtype=torch.int32, device="cuda")
     for _ in range(warmup):
-        flush.max()
+        if flush:
+            flush()
         fn()
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     times = []
     for _ in range(iters):
-        flush.max()
+        if flush:
+            flush()
         torch.cuda.synchronize()
         s.record()
         fn()
         e.record()
         torch.cuda.synchronize()
         times.append(s.elapsed_time(e))
-    del flush
     return float(np.median(times))
+
+
+def timed_cold(fn, iters=20, warmup=5, flush_mib=1024):
+    """Median ms of ``iters`` calls, each after a ``flush_mib`` MiB read."""
+    f = Flush(flush_mib)
+    t = timed_median(fn, iters, warmup, f)
+    del f
+    return t
 
 
 def dispatch_bytes(T, H, E, K):
@@ -174,14 +204,15 @@ def bench_gemm(dev, steps, warmup, skip_cpu=True):
     y = torch.empty((R, c.H), dtype=torch.bfloat16, device=dev)
     f1 = lambda: ops.grouped_gemm_fp8(xq, xs, w1q, w1s, off, out=c1)
     f2 = lambda: ops.grouped_gemm_fp8(hq, hs, w2q, w2s, off, out=y)
-    t1 = timed(f1, steps, warmup)
-    t2 = timed(f2, steps, warmup)
+    # median of per-launch event timings (MFMA-bound: no cache flush)
+    t1 = timed_median(f1, steps, warmup)
+    t2 = timed_median(f2, steps, warmup)
     # fc1 with SwiGLU + requant fused into the epilogue (the inference path),
     # against fc1 followed by the stand-alone SwiGLU kernel
     fsw = lambda: ops.swiglu_quant(c1)
-    t_sw = timed(fsw, steps, warmup)
+    t_sw = timed_median(fsw, steps, warmup)
     f1s = lambda: ops.grouped_gemm_fp8_swiglu(xq, xs, w1q, w1s, off)
-    t1s = timed(f1s, steps, warmup)
+    t1s = timed_median(f1s, steps, warmup)
     fl1 = 2.0 * R * (2 * c.I) * c.H
     fl2 = 2.0 * R * c.H * c.I
     tf = (fl1 + fl2) / ((t1 + t2) * 1e-3) / 1e12
@@ -208,15 +239,17 @@ def bench_combine(dev, c, steps, warmup):
     inv = torch.randperm(R, generator=g, device=dev).to(torch.int32)
     w = torch.rand((c.T, c.K), generator=g, device=dev)
     out = torch.empty((c.T, c.H), dtype=torch.bfloat16, device=dev)
-    t = timed(lambda: ops.unpermute_combine(y, inv, w, out=out), steps, warmup)
-    tf = timed_cold(lambda: ops.unpermute_combine(y, inv, w, out=out))
+    fn = lambda: ops.unpermute_combine(y, inv, w, out=out)
+    tf = timed_cold(fn, max(20, steps), warmup)
+    t = timed(fn, steps, warmup)
     nb = R * c.H * 2 + R * 8 + c.T * c.H * 2
     del y, out
     torch.cuda.empty_cache()
-    return {"ms": round(t, 4), "gbs": round(nb / (t * 1e-3) / 1e9, 1),
-            "roofline_frac": round(nb / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "ms_cold_median": round(tf, 4),
-            "gbs_cold_median": round(nb / (tf * 1e-3) / 1e9, 1)}
+    return {"ms": round(tf, 4), "gbs": round(nb / (tf * 1e-3) / 1e9, 1),
+            "roofline_frac": round(nb / (tf * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "timing": "median of >= 20 launches, each after a 1 GiB cache flush",
+            "ms_warm_back_to_back": round(t, 4),
+            "gbs_warm_back_to_back": round(nb / (t * 1e-3) / 1e9, 1)}
 
 
 def bench_layer(dev, steps, warmup):
@@ -230,6 +263,8 @@ def bench_layer(dev, steps, warmup):
         m.w2.copy_(W.weights(c.E, c.H, c.I, device=dev, seed=13))
     m.refresh_fp8_cache()
     x, lg = W.tokens(c.T, c.H, device=dev), W.logits(c.T, c.E, device=dev)
+    # a whole layer is ~10 launches from Python: back-to-back calls measure
+    # its throughput with the host enqueueing ahead of the GPU
     t = timed(lambda: m(x, lg), steps, warmup)
     fl = 2.0 * c.T * c.K * (2 * c.I) * c.H + 2.0 * c.T * c.K * c.H * c.I
     del m
@@ -269,11 +304,61 @@ def bench_fwd_bwd(dev, steps, warmup):
             "ms": round(t, 4), "tflops": round(3 * fwd / (t * 1e-3) / 1e12, 1)}
 
 
+def bench_ceiling(dev, c, iters=20):
+    """The HBM's rate for the dispatch step's traffic mix without the
+    quantisation: smoe_bw_probe reads the config-2 input once (T*H*2 bytes)
+    and writes every 16-byte piece to ``fanout`` places (fanout 8 with the
+    bf16 -> fp8 halving is the permute's 1:4 byte mix), each launch after a
+    cache flush; plus a plain device copy and a read-only pass."""
+    import torch
+    import smoe
+    n_in = c.T * c.H * 2
+    src = torch.ones(n_in // 4, dtype=torch.int32, device=dev)
+    dst = torch.empty(n_in * 8, dtype=torch.uint8, device=dev)
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    flush = Flush()
+    out = {"bytes_in": n_in}
+    for fanout in (0, 1, 2, 4, 8):
+        fn = lambda: smoe._C.call("smoe_bw_probe", src.data_ptr(), n_in, fanout, dst.data_ptr(),
+                                  dst.numel(), sink.data_ptr(),
+                                  torch.cuda.current_stream().cuda_stream)
+        ms = timed_median(fn, iters, 3, flush)
+        nb = n_in * (1 + fanout)
+        out[f"read1_write{fanout}"] = {"ms": round(ms, 4), "gbs": round(nb / (ms * 1e-3) / 1e9, 1),
+                                       "frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    del src, dst, flush
+    torch.cuda.empty_cache()
+    return out
+
+
+def bench_blaslt(dev, iters=20):
+    """hipBLASLt's fp8 GEMM (torch._scaled_mm, one tensor-wide scale per
+    operand, dense) at the config-4 fc1 and fc2 shapes with all 65536 rows in
+    one GEMM: the vendor library's rate without block scales or expert
+    grouping, a practical reference for the grouped kernel's MFMA ceiling."""
+    import torch
+    c = __import__("smoe").workloads.CONFIGS["dsv3"]
+    out = {}
+    one = torch.ones((), device=dev)
+    for name, (M, N, K) in (("fc1", (c.T, 2 * c.I, c.H)), ("fc2", (c.T, c.H, c.I))):
+        a = torch.randn(M, K, device=dev).to(torch.float8_e4m3fn)
+        b = torch.randn(N, K, device=dev).to(torch.float8_e4m3fn).t()
+        fn = lambda: torch._scaled_mm(a, b, scale_a=one, scale_b=one, out_dtype=torch.bfloat16)
+        ms = timed_median(fn, iters, 5)
+        out[name] = {"M": M, "N": N, "K": K, "ms": round(ms, 4),
+                     "tflops": round(2.0 * M * N * K / (ms * 1e-3) / 1e12, 1)}
+        del a, b
+    torch.cuda.empty_cache()
+    return out
+
+
 def run_only(args, dev, c):
     """One kernel family, for profiler runs: permute = the dispatch step
-    (route sort + permute_quant), gemm = DSv3 fc1 + fc2, combine = config-2
-    sized combine, copy = a plain 1 GiB device copy (calibrates the
-    FETCH_SIZE / WRITE_SIZE counters against known traffic)."""
+    (route sort + permute_quant) back to back, gemm = DSv3 fc1 + fc2,
+    combine = config-2 sized combine, copy = a plain 1 GiB device copy
+    (calibrates the FETCH_SIZE / WRITE_SIZE counters against known traffic),
+    ceiling = the HBM traffic-mix probe, blaslt = hipBLASLt's dense fp8 GEMM
+    at the config-4 shapes, router = the fused router + sort at config 2."""
     import torch
     from smoe import ops, workloads as W
     if args.only == "copy":
@@ -287,22 +372,48 @@ def run_only(args, dev, c):
         ms = timed(lambda: ops.permute_quant(x, idx, c.E), args.steps, args.warmup)
         print(json.dumps({"only": "permute", "ms": ms,
                           "gbs": dispatch_bytes(c.T, c.H, c.E, c.K) / (ms * 1e-3) / 1e9}))
+    elif args.only == "router":
+        print(json.dumps({"only": "router", **bench_router(dev, c, args.steps, args.warmup)}))
     elif args.only == "fwdbwd":
         print(json.dumps({"only": "fwdbwd", **bench_fwd_bwd(dev, args.steps, args.warmup)}))
     elif args.only == "gemm":
         print(json.dumps({"only": "gemm", **bench_gemm(dev, args.steps, args.warmup)}))
+    elif args.only == "ceiling":
+        print(json.dumps({"only": "ceiling", **bench_ceiling(dev, c, max(20, args.steps))}))
+    elif args.only == "blaslt":
+        print(json.dumps({"only": "blaslt", **bench_blaslt(dev, max(20, args.steps))}))
     else:
         print(json.dumps({"only": "combine", **bench_combine(dev, c, args.steps, args.warmup)}))
+
+
+def bench_router(dev, c, steps, warmup):
+    """The fused router + expert sort at config 2 (T=16384, E=256, top-8,
+    with bias): three launches, median of per-call event timings after a
+    cache flush.  Algorithmic bytes: logits T*E*4 + bias E*4 read, ids and
+    weights T*K*8, row_map/inv_map R*8 and offsets/counts written (the
+    router launch alone: T*E*4 + T*K*8)."""
+    from smoe import ops, workloads as W
+    lg = W.logits(c.T, c.E, device=dev)
+    b = W.router_bias(c.E, device=dev)
+    flush = Flush()
+    ms = timed_median(lambda: ops.route_topk_sort(lg, c.K, b), max(20, steps), warmup, flush)
+    ms_r = timed_median(lambda: ops.router_topk(lg, c.K, b), max(20, steps), warmup, flush)
+    R = c.T * c.K
+    nb = c.T * c.E * 4 + c.E * 4 + R * 8 + R * 8 + (2 * c.E + 1) * 4
+    nr = c.T * c.E * 4 + R * 8
+    return {"route_topk_sort_ms": round(ms, 4), "route_topk_sort_gbs": round(nb / (ms * 1e-3) / 1e9, 1),
+            "router_topk_ms": round(ms_r, 4), "router_topk_gbs": round(nr / (ms_r * 1e-3) / 1e9, 1)}
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-extra", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--only", choices=["permute", "gemm", "combine", "copy", "fwdbwd"],
+    ap.add_argument("--only", choices=["permute", "gemm", "combine", "copy", "fwdbwd", "ceiling",
+                                       "blaslt", "router"],
                     help="run one kernel family only (for rocprofv3 runs) and print its timing")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -342,40 +453,40 @@ def main():
         smoe._C.call("smoe_permute_quant", x.data_ptr(), inv_map.data_ptr(), c.T, c.H, c.K,
                      xq.data_ptr(), xs.data_ptr(), torch.cuda.current_stream().cuda_stream)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s.record()
-    for _ in range(args.steps):
-        step()
-    e.record()
-    torch.cuda.synchronize()
-    ms = s.elapsed_time(e) / args.steps
+    # The timed steps: W warm-ups, then exactly K steps, each bracketed by
+    # HIP events after a synchronise and a 1 GiB cache flush (x is not in
+    # L2 or the last-level cache when a step starts); ms_per_step is their
+    # median.  Every permute_quant launch of this run is a flushed one, so a
+    # profiler's average over the run is the cold figure too.
+    flush = Flush()
+    ms = timed_median(step, args.steps, args.warmup, flush)
     nbytes = dispatch_bytes(c.T, c.H, c.E, c.K)
     value = nbytes / (ms * 1e-3) / 1e9
-    log(f"dispatch step {ms:.4f} ms  {value:.1f} GB/s")
+    log(f"dispatch step {ms:.4f} ms  {value:.1f} GB/s (median of {args.steps}, flushed)")
 
-    pk_ms = timed(permute_only, args.steps, 2)
-    pk_cold = timed_cold(permute_only)
+    pk_ms = timed_median(permute_only, max(20, args.steps), args.warmup, flush)
+    del flush
     pk_bytes = permute_kernel_bytes(c.T, c.H, c.K)
     pk_gbs = pk_bytes / (pk_ms * 1e-3) / 1e9
-    log(f"permute_quant kernel {pk_ms:.4f} ms  {pk_gbs:.1f} GB/s")
+    log(f"permute_quant kernel {pk_ms:.4f} ms  {pk_gbs:.1f} GB/s (median, flushed)")
     roof = {"kernel": "smoe::permute_quant_kernel<4, true>", "bound": "hbm", "achieved": round(pk_gbs, 1),
             "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(pk_gbs / HBM_PEAK_GBS, 4),
             "traffic": PERMUTE_TRAFFIC_BYTES, "kernel_ms": round(pk_ms, 4),
             "bytes_per_launch": pk_bytes,
-            "kernel_ms_cold_median": round(pk_cold, 4),
-            "frac_cold_median": round(pk_bytes / (pk_cold * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+            "timing": "median of >= 20 launches, each after a 1 GiB cache flush"}
     del x, xq, xs
     torch.cuda.empty_cache()
 
     extra = {}
     if not args.skip_extra:
-        sx = max(5, args.steps // 5)
-        extra["grouped_gemm_fp8"] = bench_gemm(dev, sx, 2, skip_cpu=args.skip_cpu)
+        sx = max(20, args.steps)
+        extra["hbm_ceiling_dispatch_mix"] = bench_ceiling(dev, c)
+        log("ceiling", extra["hbm_ceiling_dispatch_mix"])
+        extra["router_cfg2"] = bench_router(dev, c, sx, 3)
+        log("router", extra["router_cfg2"])
+        extra["grouped_gemm_fp8"] = bench_gemm(dev, sx, 3, skip_cpu=args.skip_cpu)
         log("gemm", extra["grouped_gemm_fp8"])
-        extra["combine_cfg2"] = bench_combine(dev, c, sx, 2)
+        extra["combine_cfg2"] = bench_combine(dev, c, sx, 3)
         log("combine", extra["combine_cfg2"])
         extra["layer_mixtral"] = bench_layer(dev, 10, 3)
         log("layer", extra["layer_mixtral"])
@@ -389,7 +500,8 @@ def main():
             "scaling": "weak", "vs_baseline": None, "dtype": "fp8-e4m3 (bf16 in, fp32 scales)",
             "data": "synthetic (seeded N(0,1) bf16 tokens with 0.1% x50 outliers, N(0,1) logits + N(0,0.5) bias)",
             "config": {"workload": "permute+quantize cfg2: route_sort + permute_quant",
-                       "T": c.T, "H": c.H, "E": c.E, "top_k": c.K, "parallelism": "ep1"},
+                       "T": c.T, "H": c.H, "E": c.E, "top_k": c.K, "parallelism": "ep1",
+                       "timing": "median of K steps, each after a 1 GiB cache flush"},
             "roofline": roof, "cpu_baseline": cpu, "extra": extra}
     print(json.dumps(line), flush=True)
 

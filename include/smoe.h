@@ -68,19 +68,52 @@ int smoe_router_topk(const float* logits, const float* bias, int T, int E, int K
                      int32_t* topk_idx, float* topk_w, void* stream);
 
 /*
+ * Router backward: dtopk_w [T,K] f32 (gradient of the renormalised weights)
+ * -> dlogits [T,E] f32, through the renormalisation and the softmax (the
+ * selection bias has no gradient).  topk_idx are the forward's picks.  With
+ * S = sum_k p[s_k] and c = sum_k g_k w_k:
+ *   dp[s_k] = (g_k - c) / S,  dlogits_e = p_e (dp_e - sum_k p[s_k] dp[s_k]).
+ * Replaces the router's autograd backward (gate -> softmax -> top-k ->
+ * renorm, moe/MoE_detailed_computation_dataflow.md:53-66, backward chain
+ * :209-226).
+ */
+int smoe_router_topk_bwd(const float* logits, const int32_t* topk_idx, const float* dtopk_w,
+                         int T, int E, int K, float* dlogits, void* stream);
+
+/*
  * Expert sort: stable counting sort of the T*K (token, slot) pairs by expert.
  * topk_idx [T,K] i32 -> row_map [T*K], inv_map [T*K], counts [E],
- * offsets [E+1] (all i32).  ws must hold smoe_route_sort_workspace_size().
+ * offsets [E+1] (all i32).  ws (16-byte aligned) must hold
+ * smoe_route_sort_workspace_size() bytes.
+ * Ids outside [0, E) are an error the call cannot report synchronously (they
+ * live on the device): such a pair gets no row and inv_map[p] = -1, so
+ * offsets[E] = T*K minus their number, and the int32 at byte
+ * SMOE_ROUTE_STATUS_OFFSET of ws receives that number (0 when every id is
+ * valid).  The status word is rewritten by every call.
  * Replaces the pack sort phase that yields pack_perm "sorted pair index ->
  * original pair index" (notes/2026-04/2026-04-10_monolithmoe_layout_c_pack_optimization.md:56,80)
  * and Megatron's tokens_per_expert computation in Dispatcher.permute
  * (moe/MegatronCore_MoE_reading_notes.md:94-99), without the host .tolist()
  * sync (summary/fp8_expert_gemm_optimization.md:190).
  */
+#define SMOE_ROUTE_STATUS_OFFSET 0
 size_t smoe_route_sort_workspace_size(int T, int K, int E);
 int smoe_route_sort(const int32_t* topk_idx, int T, int K, int E, int32_t* row_map,
                     int32_t* inv_map, int32_t* counts, int32_t* offsets, void* ws,
                     size_t ws_bytes, void* stream);
+
+/*
+ * Router fused with the sort: smoe_router_topk's outputs plus smoe_route_sort's,
+ * with the sort's per-segment expert histogram counted inside the router
+ * launch (three launches in all, no host sync).  Same bytes as
+ * smoe_router_topk followed by smoe_route_sort; ws as for smoe_route_sort.
+ * Replaces the fused router kernel with its expert histogram that feeds the
+ * permutation ("fused router with aux score", notes/2026-04/2026-04-25_gptoss_22_sync_free_moe_stage_audit.md:25-26,104-124).
+ */
+int smoe_route_topk_sort(const float* logits, const float* bias, int T, int E, int K,
+                         int32_t* topk_idx, float* topk_w, int32_t* row_map, int32_t* inv_map,
+                         int32_t* counts, int32_t* offsets, void* ws, size_t ws_bytes,
+                         void* stream);
 
 /*
  * Fused permute + 1x128 fp8 quantisation.  Each token row of x [T,H] bf16 is
@@ -322,6 +355,17 @@ int smoe_unpermute_combine_bwd_quant(const uint16_t* dout, const uint16_t* y,
                                      const float* w, int T, int K, int H, const int32_t* offsets,
                                      int E, int ld, uint8_t* dyq, float* dys, uint8_t* dyTq,
                                      float* dyTs, int32_t* pad, float* dw, void* stream);
+
+/*
+ * Measurement utility (no counterpart in the reference): reads n_in bytes
+ * of src once and writes each 16-byte piece to `fanout` places of dst
+ * (fanout * n_in bytes, the copies n_in bytes apart) with 128-bit loads and
+ * non-temporal 128-bit stores; fanout = 0 only reads.  It reproduces the
+ * read:write mix of the dispatch step (1:K) without the quantisation, so
+ * its rate is the HBM ceiling for that mix.  sink: one device word.
+ */
+int smoe_bw_probe(const void* src, size_t n_in, int fanout, void* dst, size_t dst_bytes,
+                  void* sink, void* stream);
 
 #ifdef __cplusplus
 }

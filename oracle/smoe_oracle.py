@@ -212,6 +212,28 @@ def router_topk(logits: np.ndarray, K: int, bias: np.ndarray | None = None):
     return order.astype(np.int32), w
 
 
+def router_topk_bwd(logits: np.ndarray, topk_idx: np.ndarray, dtopk_w: np.ndarray) -> np.ndarray:
+    """Gradient of the renormalised top-K weights with respect to the
+    logits, in float64 (moe/MoE_detailed_computation_dataflow.md:53-66,
+    backward chain :209-226).  With p = softmax(l), picks s_k, S = sum_k
+    p[s_k], w_k = p[s_k]/S and g = dL/dw:
+        dp[s_k] = (g_k - sum_j g_j w_j) / S   (0 for experts not picked)
+        dl = p * (dp - sum_e p_e dp_e).
+    The selection bias has no gradient."""
+    l = np.asarray(logits, np.float64)
+    p = np.exp(l - l.max(axis=1, keepdims=True))
+    p /= p.sum(axis=1, keepdims=True)
+    idx = np.asarray(topk_idx, np.int64)
+    g = np.asarray(dtopk_w, np.float64)
+    pk = np.take_along_axis(p, idx, axis=1)
+    S = pk.sum(axis=1, keepdims=True)
+    w = pk / S
+    c = (g * w).sum(axis=1, keepdims=True)
+    dp = np.zeros_like(p)
+    np.put_along_axis(dp, idx, (g - c) / S, axis=1)
+    return p * (dp - (p * dp).sum(axis=1, keepdims=True))
+
+
 # ---------------------------------------------------------------------------
 # K0: expert sort
 # ---------------------------------------------------------------------------

@@ -1,13 +1,15 @@
 // smoe_route.hip — router top-k and the stable expert sort (gfx950).
 //
-// Router (C1): one wave per token.  Softmax over fp32 logits with the
-// library's exp; the denominator is a fixed reduction tree (lane j sums
-// experts j, j+64, ... in order, then an xor butterfly 32..1), so the
-// probabilities are bit-reproducible.  Top-K by (score desc, id asc).
+// Router (C1): 16 lanes per token (64 for E > 256).  Softmax over fp32
+// logits with the library's exp; the denominator is the fixed reduction tree
+// of a 64-lane wave (lane j sums experts j, j+64, ... in order, then an xor
+// butterfly 32..1), so the probabilities are bit-reproducible whatever the
+// lane mapping.  Top-K by (score desc, id asc).
 //
 // Sort (C2): three small launches over the R = T*K (token, slot) pairs,
 // each wave owning one segment of kSeg consecutive pairs:
-//   1. route_hist  — per-segment expert histogram hist[e][seg] (LDS atomics)
+//   1. route_hist  — per-segment expert histogram hist[e][seg] (LDS atomics);
+//                    router_hist fuses this pass into the router
 //   2. route_rowscan — one wave per expert: exclusive scan of hist[e][:] in
 //                    place (the expert's rows that earlier segments own) and
 //                    counts[e]
@@ -17,6 +19,11 @@
 //                    expert ids are found with one ballot per id bit, so the
 //                    rank inside a chunk is a popcount of lower matching lanes.
 //                    Order is stable and no global atomics are used.
+// A pair whose id lies outside [0, E) gets no row: inv_map[p] = -1, and the
+// number of such pairs is written to the status word at the head of the
+// workspace (0 when every id is valid).
+#include <type_traits>
+
 #include "smoe_common.h"
 
 namespace smoe {
@@ -24,9 +31,9 @@ namespace smoe {
 constexpr int kSeg = 512;  // pairs per segment (one wave)
 
 // ------------------------------------------------------------------ router
-// One butterfly level of the wave arg-max: the partner at distance kO wins
-// with a larger score, or an equal score and a lower id (0x7fffffff marks a
-// lane with no candidate).
+// One butterfly level of the arg-max: the partner at distance kO wins with a
+// larger score, or an equal score and a lower id (0x7fffffff marks a lane
+// with no candidate).
 template <int kO>
 __device__ __forceinline__ void argmax_step(float& bs, int& bi, float& bp) {
   const float os = xor_lanes<kO>(bs);
@@ -40,76 +47,228 @@ __device__ __forceinline__ void argmax_step(float& bs, int& bi, float& bp) {
   }
 }
 
-template <int NC>
-__global__ __launch_bounds__(256) void router_topk_kernel(
-    const float* __restrict__ logits, const float* __restrict__ bias, int T, int E, int K,
-    int32_t* __restrict__ topk_idx, float* __restrict__ topk_w) {
-  const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= T) return;
-  const float* row = logits + (size_t)t * E;
-  float l[NC];
-  bool ok[NC];
+// Butterfly over the kLPT lanes of a token group, top level first.
+template <int kLPT, class F>
+__device__ __forceinline__ void group_levels(F&& f) {
+  if constexpr (kLPT >= 64) f(std::integral_constant<int, 32>{});
+  if constexpr (kLPT >= 32) f(std::integral_constant<int, 16>{});
+  f(std::integral_constant<int, 8>{});
+  f(std::integral_constant<int, 4>{});
+  f(std::integral_constant<int, 2>{});
+  f(std::integral_constant<int, 1>{});
+}
+
+// Routing of one token by a group of kLPT (16 or 64) lanes; lane i of the
+// group holds experts e = i + kLPT*q, q < kNV.
+//
+// Bit-reproducibility: the softmax denominator is the reduction tree of a
+// 64-lane wave in which "virtual lane" j (0..63) sums experts j, j+64, ...
+// in order and a butterfly at distances 32, 16, ..., 1 combines the lanes.
+// With 16 lanes per token, virtual lane j = i + 16a lives in physical lane i
+// (a = q mod 4), so distances 32 and 16 are additions between a lane's own
+// four partial sums and distances 8..1 are lane exchanges: the same
+// operations on the same operands as the 64-lane tree, hence the same bits.
+// Top-K is a total order (score desc, id asc), so the arg-max tree shape
+// does not change the picks; the K picked probabilities are summed in pick
+// order.  Lane (k mod kLPT) returns pick k in slot k / kLPT.
+template <int kLPT, int kNV>
+struct TokenRoute {
+  int id[2];
+  float w[2];
+};
+
+template <int kLPT, int kNV>
+__device__ __forceinline__ TokenRoute<kLPT, kNV> route_token(const float* __restrict__ row,
+                                                             const float* __restrict__ bias,
+                                                             int E, int K, int i) {
+  constexpr int kVirt = 64 / kLPT;  // virtual lanes per physical lane
+  float p[kNV];
+  uint32_t ok = 0;  // bit q: expert i + kLPT*q is valid and not yet picked
   float m = -__builtin_inff();
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    int j = c * kWave + lane;
-    ok[c] = j < E;
-    l[c] = ok[c] ? row[j] : -__builtin_inff();
-    m = fmaxf(m, l[c]);
+  for (int q = 0; q < kNV; ++q) {
+    const int e = i + kLPT * q;
+    p[q] = e < E ? row[e] : -__builtin_inff();
+    if (e < E) ok |= 1u << q;
+    m = fmaxf(m, p[q]);
   }
-  m = wave_max(m);
-  float p[NC];
-  float acc = 0.0f;
+  group_levels<kLPT>([&](auto o) { m = fmaxf(m, xor_lanes<decltype(o)::value>(m)); });
+  float vs[kVirt];
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    p[c] = ok[c] ? expf32(l[c] - m) : 0.0f;
-    acc = acc + p[c];
-  }
-  const float denom = wave_sum_tree(acc);
-  float sc[NC];
+  for (int a = 0; a < kVirt; ++a) vs[a] = 0.0f;
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    p[c] = p[c] / denom;
-    sc[c] = bias ? p[c] + (ok[c] ? bias[c * kWave + lane] : 0.0f) : p[c];
+  for (int q = 0; q < kNV; ++q) {
+    p[q] = (ok >> q) & 1u ? expf32(p[q] - m) : 0.0f;
+    vs[q % kVirt] = vs[q % kVirt] + p[q];
   }
+  float den;
+  if constexpr (kVirt == 4) den = (vs[0] + vs[2]) + (vs[1] + vs[3]);  // distances 32, 16
+  else den = vs[0];
+  group_levels<kLPT>([&](auto o) { den = den + xor_lanes<decltype(o)::value>(den); });
+  float sc[kNV];
+#pragma unroll
+  for (int q = 0; q < kNV; ++q) {
+    p[q] = p[q] / den;
+    sc[q] = bias ? p[q] + ((ok >> q) & 1u ? bias[i + kLPT * q] : 0.0f) : p[q];
+  }
+  TokenRoute<kLPT, kNV> r;
+  r.id[0] = r.id[1] = 0;
+  r.w[0] = r.w[1] = 0.0f;
   float psum = 0.0f;
-  float my_p = 0.0f;
-  int my_id = 0;
   for (int k = 0; k < K; ++k) {
-    // lane-local best among not-yet-taken experts
     float bs = -__builtin_inff();
     int bi = 0x7fffffff;
     float bp = 0.0f;
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      if (ok[c] && (sc[c] > bs || bi == 0x7fffffff)) {
-        bs = sc[c];
-        bi = c * kWave + lane;
-        bp = p[c];
+    for (int q = 0; q < kNV; ++q) {
+      if (((ok >> q) & 1u) && (sc[q] > bs || bi == 0x7fffffff)) {
+        bs = sc[q];
+        bi = i + kLPT * q;
+        bp = p[q];
       }
     }
-    // wave arg-max: larger score wins, equal scores -> lower id
-    argmax_step<32>(bs, bi, bp);
-    argmax_step<16>(bs, bi, bp);
-    argmax_step<8>(bs, bi, bp);
-    argmax_step<4>(bs, bi, bp);
-    argmax_step<2>(bs, bi, bp);
-    argmax_step<1>(bs, bi, bp);
-    // owner lane retires the winner
+    group_levels<kLPT>([&](auto o) { argmax_step<decltype(o)::value>(bs, bi, bp); });
 #pragma unroll
-    for (int c = 0; c < NC; ++c)
-      if (c * kWave + lane == bi) ok[c] = false;
+    for (int q = 0; q < kNV; ++q)
+      if (i + kLPT * q == bi) ok &= ~(1u << q);
     psum = psum + bp;
-    if (lane == k) {
-      my_p = bp;
-      my_id = bi;
+    if ((k & (kLPT - 1)) == i) {
+      r.id[k / kLPT] = bi;
+      r.w[k / kLPT] = bp;
     }
   }
-  if (lane < K) {
-    topk_idx[(size_t)t * K + lane] = my_id;
-    topk_w[(size_t)t * K + lane] = my_p / psum;
+  r.w[0] = r.w[0] / psum;
+  r.w[1] = r.w[1] / psum;
+  return r;
+}
+
+// Router only: kLPT lanes per token, 256 threads.
+template <int kLPT, int kNV>
+__global__ __launch_bounds__(256) void router_topk_kernel(
+    const float* __restrict__ logits, const float* __restrict__ bias, int T, int E, int K,
+    int32_t* __restrict__ topk_idx, float* __restrict__ topk_w) {
+  const int i = threadIdx.x & (kLPT - 1);
+  const int t = blockIdx.x * (256 / kLPT) + threadIdx.x / kLPT;
+  if (t >= T) return;  // whole token groups leave; no workgroup barrier below
+  const TokenRoute<kLPT, kNV> r = route_token<kLPT, kNV>(logits + (size_t)t * E, bias, E, K, i);
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const int k = s * kLPT + i;
+    if (k < K) {
+      topk_idx[(size_t)t * K + k] = r.id[s];
+      topk_w[(size_t)t * K + k] = r.w[s];
+    }
   }
+}
+
+// Router backward.  With p = softmax(l), the picks s_0..s_{K-1},
+// S = sum_k p[s_k] (pick order) and w_k = p[s_k] / S, the gradient g_k of
+// w_k gives
+//   c = sum_k g_k w_k,  dp[s_k] = (g_k - c) / S  (0 for experts not picked),
+//   dl_e = p_e (dp_e - sum_k p[s_k] dp[s_k]).
+// The bias only selects, so it has no gradient.  p is recomputed exactly as
+// the forward computes it; every lane evaluates the K-term sums itself (the
+// picked probabilities from their logits), so no lane exchange is needed
+// beyond the softmax reductions.
+template <int kLPT, int kNV>
+__global__ __launch_bounds__(256) void router_topk_bwd_kernel(
+    const float* __restrict__ logits, const int32_t* __restrict__ topk_idx,
+    const float* __restrict__ dtopk_w, int T, int E, int K, float* __restrict__ dlogits) {
+  constexpr int kVirt = 64 / kLPT;
+  const int i = threadIdx.x & (kLPT - 1);
+  const int t = blockIdx.x * (256 / kLPT) + threadIdx.x / kLPT;
+  if (t >= T) return;
+  const float* row = logits + (size_t)t * E;
+  float p[kNV];
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int q = 0; q < kNV; ++q) {
+    const int e = i + kLPT * q;
+    p[q] = e < E ? row[e] : -__builtin_inff();
+    m = fmaxf(m, p[q]);
+  }
+  group_levels<kLPT>([&](auto o) { m = fmaxf(m, xor_lanes<decltype(o)::value>(m)); });
+  float vs[kVirt];
+#pragma unroll
+  for (int a = 0; a < kVirt; ++a) vs[a] = 0.0f;
+#pragma unroll
+  for (int q = 0; q < kNV; ++q) {
+    p[q] = i + kLPT * q < E ? expf32(p[q] - m) : 0.0f;
+    vs[q % kVirt] = vs[q % kVirt] + p[q];
+  }
+  float den;
+  if constexpr (kVirt == 4) den = (vs[0] + vs[2]) + (vs[1] + vs[3]);
+  else den = vs[0];
+  group_levels<kLPT>([&](auto o) { den = den + xor_lanes<decltype(o)::value>(den); });
+#pragma unroll
+  for (int q = 0; q < kNV; ++q) p[q] = p[q] / den;
+  const int32_t* ids = topk_idx + (size_t)t * K;
+  const float* g = dtopk_w + (size_t)t * K;
+  float psum = 0.0f;
+  for (int k = 0; k < K; ++k) {
+    const int e = min(max(ids[k], 0), E - 1);
+    psum = psum + expf32(row[e] - m) / den;
+  }
+  float c = 0.0f;
+  for (int k = 0; k < K; ++k) {
+    const int e = min(max(ids[k], 0), E - 1);
+    c = c + g[k] * ((expf32(row[e] - m) / den) / psum);
+  }
+  float dot = 0.0f;
+  float dp[kNV];
+#pragma unroll
+  for (int q = 0; q < kNV; ++q) dp[q] = 0.0f;
+  for (int k = 0; k < K; ++k) {
+    const int e = min(max(ids[k], 0), E - 1);
+    const float pk = expf32(row[e] - m) / den;
+    const float d = (g[k] - c) / psum;
+    dot = dot + pk * d;
+#pragma unroll
+    for (int q = 0; q < kNV; ++q)
+      if (i + kLPT * q == e) dp[q] = d;
+  }
+  float* out = dlogits + (size_t)t * E;
+#pragma unroll
+  for (int q = 0; q < kNV; ++q) {
+    const int e = i + kLPT * q;
+    if (e < E) out[e] = p[q] * (dp[q] - dot);
+  }
+}
+
+// Router fused with the sort's first pass: workgroup s routes every token
+// that has a pair in segment s (pairs s*kSeg .. +kSeg; a token whose pairs
+// straddle two segments is routed by both workgroups, and each writes only
+// its own pairs), counts the segment's picks per expert in LDS and writes
+// the histogram column hist[e][s] that route_rowscan and route_rank consume.
+constexpr int kSegR = 512;  // pairs per segment; equals kSeg below
+template <int kLPT, int kNV>
+__global__ __launch_bounds__(1024) void router_hist_kernel(
+    const float* __restrict__ logits, const float* __restrict__ bias, int T, int E, int K,
+    int nseg, int32_t* __restrict__ topk_idx, float* __restrict__ topk_w,
+    int32_t* __restrict__ hist) {
+  extern __shared__ int32_t hh[];  // [E]
+  const int seg = blockIdx.x;
+  const int R = T * K;
+  for (int e = threadIdx.x; e < E; e += 1024) hh[e] = 0;
+  __syncthreads();
+  const int p0 = seg * kSegR, p1 = min(R, p0 + kSegR);
+  const int t0 = p0 / K, t1 = (p1 - 1) / K;  // tokens with a pair in [p0, p1)
+  const int i = threadIdx.x & (kLPT - 1);
+  for (int t = t0 + threadIdx.x / kLPT; t <= t1; t += 1024 / kLPT) {
+    const TokenRoute<kLPT, kNV> r = route_token<kLPT, kNV>(logits + (size_t)t * E, bias, E, K, i);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int k = s * kLPT + i;
+      const int p = t * K + k;
+      if (k < K && p >= p0 && p < p1) {
+        topk_idx[p] = r.id[s];
+        topk_w[p] = r.w[s];
+        atomicAdd(&hh[r.id[s]], 1);
+      }
+    }
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += 1024) hist[(size_t)e * nseg + seg] = hh[e];
 }
 
 // ------------------------------------------------------------------- sort
@@ -172,7 +331,8 @@ __global__ __launch_bounds__(256) void route_rank_kernel(const int32_t* __restri
                                                          int R, int E, int nseg, int nbits,
                                                          int32_t* __restrict__ offsets,
                                                          int32_t* __restrict__ row_map,
-                                                         int32_t* __restrict__ inv_map) {
+                                                         int32_t* __restrict__ inv_map,
+                                                         int32_t* __restrict__ status) {
   extern __shared__ int32_t c_lds[];  // offs[E] then cur[4][E]
   __shared__ int32_t wtot[4];
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
@@ -199,7 +359,11 @@ __global__ __launch_bounds__(256) void route_rank_kernel(const int32_t* __restri
       if (blockIdx.x == 0) offsets[e] = ex;
     }
   }
-  if (blockIdx.x == 0 && tid == 0) offsets[E] = wtot[0] + wtot[1] + wtot[2] + wtot[3];
+  if (blockIdx.x == 0 && tid == 0) {
+    const int total = wtot[0] + wtot[1] + wtot[2] + wtot[3];
+    offsets[E] = total;
+    *status = R - total;  // pairs dropped for an id outside [0, E)
+  }
   __syncthreads();
 
   const int seg = blockIdx.x * 4 + w;
@@ -217,8 +381,8 @@ __global__ __launch_bounds__(256) void route_rank_kernel(const int32_t* __restri
 #pragma unroll
   for (int i = 0; i < kPerLane; ++i) {
     const int p = p0 + i * kWave + lane;
-    const int e = v[i];
-    const bool valid = (unsigned)e < (unsigned)E;
+    const bool valid = (unsigned)v[i] < (unsigned)E;
+    const int e = valid ? v[i] : E;  // out-of-range ids rank as the sentinel
     uint64_t m = ~0ull;
     for (int b = 0; b < nbits; ++b) {
       const bool bit = (e >> b) & 1;
@@ -233,6 +397,8 @@ __global__ __launch_bounds__(256) void route_rank_kernel(const int32_t* __restri
     if (valid) {
       row_map[r] = p;
       inv_map[p] = r;
+    } else if (p < R) {
+      inv_map[p] = -1;
     }
   }
 }
@@ -243,57 +409,135 @@ static inline int seg_count(int R) { return (R + kSeg - 1) / kSeg; }
 
 using namespace smoe;
 
-extern "C" int smoe_router_topk(const float* logits, const float* bias, int T, int E, int K,
-                                int32_t* topk_idx, float* topk_w, void* stream) {
+// Router instance for E experts: 16 lanes per token up to E = 256, 64 above.
+#define SMOE_ROUTE_DISPATCH(E, LAUNCH) \
+  do {                                 \
+    if ((E) <= 16) LAUNCH(16, 1);      \
+    else if ((E) <= 32) LAUNCH(16, 2); \
+    else if ((E) <= 64) LAUNCH(16, 4); \
+    else if ((E) <= 128) LAUNCH(16, 8); \
+    else if ((E) <= 256) LAUNCH(16, 16); \
+    else if ((E) <= 512) LAUNCH(64, 8); \
+    else LAUNCH(64, 16);               \
+  } while (0)
+
+static int check_router_args(const float* logits, const float* bias, int T, int E, int K,
+                             const int32_t* topk_idx, const float* topk_w) {
   if (T <= 0) return SMOE_EINVAL_DIM;
   if (E <= 0 || E > SMOE_MAX_EXPERTS) return SMOE_EINVAL_EXPERTS;
   if (K <= 0 || K > E || K > 32) return SMOE_EINVAL_TOPK;
+  if ((long long)T * E > 0x7fffffffLL || (long long)T * K > 0x7fffffffLL) return SMOE_EINVAL_DIM;
   if (!logits || !topk_idx || !topk_w) return SMOE_EINVAL_NULL;
   if (((uintptr_t)logits | (uintptr_t)topk_idx | (uintptr_t)topk_w | (uintptr_t)bias) & 3u)
     return SMOE_EINVAL_PTRALIGN;
-  const int nc = (E + kWave - 1) / kWave;
-  dim3 grid((T + 3) / 4), block(256);
+  return SMOE_OK;
+}
+
+extern "C" int smoe_router_topk(const float* logits, const float* bias, int T, int E, int K,
+                                int32_t* topk_idx, float* topk_w, void* stream) {
+  const int st = check_router_args(logits, bias, T, E, K, topk_idx, topk_w);
+  if (st) return st;
   hipStream_t s = (hipStream_t)stream;
-#define SMOE_ROUTER(NC) \
-  router_topk_kernel<NC><<<grid, block, 0, s>>>(logits, bias, T, E, K, topk_idx, topk_w)
-  if (nc <= 1) SMOE_ROUTER(1);
-  else if (nc <= 2) SMOE_ROUTER(2);
-  else if (nc <= 4) SMOE_ROUTER(4);
-  else if (nc <= 8) SMOE_ROUTER(8);
-  else SMOE_ROUTER(16);
+#define SMOE_ROUTER(LPT, NV)                                                          \
+  router_topk_kernel<LPT, NV><<<dim3((T + 256 / LPT - 1) / (256 / LPT)), dim3(256), 0, s>>>( \
+      logits, bias, T, E, K, topk_idx, topk_w)
+  SMOE_ROUTE_DISPATCH(E, SMOE_ROUTER);
 #undef SMOE_ROUTER
   SMOE_RETURN_LAUNCH();
 }
 
+extern "C" int smoe_router_topk_bwd(const float* logits, const int32_t* topk_idx,
+                                    const float* dtopk_w, int T, int E, int K, float* dlogits,
+                                    void* stream) {
+  if (T <= 0) return SMOE_EINVAL_DIM;
+  if (E <= 0 || E > SMOE_MAX_EXPERTS) return SMOE_EINVAL_EXPERTS;
+  if (K <= 0 || K > E || K > 32) return SMOE_EINVAL_TOPK;
+  if ((long long)T * E > 0x7fffffffLL) return SMOE_EINVAL_DIM;
+  if (!logits || !topk_idx || !dtopk_w || !dlogits) return SMOE_EINVAL_NULL;
+  if (((uintptr_t)logits | (uintptr_t)topk_idx | (uintptr_t)dtopk_w | (uintptr_t)dlogits) & 3u)
+    return SMOE_EINVAL_PTRALIGN;
+  hipStream_t s = (hipStream_t)stream;
+#define SMOE_RBWD(LPT, NV)                                                                \
+  router_topk_bwd_kernel<LPT, NV><<<dim3((T + 256 / LPT - 1) / (256 / LPT)), dim3(256), 0, s>>>( \
+      logits, topk_idx, dtopk_w, T, E, K, dlogits)
+  SMOE_ROUTE_DISPATCH(E, SMOE_RBWD);
+#undef SMOE_RBWD
+  SMOE_RETURN_LAUNCH();
+}
+
+// Workspace: a 16-byte status block (int32 dropped-pair count first), then
+// the per-segment histogram hist[E][nseg].
+constexpr size_t kStatusBytes = 16;
+
 extern "C" size_t smoe_route_sort_workspace_size(int T, int K, int E) {
   if (T <= 0 || K <= 0 || E <= 0) return 0;
   const size_t R = (size_t)T * K;
-  return (size_t)E * seg_count((int)R) * sizeof(int32_t);
+  return kStatusBytes + (size_t)E * seg_count((int)R) * sizeof(int32_t);
+}
+
+static int check_sort_args(int T, int K, int E, const int32_t* row_map, const int32_t* inv_map,
+                           const int32_t* counts, const int32_t* offsets, const void* ws,
+                           size_t ws_bytes) {
+  if (T <= 0) return SMOE_EINVAL_DIM;
+  if (E <= 0 || E > SMOE_MAX_EXPERTS) return SMOE_EINVAL_EXPERTS;
+  if (K <= 0 || K > E || K > 32) return SMOE_EINVAL_TOPK;
+  if ((long long)T * K > 0x7fffffffLL) return SMOE_EINVAL_DIM;
+  if (!row_map || !inv_map || !counts || !offsets) return SMOE_EINVAL_NULL;
+  if (((uintptr_t)row_map | (uintptr_t)inv_map | (uintptr_t)counts | (uintptr_t)offsets) & 3u)
+    return SMOE_EINVAL_PTRALIGN;
+  if (!ws || ((uintptr_t)ws & 15u)) return ws ? SMOE_EINVAL_PTRALIGN : SMOE_EINVAL_WORKSPACE;
+  if (ws_bytes < smoe_route_sort_workspace_size(T, K, E)) return SMOE_EINVAL_WORKSPACE;
+  return SMOE_OK;
+}
+
+// Passes 2 and 3 of the sort, from a filled histogram.
+static void sort_tail(const int32_t* topk_idx, int R, int E, int nseg, int32_t* row_map,
+                      int32_t* inv_map, int32_t* counts, int32_t* offsets, void* ws,
+                      hipStream_t s) {
+  int nbits = 1;
+  while ((1 << nbits) <= E) ++nbits;  // ids 0..E (E is the sentinel)
+  int32_t* status = (int32_t*)ws;
+  int32_t* hist = (int32_t*)((char*)ws + kStatusBytes);
+  route_rowscan_kernel<<<dim3((E + 3) / 4), dim3(256), 0, s>>>(hist, E, nseg, counts);
+  route_rank_kernel<<<dim3((nseg + 3) / 4), dim3(256), (size_t)5 * E * sizeof(int32_t), s>>>(
+      topk_idx, hist, counts, R, E, nseg, nbits, offsets, row_map, inv_map, status);
 }
 
 extern "C" int smoe_route_sort(const int32_t* topk_idx, int T, int K, int E, int32_t* row_map,
                                int32_t* inv_map, int32_t* counts, int32_t* offsets, void* ws,
                                size_t ws_bytes, void* stream) {
-  if (T <= 0) return SMOE_EINVAL_DIM;
-  if (E <= 0 || E > SMOE_MAX_EXPERTS) return SMOE_EINVAL_EXPERTS;
-  if (K <= 0 || K > E || K > 32) return SMOE_EINVAL_TOPK;
-  if ((long long)T * K > 0x7fffffffLL) return SMOE_EINVAL_DIM;
-  if (!topk_idx || !row_map || !inv_map || !counts || !offsets) return SMOE_EINVAL_NULL;
-  if (((uintptr_t)topk_idx | (uintptr_t)row_map | (uintptr_t)inv_map | (uintptr_t)counts |
-       (uintptr_t)offsets) & 3u)
-    return SMOE_EINVAL_PTRALIGN;
-  if (!ws || ws_bytes < smoe_route_sort_workspace_size(T, K, E)) return SMOE_EINVAL_WORKSPACE;
+  int st = check_sort_args(T, K, E, row_map, inv_map, counts, offsets, ws, ws_bytes);
+  if (st) return st;
+  if (!topk_idx) return SMOE_EINVAL_NULL;
+  if ((uintptr_t)topk_idx & 3u) return SMOE_EINVAL_PTRALIGN;
   const int R = T * K;
   const int nseg = seg_count(R);
-  int nbits = 1;
-  while ((1 << nbits) <= E) ++nbits;  // ids 0..E (E is the sentinel)
-  int32_t* hist = (int32_t*)ws;
+  int32_t* hist = (int32_t*)((char*)ws + kStatusBytes);
   hipStream_t s = (hipStream_t)stream;
-  const dim3 grid((nseg + 3) / 4), block(256);
-  route_hist_kernel<<<grid, block, (size_t)4 * E * sizeof(int32_t), s>>>(topk_idx, R, E, nseg,
-                                                                        hist);
-  route_rowscan_kernel<<<dim3((E + 3) / 4), block, 0, s>>>(hist, E, nseg, counts);
-  route_rank_kernel<<<grid, block, (size_t)5 * E * sizeof(int32_t), s>>>(
-      topk_idx, hist, counts, R, E, nseg, nbits, offsets, row_map, inv_map);
+  route_hist_kernel<<<dim3((nseg + 3) / 4), dim3(256), (size_t)4 * E * sizeof(int32_t), s>>>(
+      topk_idx, R, E, nseg, hist);
+  sort_tail(topk_idx, R, E, nseg, row_map, inv_map, counts, offsets, ws, s);
+  SMOE_RETURN_LAUNCH();
+}
+
+extern "C" int smoe_route_topk_sort(const float* logits, const float* bias, int T, int E, int K,
+                                    int32_t* topk_idx, float* topk_w, int32_t* row_map,
+                                    int32_t* inv_map, int32_t* counts, int32_t* offsets,
+                                    void* ws, size_t ws_bytes, void* stream) {
+  int st = check_router_args(logits, bias, T, E, K, topk_idx, topk_w);
+  if (st) return st;
+  st = check_sort_args(T, K, E, row_map, inv_map, counts, offsets, ws, ws_bytes);
+  if (st) return st;
+  const int R = T * K;
+  const int nseg = seg_count(R);
+  int32_t* hist = (int32_t*)((char*)ws + kStatusBytes);
+  hipStream_t s = (hipStream_t)stream;
+  static_assert(kSegR == kSeg, "fused router segments are the sort's segments");
+#define SMOE_RHIST(LPT, NV)                                                                \
+  router_hist_kernel<LPT, NV><<<dim3(nseg), dim3(1024), (size_t)E * sizeof(int32_t), s>>>( \
+      logits, bias, T, E, K, nseg, topk_idx, topk_w, hist)
+  SMOE_ROUTE_DISPATCH(E, SMOE_RHIST);
+#undef SMOE_RHIST
+  sort_tail(topk_idx, R, E, nseg, row_map, inv_map, counts, offsets, ws, s);
   SMOE_RETURN_LAUNCH();
 }

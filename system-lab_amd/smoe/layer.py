@@ -15,14 +15,55 @@ from torch import nn
 from . import ops
 
 
+class _SimpleMoEFunction(torch.autograd.Function):
+    """Autograd node of one SimpleMoE forward.  The forward keeps the
+    intermediates the fp8 backward needs; the backward is
+    ``SimpleMoE.backward_from`` (every stage a HIP kernel) plus the router
+    backward into the logits.  The gating linear that produces the logits
+    (x @ w_gate) sits outside this node, so autograd carries dlogits on into
+    x and w_gate.  Weight gradients are computed in fp32; a parameter with a
+    ``main_grad`` fp32 buffer (Megatron's gradient-accumulation convention)
+    has them accumulated there, otherwise they are returned in the
+    parameter's dtype."""
+
+    @staticmethod
+    def forward(ctx, x, logits, w1, w2, module):
+        out, inter = module._forward_impl(x, logits, save=True)
+        ctx.module = module
+        ctx.inter = inter
+        ctx.dtypes = (x.dtype, w1.dtype, w2.dtype)
+        ctx.main_grads = (getattr(w1, "main_grad", None), getattr(w2, "main_grad", None))
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        g = ctx.module.backward_from(ctx.inter, dout.to(torch.bfloat16).contiguous())
+        ctx.inter = None
+        grads = []
+        for dw, mg, dt in zip((g["dw1"], g["dw2"]), ctx.main_grads, ctx.dtypes[1:]):
+            if mg is not None:
+                mg.add_(dw)
+                grads.append(None)
+            else:
+                grads.append(dw.to(dt))
+        return g["dx"].to(ctx.dtypes[0]), g["dlogits"], grads[0], grads[1], None
+
+
 class SimpleMoE(nn.Module):
     """Dropless top-k MoE FFN with SwiGLU experts in blockwise fp8.
 
     Parameters follow the notes' naming: ``w1`` [E, 2I, H] holds the gate
     rows [0, I) and up rows [I, 2I) of fc1 in [N, K] layout; ``w2`` [E, H, I]
     is fc2.  ``w_gate`` [H, E] is the router's gating linear.
-    Weights are quantised to fp8 with 128x128 block scales on first use and
-    cached (``refresh_fp8_cache`` re-quantises after an update).
+    Weights are quantised to fp8 with 128x128 block scales on first use; the
+    cache is keyed on the parameters' storage and version counters, so an
+    in-place update (an optimizer step) re-quantises on the next call.
+
+    Under autograd (grad mode on and an input or parameter requiring grad),
+    ``forward`` records one graph node whose backward runs the fp8 backward
+    (``loss.backward()`` fills w1.grad, w2.grad, w_gate.grad and x.grad).
+    Without autograd it is the inference path: SwiGLU and its requantisation
+    run in the fc1 epilogue and nothing is saved.
     """
 
     def __init__(self, hidden: int, intermediate: int, num_experts: int, top_k: int,
@@ -36,36 +77,76 @@ class SimpleMoE(nn.Module):
         self.w2 = nn.Parameter(torch.empty(num_experts, hidden, intermediate, **kw))
         self.register_buffer("router_bias", torch.zeros(num_experts, device=device) if router_bias else None)
         self._fp8 = None
+        self._fp8_key = None
+        self._fp8_t = None
 
     @torch.no_grad()
     def reset_parameters(self, generator: torch.Generator | None = None, std: float = 0.02):
         for p in (self.w_gate, self.w1, self.w2):
             p.copy_(torch.randn(p.shape, generator=generator, dtype=torch.float32,
                                 device=generator.device if generator is not None else p.device).to(p) * std)
-        self._fp8 = None
+
+    def _weights_key(self):
+        return tuple((p.data_ptr(), p._version, tuple(p.shape)) for p in (self.w1, self.w2))
 
     @torch.no_grad()
     def refresh_fp8_cache(self):
-        w1q, w1s = ops.quantize_weight_blockwise(self.w1.detach().contiguous())
-        w2q, w2s = ops.quantize_weight_blockwise(self.w2.detach().contiguous())
+        w1q, w1s = ops.quantize_weight_blockwise(self.w1.detach().to(torch.bfloat16).contiguous())
+        w2q, w2s = ops.quantize_weight_blockwise(self.w2.detach().to(torch.bfloat16).contiguous())
         self._fp8 = (w1q, w1s, w2q, w2s)
+        self._fp8_key = self._weights_key()
+        self._fp8_t = None
         return self._fp8
 
     def fp8_weights(self):
-        return self._fp8 if self._fp8 is not None else self.refresh_fp8_cache()
+        """(w1q, w1s, w2q, w2s), re-quantised when w1 or w2 changed since the
+        cache was filled (storage moved or version counter advanced)."""
+        if self._fp8 is None or self._fp8_key != self._weights_key():
+            self.refresh_fp8_cache()
+        return self._fp8
 
-    @torch.no_grad()
+    def fp8_weights_t(self):
+        """The dgrad weights: (w1q^T, w1s^T, w2q^T, w2s^T), cached with the
+        fp8 weights they come from."""
+        w1q, w1s, w2q, w2s = self.fp8_weights()
+        if self._fp8_t is None:
+            self._fp8_t = ops.transpose_blockwise(w1q, w1s) + ops.transpose_blockwise(w2q, w2s)
+        return self._fp8_t
+
     def forward(self, x: torch.Tensor, logits: torch.Tensor | None = None,
                 return_intermediates: bool = False):
         """x [T, H] bf16 -> y [T, H] bf16.  ``logits`` [T, E] f32 may be given
         directly (the benchmark configs specify router logits); otherwise
-        they are x @ w_gate in fp32."""
+        they are x @ w_gate in fp32.  ``return_intermediates`` returns
+        (y, intermediates) for a later ``backward_from`` without recording an
+        autograd graph."""
+        if return_intermediates:
+            with torch.no_grad():
+                if logits is None:
+                    logits = x.float() @ self.w_gate
+                    out, inter = self._forward_impl(x, logits, save=True)
+                    inter["logits_from_gate"] = True
+                    return out, inter
+                return self._forward_impl(x, logits, save=True)
         if logits is None:
             logits = x.float() @ self.w_gate
+        params = (x, logits, self.w1, self.w2)
+        if torch.is_grad_enabled() and any(t.requires_grad for t in params):
+            return _SimpleMoEFunction.apply(x, logits, self.w1, self.w2, self)
+        with torch.no_grad():
+            return self._forward_impl(x, logits, save=False)
+
+    @torch.no_grad()
+    def _forward_impl(self, x: torch.Tensor, logits: torch.Tensor, save: bool):
+        x = x.detach().to(torch.bfloat16).contiguous()
+        logits = logits.detach().float().contiguous()
         w1q, w1s, w2q, w2s = self.fp8_weights()
-        idx, w = ops.router_topk(logits.contiguous(), self.top_k, self.router_bias)
-        xq, xs, row_map, inv_map, counts, offsets = ops.permute_quant(x, idx, self.num_experts)
-        if return_intermediates:
+        # router and expert sort in three launches (the sort's histogram is
+        # counted inside the router launch)
+        idx, w, row_map, inv_map, counts, offsets = ops.route_topk_sort(logits, self.top_k,
+                                                                        self.router_bias)
+        xq, xs = ops.permute_quant_rows(x, inv_map, self.top_k)
+        if save:
             # the backward pass needs c1 and bf16 h, so fc1 and SwiGLU run
             # as two kernels here
             c1 = ops.grouped_gemm_fp8(xq, xs, w1q, w1s, offsets)
@@ -75,10 +156,10 @@ class SimpleMoE(nn.Module):
             hq, hs = ops.grouped_gemm_fp8_swiglu(xq, xs, w1q, w1s, offsets)
         y = ops.grouped_gemm_fp8(hq, hs, w2q, w2s, offsets)
         out = ops.unpermute_combine(y, inv_map, w)
-        if return_intermediates:
-            return out, dict(x=x, topk_idx=idx, topk_w=w, row_map=row_map, inv_map=inv_map,
-                             counts=counts, offsets=offsets, xq=xq, xs=xs, c1=c1, hq=hq,
-                             hs=hs, h=h, y=y)
+        if save:
+            return out, dict(x=x, logits=logits, topk_idx=idx, topk_w=w, row_map=row_map,
+                             inv_map=inv_map, counts=counts, offsets=offsets, xq=xq, xs=xs,
+                             c1=c1, hq=hq, hs=hs, h=h, y=y)
         return out
 
     @torch.no_grad()
@@ -91,14 +172,15 @@ class SimpleMoE(nn.Module):
         fc2 dgrad (W2^T) and fc2 wgrad (128x1 dy, h) -> SwiGLU bwd fused with
         both quantisations of dc1 -> fc1 dgrad (W1^T) and fc1 wgrad (128x1
         dc1, sorted x) -> sum of the K replicas into dx.
-        Returns dx [T,H] bf16, dw1 [E,2I,H] f32, dw2 [E,H,I] f32 and the
-        router-weight gradient dtopk_w [T,K] f32 (plus dy's 1x128 quantisation dyq,
-        dys and the intermediates dh, dxs).  Every stage is a HIP kernel;
-        nothing synchronises with the host."""
-        w1q, w1s, w2q, w2s = self.fp8_weights()
-        if getattr(self, "_fp8_t", None) is None or self._fp8_t[0] is not w1q:
-            self._fp8_t = (w1q,) + ops.transpose_blockwise(w1q, w1s) + ops.transpose_blockwise(w2q, w2s)
-        _, w1tq, w1ts, w2tq, w2ts = self._fp8_t
+        Returns dx [T,H] bf16, dw1 [E,2I,H] f32, dw2 [E,H,I] f32, the
+        router-weight gradient dtopk_w [T,K] f32 and its continuation through
+        the renormalisation and softmax, dlogits [T,E] f32 (plus dy's 1x128
+        quantisation dyq, dys and the intermediates dh, dxs).  When the
+        forward computed the logits itself (x @ w_gate), dx also holds the
+        gating linear's contribution and dw_gate [H,E] f32 is returned.
+        Every expert stage is a HIP kernel; the gating linear's two small
+        fp32 matmuls are library GEMMs.  Nothing synchronises with the host."""
+        w1tq, w1ts, w2tq, w2ts = self.fp8_weights_t()
         off, inv = inter["offsets"], inter["inv_map"]
         K = self.top_k
         # The weight gradients are off the dx critical path.  They run on a
@@ -137,8 +219,17 @@ class SimpleMoE(nn.Module):
             ops.grouped_gemm_fp8_wgrad(dcTq, dcTs, xTq, xTs, pad, ld, out=dw1)
         dxs = ops.grouped_gemm_fp8(dcq, dcs, w1tq, w1ts, off)
         dx = ops.unpermute_combine(dxs, inv, ones)
+        # router: renormalisation + softmax backward into the logits
+        dlogits = ops.router_topk_bwd(inter["logits"], inter["topk_idx"], dw)
+        out = dict(dx=dx, dw1=dw1, dw2=dw2, dtopk_w=dw, dlogits=dlogits, dyq=dyq, dys=dys,
+                   dh=dh, dxs=dxs)
+        if inter.get("logits_from_gate"):
+            # logits = x @ w_gate in fp32: the gating linear's gradients
+            x32 = inter["x"].float()
+            out["dx"] = (dx.float() + dlogits @ self.w_gate.detach().t()).to(torch.bfloat16)
+            out["dw_gate"] = x32.t() @ dlogits
         main.wait_stream(side)
-        return dict(dx=dx, dw1=dw1, dw2=dw2, dtopk_w=dw, dyq=dyq, dys=dys, dh=dh, dxs=dxs)
+        return out
 
     def _side_stream(self, device) -> torch.cuda.Stream:
         s = getattr(self, "_side", None)

@@ -69,10 +69,63 @@ def router_topk(logits: torch.Tensor, top_k: int, bias: torch.Tensor | None = No
     return idx, w
 
 
+def router_topk_bwd(logits: torch.Tensor, topk_idx: torch.Tensor, dtopk_w: torch.Tensor):
+    """Backward of ``router_topk`` through the renormalisation and the
+    softmax: dtopk_w [T,K] f32 -> dlogits [T,E] f32 (the selection bias has
+    no gradient; ``topk_idx`` are the forward's picks)."""
+    _check(logits, "logits", (torch.float32,), 2)
+    _check(topk_idx, "topk_idx", (torch.int32,), 2)
+    _check(dtopk_w, "dtopk_w", (torch.float32,), 2)
+    T, E = logits.shape
+    if topk_idx.shape[0] != T or dtopk_w.shape != topk_idx.shape:
+        raise ValueError("topk_idx and dtopk_w must be [T, K] for logits [T, E]")
+    K = topk_idx.shape[1]
+    dl = torch.empty((T, E), dtype=torch.float32, device=logits.device)
+    _C.call("smoe_router_topk_bwd", _ptr(logits), _ptr(topk_idx), _ptr(dtopk_w), T, E, K,
+            _ptr(dl), _stream())
+    return dl
+
+
 # -------------------------------------------------------------------- sort
+# Byte offset of the routing status word in the sort workspace
+# (SMOE_ROUTE_STATUS_OFFSET): the number of pairs whose expert id was
+# outside [0, E), rewritten by every sort.
+ROUTE_STATUS_OFFSET = 0
+_route_status: dict = {}
+
+
+def _sort_workspace(T: int, K: int, E: int, dev) -> torch.Tensor:
+    nbytes = int(_C.lib().smoe_route_sort_workspace_size(T, K, E))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    # the status word of this call; check_route_status() reads it lazily
+    _route_status[dev] = ws[ROUTE_STATUS_OFFSET:ROUTE_STATUS_OFFSET + 4].view(torch.int32)
+    return ws
+
+
+def last_route_status(device=None) -> torch.Tensor:
+    """Device int32 [1]: pairs dropped for an out-of-range expert id by the
+    most recent sort on ``device`` (0 when every id was valid).  Reading it
+    does not synchronise; converting it to a Python int does."""
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    if dev not in _route_status:
+        raise RuntimeError(f"no routing sort has run on {dev}")
+    return _route_status[dev]
+
+
+def check_route_status(device=None) -> None:
+    """Synchronise and raise if the most recent sort on ``device`` met
+    expert ids outside [0, E): those pairs got no row (inv_map = -1) and
+    contribute nothing to the combine."""
+    n = int(last_route_status(device).item())
+    if n:
+        raise ValueError(f"routing: {n} (token, slot) pairs had an expert id outside [0, E) "
+                         "and were dropped")
+
+
 def route_sort(topk_idx: torch.Tensor, num_experts: int):
     """Stable expert sort of the T*K pairs.  -> (row_map [R], inv_map [R],
-    counts [E], offsets [E+1]), all int32 on the device."""
+    counts [E], offsets [E+1]), all int32 on the device.  Ids outside
+    [0, E) get no row (inv_map = -1); ``check_route_status`` reports them."""
     _check(topk_idx, "topk_idx", (torch.int32,), 2)
     T, K = topk_idx.shape
     dev = topk_idx.device
@@ -81,11 +134,35 @@ def route_sort(topk_idx: torch.Tensor, num_experts: int):
     inv_map = torch.empty(R, dtype=torch.int32, device=dev)
     counts = torch.empty(num_experts, dtype=torch.int32, device=dev)
     offsets = torch.empty(num_experts + 1, dtype=torch.int32, device=dev)
-    nbytes = _C.lib().smoe_route_sort_workspace_size(T, K, num_experts)
-    ws = torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=dev)
+    ws = _sort_workspace(T, K, num_experts, dev)
     _C.call("smoe_route_sort", _ptr(topk_idx), T, K, num_experts, _ptr(row_map), _ptr(inv_map),
             _ptr(counts), _ptr(offsets), _ptr(ws), ws.numel(), _stream())
     return row_map, inv_map, counts, offsets
+
+
+def route_topk_sort(logits: torch.Tensor, top_k: int, bias: torch.Tensor | None = None):
+    """Router fused with the expert sort (the sort's histogram is counted in
+    the router launch): the outputs of ``router_topk`` then ``route_sort``,
+    byte for byte.  -> (topk_idx, topk_w, row_map, inv_map, counts, offsets)."""
+    _check(logits, "logits", (torch.float32,), 2)
+    T, E = logits.shape
+    if bias is not None:
+        _check(bias, "bias", (torch.float32,), 1)
+        if bias.numel() != E:
+            raise ValueError("bias must have E entries")
+    dev = logits.device
+    R = T * top_k
+    idx = torch.empty((T, top_k), dtype=torch.int32, device=dev)
+    w = torch.empty((T, top_k), dtype=torch.float32, device=dev)
+    row_map = torch.empty(R, dtype=torch.int32, device=dev)
+    inv_map = torch.empty(R, dtype=torch.int32, device=dev)
+    counts = torch.empty(E, dtype=torch.int32, device=dev)
+    offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    ws = _sort_workspace(T, top_k, E, dev)
+    _C.call("smoe_route_topk_sort", _ptr(logits), _ptr(bias), T, E, top_k, _ptr(idx), _ptr(w),
+            _ptr(row_map), _ptr(inv_map), _ptr(counts), _ptr(offsets), _ptr(ws), ws.numel(),
+            _stream())
+    return idx, w, row_map, inv_map, counts, offsets
 
 
 # ---------------------------------------------------------------- dispatch
@@ -123,8 +200,7 @@ def permute_quant(x: torch.Tensor, topk_idx: torch.Tensor, num_experts: int):
     offsets = torch.empty(num_experts + 1, dtype=torch.int32, device=dev)
     xq = torch.empty((R, H), dtype=FP8, device=dev)
     xs = torch.empty((R, H // GROUP), dtype=torch.float32, device=dev)
-    nbytes = _C.lib().smoe_route_sort_workspace_size(T, K, num_experts)
-    ws = torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=dev)
+    ws = _sort_workspace(T, K, num_experts, dev)
     _C.call("smoe_dispatch_quant", _ptr(x), _ptr(topk_idx), T, H, K, num_experts,
             _ptr(row_map), _ptr(inv_map), _ptr(counts), _ptr(offsets), _ptr(xq), _ptr(xs),
             _ptr(ws), ws.numel(), _stream())
@@ -235,6 +311,10 @@ def unpermute_combine(y: torch.Tensor, inv_map: torch.Tensor, topk_w: torch.Tens
         raise ValueError("y / inv_map must have T*K rows")
     if out is None:
         out = torch.empty((T, H), dtype=torch.bfloat16, device=y.device)
+    else:
+        _check(out, "out", (torch.bfloat16,), 2)
+        if tuple(out.shape) != (T, H):
+            raise ValueError(f"out must be [{T}, {H}] bf16")
     _C.call("smoe_unpermute_combine", _ptr(y), _ptr(inv_map), _ptr(topk_w), T, K, H, _ptr(out),
             _stream())
     return out
@@ -258,6 +338,10 @@ def transpose_blockwise(wq: torch.Tensor, ws: torch.Tensor):
     _check(wq, "wq", (FP8, torch.uint8), 3)
     _check(ws, "ws", (torch.float32,), 3)
     E, N, Kd = wq.shape
+    if N % GROUP or Kd % GROUP:
+        raise ValueError("wq dims must be multiples of 128")
+    if tuple(ws.shape) != (E, N // GROUP, Kd // GROUP):
+        raise ValueError(f"ws must be [{E}, {N // GROUP}, {Kd // GROUP}] for wq {tuple(wq.shape)}")
     wqT = torch.empty((E, Kd, N), dtype=FP8, device=wq.device)
     wsT = torch.empty((E, Kd // GROUP, N // GROUP), dtype=torch.float32, device=wq.device)
     _C.call("smoe_transpose_blockwise_fp8", _ptr(_bytes(wq)), _ptr(ws), E, N, Kd,
@@ -277,6 +361,12 @@ def quant_cols(x: torch.Tensor, offsets: torch.Tensor, gather: torch.Tensor | No
     if gather is not None:
         _check(gather, "gather", (torch.int32,), 1)
         R = gather.numel()
+        if gather_div < 1:
+            raise ValueError("gather_div must be >= 1")
+        # the kernel reads x row gather[r] // gather_div with gather[r] < R
+        if x.shape[0] * gather_div < R:
+            raise ValueError(f"x has {x.shape[0]} rows; gather of {R} rows / {gather_div} "
+                             f"needs at least {-(-R // gather_div)}")
     else:
         R = x.shape[0]
     E = offsets.numel() - 1
@@ -343,10 +433,14 @@ def grouped_gemm_fp8_wgrad(aTq, aTs, bTq, bTs, pad, ld: int, out: torch.Tensor |
     aT [N, ld], bT [K, ld] -> fp32 [E, N, K] (into ``out`` when given)."""
     _check(aTq, "aTq", (FP8, torch.uint8), 2)
     _check(bTq, "bTq", (FP8, torch.uint8), 2)
+    _check(aTs, "aTs", (torch.float32,), 2)
+    _check(bTs, "bTs", (torch.float32,), 2)
     _check(pad, "pad", (torch.int32,), 1)
     N, K, E = aTq.shape[0], bTq.shape[0], pad.numel() - 1
-    if aTq.shape[1] != ld or bTq.shape[1] != ld:
-        raise ValueError("operands must share the padded row length ld")
+    if aTq.shape[1] != ld or bTq.shape[1] != ld or ld % GROUP:
+        raise ValueError("operands must share the padded row length ld (a multiple of 128)")
+    if tuple(aTs.shape) != (N, ld // GROUP) or tuple(bTs.shape) != (K, ld // GROUP):
+        raise ValueError(f"scales must be [{N}, {ld // GROUP}] and [{K}, {ld // GROUP}]")
     if out is None:
         dW = torch.empty((E, N, K), dtype=torch.float32, device=aTq.device)
     else:
@@ -380,6 +474,8 @@ def unpermute_combine_bwd(dout: torch.Tensor, y: torch.Tensor, inv_map: torch.Te
     _check(topk_w, "topk_w", (torch.float32,), 2)
     T, K = topk_w.shape
     H = dout.shape[1]
+    if dout.shape[0] != T or tuple(y.shape) != (T * K, H) or inv_map.numel() != T * K:
+        raise ValueError("dout must be [T, H], y [T*K, H] and inv_map T*K for topk_w [T, K]")
     dy = torch.empty((T * K, H), dtype=torch.bfloat16, device=dout.device)
     dw = torch.empty((T, K), dtype=torch.float32, device=dout.device)
     _C.call("smoe_unpermute_combine_bwd", _ptr(dout), _ptr(y), _ptr(inv_map), _ptr(topk_w), T, K,

@@ -66,6 +66,20 @@ def test_route_sort_rejects():
     assert lib.smoe_route_sort(None, 16, 2, 8, FAKE, FAKE, FAKE, FAKE, FAKE, 1 << 20, None) == -1
 
 
+def test_route_topk_sort_rejects():
+    lib = _C.lib()
+    need = lib.smoe_route_sort_workspace_size(16, 2, 8)
+    f = lib.smoe_route_topk_sort
+    ok = (FAKE, None, 16, 8, 2, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE)
+    assert f(*ok, FAKE, need - 1, None) == -5
+    assert f(*ok, None, need, None) == -5
+    assert f(*ok, MIS, need, None) == -6
+    assert f(None, None, 16, 8, 2, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, need, None) == -1
+    assert f(FAKE, None, 16, 8, 9, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, need, None) == -7
+    assert f(FAKE, None, 16, 2000, 2, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, need, None) == -4
+    assert f(FAKE, None, 0, 8, 2, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, need, None) == -2
+
+
 def test_gemm_swiglu_combine_router_reject():
     lib = _C.lib()
     g = lib.smoe_grouped_gemm_fp8

@@ -68,6 +68,23 @@ def test_router_bit_exact(dev, T, E, K, bias):
     assert np.array_equal(w.cpu().numpy().view(np.uint32), rw.view(np.uint32))
 
 
+@pytest.mark.parametrize("T,E,K,bias", [(4096, 256, 8, True), (2048, 8, 2, False),
+                                        (300, 1024, 32, False), (1000, 37, 6, True)])
+def test_router_bwd_matches_oracle(dev, T, E, K, bias):
+    """dlogits from the HIP router backward against the float64 oracle
+    (itself pinned to torch autograd); fp32 arithmetic, so a relative bar."""
+    say("router bwd", T, E, K, bias)
+    lg = W.logits(T, E)
+    b = W.router_bias(E) if bias else None
+    idx, _ = ops.router_topk(lg.to(dev), K, None if b is None else b.to(dev))
+    g = torch.randn((T, K), generator=torch.Generator().manual_seed(3))
+    dl = ops.router_topk_bwd(lg.to(dev), idx, g.to(dev)).cpu().numpy().astype(np.float64)
+    ref = O.router_topk_bwd(lg.numpy(), idx.cpu().numpy(), g.numpy().astype(np.float64))
+    d = np.abs(dl - ref)
+    assert d.max() <= 1e-5 * np.abs(ref).max(), d.max() / np.abs(ref).max()
+    assert d.mean() <= 1e-6 * np.abs(ref).mean()
+
+
 def test_router_ties(dev):
     say("router ties")
     rng = np.random.default_rng(11)
@@ -111,6 +128,72 @@ def test_sort_bit_exact(dev, T, K, E, mode):
     else:
         idx = rng.integers(0, E, (T, K)).astype(np.int32)
     _check_sort(dev, idx, E)
+
+
+@pytest.mark.parametrize("T,E,K,bias", [(16384, 256, 8, True), (16384, 128, 8, False),
+                                        (8192, 8, 2, False), (2048, 8, 2, False),
+                                        (1000, 37, 6, True), (333, 1024, 32, False),
+                                        (700, 512, 3, True), (5, 16, 1, False),
+                                        (1, 4, 4, False)])
+def test_route_topk_sort_fused(dev, T, E, K, bias):
+    """Router with the sort's histogram counted in the same launch: the same
+    bytes as router_topk then route_sort, and both equal the oracle.  Shapes
+    cover 16 and 64 lanes per token, K that does not divide the 512-pair
+    segment (tokens straddling two workgroups) and the bench configs."""
+    say("route_topk_sort", T, E, K, bias)
+    lg = W.logits(T, E)
+    b = W.router_bias(E) if bias else None
+    bd = None if b is None else b.to(dev)
+    got = ops.route_topk_sort(lg.to(dev), K, bd)
+    ri, rw = O.router_topk(lg.numpy(), K, None if b is None else b.numpy())
+    ref = (ri, rw) + tuple(O.route_sort(ri, E))
+    names = ("topk_idx", "topk_w", "row_map", "inv_map", "counts", "offsets")
+    for g_, r_, n in zip(got, ref, names):
+        assert np.array_equal(g_.cpu().numpy().view(np.uint32), np.asarray(r_).view(np.uint32)), n
+    assert int(ops.last_route_status().item()) == 0
+
+
+def test_route_sort_out_of_range_ids(dev):
+    """Ids outside [0, E) get no row: inv_map = -1, offsets[E] counts only the
+    valid pairs, the valid pairs keep the stable order, and the status word
+    holds the number dropped; check_route_status raises on it."""
+    say("route_sort out-of-range ids")
+    T, K, E = 3000, 4, 16
+    rng = np.random.default_rng(7)
+    idx = rng.integers(0, E, (T, K)).astype(np.int32)
+    bad = rng.random((T, K)) < 0.01
+    idx[bad] = rng.choice(np.array([E, E + 3, 19, -1, 1 << 20], np.int32), bad.sum())
+    rm, im, cnt, off = ops.route_sort(torch.from_numpy(idx).to(dev), E)
+    flat = idx.reshape(-1)
+    valid = (flat >= 0) & (flat < E)
+    p_valid = np.nonzero(valid)[0]
+    order = p_valid[np.argsort(flat[p_valid], kind="stable")]
+    nv = order.size
+    assert int(ops.last_route_status().item()) == flat.size - nv
+    with pytest.raises(ValueError):
+        ops.check_route_status()
+    im_np = im.cpu().numpy()
+    assert np.all(im_np[~valid] == -1)
+    assert np.array_equal(rm.cpu().numpy()[:nv], order)
+    assert np.array_equal(im_np[order], np.arange(nv))
+    assert np.array_equal(cnt.cpu().numpy(), np.bincount(flat[valid], minlength=E))
+    assert off.cpu().numpy()[-1] == nv
+    # the dropped pairs contribute nothing to the combine
+    H = 128
+    y = torch.randn((T * K, H), device=dev).to(torch.bfloat16)
+    w = torch.ones((T, K), device=dev)
+    out = ops.unpermute_combine(y, im, w).float().cpu().numpy()
+    yv = y.float().cpu().numpy()
+    ref = np.zeros((T, H), np.float32)
+    for t in range(T):
+        for k in range(K):
+            r = im_np[t * K + k]
+            if r >= 0:
+                ref[t] = ref[t] + yv[r]
+    assert np.array_equal(O.f32_to_bf16(ref), np_u16(torch.from_numpy(out).to(torch.bfloat16)))
+    # a clean sort afterwards clears the status
+    ops.route_sort(torch.from_numpy(np.where(valid.reshape(T, K), idx, 0)).to(dev), E)
+    ops.check_route_status()
 
 
 # ---------------------------------------------------------- permute_quant

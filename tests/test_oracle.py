@@ -121,6 +121,28 @@ def test_router_topk_brute_force_with_ties():
 
 
 # ----------------------------------------------------------------- sort
+def test_router_topk_bwd_matches_float64_autograd():
+    """The router backward formula against torch float64 autograd through
+    softmax -> gather of the picks -> renormalisation, with a selection bias
+    (which only changes the picks) and K up to E."""
+    rng = np.random.default_rng(5)
+    for T, E, K, use_bias in ((64, 8, 2, False), (32, 64, 6, True), (16, 256, 8, True), (8, 5, 5, False)):
+        lg = rng.standard_normal((T, E)).astype(np.float32)
+        b = rng.standard_normal(E).astype(np.float32) * 0.5 if use_bias else None
+        idx, _ = O.router_topk(lg, K, b)
+        g = rng.standard_normal((T, K))
+        l64 = torch.tensor(lg, dtype=torch.float64, requires_grad=True)
+        p = torch.softmax(l64, dim=1)
+        pk = torch.gather(p, 1, torch.from_numpy(idx.astype(np.int64)))
+        w = pk / pk.sum(dim=1, keepdim=True)
+        (w * torch.from_numpy(g)).sum().backward()
+        got = O.router_topk_bwd(lg, idx, g)
+        ref = l64.grad.numpy()
+        assert np.abs(got - ref).max() <= 1e-12 * max(1.0, np.abs(ref).max())
+        # each row's logit gradient sums to zero (softmax shift invariance)
+        assert np.abs(got.sum(axis=1)).max() < 1e-12
+
+
 def test_route_sort_reference_worked_example():
     g = np.load(os.path.join(GOLDEN, "worked_example.npz"))
     row_map, inv_map, counts, offsets = O.route_sort(g["topk_idx"], 8)
