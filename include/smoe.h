@@ -103,6 +103,24 @@ int smoe_route_sort(const int32_t* topk_idx, int T, int K, int E, int32_t* row_m
                     size_t ws_bytes, void* stream);
 
 /*
+ * Allocation-free variant of smoe_route_sort (no counterpart in the
+ * reference: it is for callers that cannot allocate device memory, such as
+ * code under HIP graph capture or a serving loop that forbids allocation).
+ * Same arguments and bytes as smoe_route_sort without ws / ws_bytes: the
+ * workspace is a static device array inside the library (one per GPU,
+ * smoe_route_sort_noalloc_max_bytes() bytes, held until the process ends).
+ * Sizes whose workspace would exceed it (E * ceil(T*K/512) * 4 + 16 bytes >
+ * the maximum, e.g. E = 256 with T*K above 2M pairs) return
+ * SMOE_EINVAL_WORKSPACE.  The routing status word is written to the static
+ * array and not exposed: offsets[E] < T*K still reports dropped ids.  Every
+ * call on one GPU shares the array: calls that overlap on one GPU (other
+ * streams or threads) race.  It calls no allocator.
+ */
+size_t smoe_route_sort_noalloc_max_bytes(void);
+int smoe_route_sort_noalloc(const int32_t* topk_idx, int T, int K, int E, int32_t* row_map,
+                            int32_t* inv_map, int32_t* counts, int32_t* offsets, void* stream);
+
+/*
  * Router fused with the sort: smoe_router_topk's outputs plus smoe_route_sort's,
  * with the sort's per-segment expert histogram counted inside the router
  * launch (three launches in all, no host sync).  Same bytes as

@@ -22,6 +22,7 @@
 // A pair whose id lies outside [0, E) gets no row: inv_map[p] = -1, and the
 // number of such pairs is written to the status word at the head of the
 // workspace (0 when every id is valid).
+#include <mutex>
 #include <type_traits>
 
 #include "smoe_common.h"
@@ -540,4 +541,58 @@ extern "C" int smoe_route_topk_sort(const float* logits, const float* bias, int 
 #undef SMOE_RHIST
   sort_tail(topk_idx, R, E, nseg, row_map, inv_map, counts, offsets, ws, s);
   SMOE_RETURN_LAUNCH();
+}
+
+// ---------------------------------------------------- allocation-free sort
+// The sort's workspace (status block + histogram) as a file-scope device
+// array: callers that cannot allocate (HIP graph capture, serving loops)
+// use smoe_route_sort_noalloc.  Each GPU holds its own copy for the life of
+// the process; its device address is looked up once per device with
+// hipGetSymbolAddress and only that address is passed to kernels.  Every
+// call overwrites the whole status block and the histogram columns it uses,
+// so nothing needs clearing between calls; calls that overlap on one GPU
+// (different streams) share the array and race.
+namespace smoe {
+constexpr size_t kScratchBytes = kStatusBytes + ((size_t)1 << 22);  // 4 MiB of histogram
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static void* g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+// The current device's address of `scratch`, or nullptr on a HIP error.
+static void* scratch_ptr(hipError_t* err) {
+  int dev = 0;
+  *err = hipGetDevice(&dev);
+  if (*err != hipSuccess) return nullptr;
+  if (dev < 0 || dev >= kMaxDevices) {
+    *err = hipErrorInvalidDevice;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    *err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (*err != hipSuccess) return nullptr;
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+}  // namespace smoe
+
+extern "C" size_t smoe_route_sort_noalloc_max_bytes(void) { return smoe::kScratchBytes; }
+
+extern "C" int smoe_route_sort_noalloc(const int32_t* topk_idx, int T, int K, int E,
+                                       int32_t* row_map, int32_t* inv_map, int32_t* counts,
+                                       int32_t* offsets, void* stream) {
+  if (T <= 0 || K <= 0 || E <= 0) return SMOE_EINVAL_DIM;
+  if ((long long)T * K > 0x7fffffffLL) return SMOE_EINVAL_DIM;
+  // the sort needs E * ceil(T*K / 512) histogram words: reject what the
+  // static array cannot hold
+  if (smoe_route_sort_workspace_size(T, K, E) > kScratchBytes) return SMOE_EINVAL_WORKSPACE;
+  hipError_t err = hipSuccess;
+  void* ws = scratch_ptr(&err);
+  if (!ws) return err == hipSuccess ? SMOE_EINVAL_WORKSPACE : (int)err;
+  return smoe_route_sort(topk_idx, T, K, E, row_map, inv_map, counts, offsets, ws,
+                         kScratchBytes, stream);
 }

@@ -24,6 +24,8 @@ SIGNATURES = {
     "smoe_router_topk_bwd": (c_int, [P, P, P, c_int, c_int, c_int, P, P]),
     "smoe_route_sort_workspace_size": (c_size_t, [c_int, c_int, c_int]),
     "smoe_route_sort": (c_int, [P, c_int, c_int, c_int, P, P, P, P, P, c_size_t, P]),
+    "smoe_route_sort_noalloc_max_bytes": (c_size_t, []),
+    "smoe_route_sort_noalloc": (c_int, [P, c_int, c_int, c_int, P, P, P, P, P]),
     "smoe_route_topk_sort": (c_int, [P, P, c_int, c_int, c_int, P, P, P, P, P, P, P, c_size_t,
                                      P]),
     "smoe_permute_quant": (c_int, [P, P, c_int, c_int, c_int, P, P, P]),
