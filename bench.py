@@ -39,8 +39,9 @@ sys.path.insert(0, os.path.join(ROOT, "system-lab_amd"))
 
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per permute_quant launch at config 2 from rocprofv3 FETCH_SIZE
-# (x2.0 copy calibration) + WRITE_SIZE (x1.0): profiles/permute_quant_cfg2.md
-PERMUTE_TRAFFIC_BYTES = 1_211_621_376
+# (115,172 KiB x 2.0 copy calibration) + WRITE_SIZE (947,065 KiB x 1.0):
+# profiles/permute_quant_cfg2.md
+PERMUTE_TRAFFIC_BYTES = 1_205_666_816
 FP8_PEAK_TFLOPS = 5000.0
 
 
@@ -306,25 +307,26 @@ def bench_fwd_bwd(dev, steps, warmup):
 
 def bench_ceiling(dev, c, iters=20):
     """The HBM's rate for the dispatch step's traffic mix without the
-    quantisation: smoe_bw_probe reads the config-2 input once (T*H*2 bytes)
-    and writes every 16-byte piece to ``fanout`` places (fanout 8 with the
-    bf16 -> fp8 halving is the permute's 1:4 byte mix), each launch after a
-    cache flush; plus a plain device copy and a read-only pass."""
+    quantisation: smoe_bw_probe reads the config-2 input (T rows of H bf16)
+    with permute_quant's access pattern and writes half its bytes to
+    ``fanout`` scattered rows (fanout 8 = the permute's 1:4 read:write byte
+    mix), each launch after a cache flush; fanout 0 only reads."""
     import torch
     import smoe
-    n_in = c.T * c.H * 2
-    src = torch.ones(n_in // 4, dtype=torch.int32, device=dev)
-    dst = torch.empty(n_in * 8, dtype=torch.uint8, device=dev)
+    row_bytes = c.H * 2
+    src = torch.ones(c.T * row_bytes // 4, dtype=torch.int32, device=dev)
+    dst = torch.empty(c.T * 8 * row_bytes // 2, dtype=torch.uint8, device=dev)
     sink = torch.zeros(4, dtype=torch.int32, device=dev)
     flush = Flush()
-    out = {"bytes_in": n_in}
-    for fanout in (0, 1, 2, 4, 8):
-        fn = lambda: smoe._C.call("smoe_bw_probe", src.data_ptr(), n_in, fanout, dst.data_ptr(),
-                                  dst.numel(), sink.data_ptr(),
+    out = {"bytes_in": c.T * row_bytes, "pattern": "permute_quant's (one wave per row, 1 KiB "
+           "scattered non-temporal row writes)"}
+    for fanout in (0, 2, 4, 8):
+        fn = lambda: smoe._C.call("smoe_bw_probe", src.data_ptr(), c.T, row_bytes, fanout,
+                                  dst.data_ptr(), dst.numel(), sink.data_ptr(),
                                   torch.cuda.current_stream().cuda_stream)
         ms = timed_median(fn, iters, 3, flush)
-        nb = n_in * (1 + fanout)
-        out[f"read1_write{fanout}"] = {"ms": round(ms, 4), "gbs": round(nb / (ms * 1e-3) / 1e9, 1),
+        nb = c.T * row_bytes * (2 + fanout) // 2
+        out[f"read2_write{fanout}"] = {"ms": round(ms, 4), "gbs": round(nb / (ms * 1e-3) / 1e9, 1),
                                        "frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     del src, dst, flush
     torch.cuda.empty_cache()
@@ -372,6 +374,8 @@ def run_only(args, dev, c):
         ms = timed(lambda: ops.permute_quant(x, idx, c.E), args.steps, args.warmup)
         print(json.dumps({"only": "permute", "ms": ms,
                           "gbs": dispatch_bytes(c.T, c.H, c.E, c.K) / (ms * 1e-3) / 1e9}))
+    elif args.only == "wgrad":
+        print(json.dumps({"only": "wgrad", **bench_wgrad(dev, max(20, args.steps), args.warmup)}))
     elif args.only == "router":
         print(json.dumps({"only": "router", **bench_router(dev, c, args.steps, args.warmup)}))
     elif args.only == "fwdbwd":
@@ -384,6 +388,36 @@ def run_only(args, dev, c):
         print(json.dumps({"only": "blaslt", **bench_blaslt(dev, max(20, args.steps))}))
     else:
         print(json.dumps({"only": "combine", **bench_combine(dev, c, args.steps, args.warmup)}))
+
+
+def bench_wgrad(dev, steps, warmup):
+    """The fc1 weight-gradient GEMM at the config-5 shape (R=131072 routed
+    rows, N=2I=1536, K=H=2048, E=128) with near-uniform loads (the config's
+    router) and with Zipf(1.2) loads over the 128 experts (4 empty): the
+    tile order balances work over the 8 XCDs in both.  Median of per-launch
+    event timings."""
+    import torch
+    from smoe import ops, workloads as W
+    c = W.CONFIGS["qwen3"]
+    R, N, K = c.T * c.K, 2 * c.I, c.H
+    dc1 = W.tokens(R, N, device=dev, seed=21)
+    xs = W.tokens(R, K, device=dev, seed=22)
+    out = {}
+    idx, _ = ops.router_topk(W.logits(c.T, c.E, device=dev), c.K)
+    _, _, cnt_r, _ = ops.route_sort(idx, c.E)
+    for name, counts in (("router", cnt_r.cpu().tolist()),
+                         ("zipf1.2", W.zipf_counts(R=R, E=c.E, zeros=4))):
+        off = W.offsets_from_counts(counts, dev)
+        aq, as_, pad, ld = ops.quant_cols(dc1, off)
+        bq, bs_, _, _ = ops.quant_cols(xs, off)
+        dW = torch.empty((c.E, N, K), dtype=torch.float32, device=dev)
+        ms = timed_median(lambda: ops.grouped_gemm_fp8_wgrad(aq, as_, bq, bs_, pad, ld, out=dW),
+                          steps, warmup)
+        out[name] = {"ms": round(ms, 4), "tflops": round(2.0 * R * N * K / (ms * 1e-3) / 1e12, 1),
+                     "max_expert_share": round(max(counts) / R, 3)}
+        del aq, bq, dW
+    torch.cuda.empty_cache()
+    return out
 
 
 def bench_router(dev, c, steps, warmup):
@@ -413,7 +447,7 @@ def main():
     ap.add_argument("--skip-extra", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--only", choices=["permute", "gemm", "combine", "copy", "fwdbwd", "ceiling",
-                                       "blaslt", "router"],
+                                       "blaslt", "router", "wgrad"],
                     help="run one kernel family only (for rocprofv3 runs) and print its timing")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -469,7 +503,7 @@ def main():
     pk_bytes = permute_kernel_bytes(c.T, c.H, c.K)
     pk_gbs = pk_bytes / (pk_ms * 1e-3) / 1e9
     log(f"permute_quant kernel {pk_ms:.4f} ms  {pk_gbs:.1f} GB/s (median, flushed)")
-    roof = {"kernel": "smoe::permute_quant_kernel<4, true>", "bound": "hbm", "achieved": round(pk_gbs, 1),
+    roof = {"kernel": "smoe::permute_quant_row_kernel<7, false>", "bound": "hbm", "achieved": round(pk_gbs, 1),
             "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(pk_gbs / HBM_PEAK_GBS, 4),
             "traffic": PERMUTE_TRAFFIC_BYTES, "kernel_ms": round(pk_ms, 4),
             "bytes_per_launch": pk_bytes,
@@ -490,6 +524,8 @@ def main():
         log("combine", extra["combine_cfg2"])
         extra["layer_mixtral"] = bench_layer(dev, 10, 3)
         log("layer", extra["layer_mixtral"])
+        extra["wgrad_cfg5_fc1"] = bench_wgrad(dev, sx, 3)
+        log("wgrad", extra["wgrad_cfg5_fc1"])
         extra["layer_qwen3_fwd_bwd"] = bench_fwd_bwd(dev, 10, 3)
         log("fwd+bwd", extra["layer_qwen3_fwd_bwd"])
 

@@ -375,15 +375,17 @@ int smoe_unpermute_combine_bwd_quant(const uint16_t* dout, const uint16_t* y,
                                      float* dyTs, int32_t* pad, float* dw, void* stream);
 
 /*
- * Measurement utility (no counterpart in the reference): reads n_in bytes
- * of src once and writes each 16-byte piece to `fanout` places of dst
- * (fanout * n_in bytes, the copies n_in bytes apart) with 128-bit loads and
- * non-temporal 128-bit stores; fanout = 0 only reads.  It reproduces the
- * read:write mix of the dispatch step (1:K) without the quantisation, so
- * its rate is the HBM ceiling for that mix.  sink: one device word.
+ * Measurement utility (no counterpart in the reference): the access pattern
+ * of smoe_permute_quant without its arithmetic.  One wave per source row of
+ * row_bytes bytes (a multiple of 2048) reads it with 128-bit loads and
+ * writes half as many bytes, derived from it, to each of `fanout`
+ * destination rows (scattered) with non-temporal 128-bit stores; fanout = 0
+ * only reads.  fanout = 8 moves the dispatch step's 1:4 read:write byte mix,
+ * so its rate is the HBM ceiling for that mix.  dst must hold
+ * rows * fanout * row_bytes / 2 bytes; sink: one device word.
  */
-int smoe_bw_probe(const void* src, size_t n_in, int fanout, void* dst, size_t dst_bytes,
-                  void* sink, void* stream);
+int smoe_bw_probe(const void* src, int rows, int row_bytes, int fanout, void* dst,
+                  size_t dst_bytes, void* sink, void* stream);
 
 #ifdef __cplusplus
 }

@@ -120,10 +120,11 @@ __device__ __forceinline__ float expf32(float x) {
   const float kLog2e = 1.4426950408889634f;
   const float kLn2Hi = __uint_as_float(0x3f317200u);
   const float kLn2Lo = __uint_as_float(0x35bfbe8eu);
-  if (x > 88.0f) return __builtin_inff();
-  if (x < -87.0f) return 0.0f;
-  float n = __builtin_rintf(x * kLog2e);
-  float r = x - n * kLn2Hi;
+  // evaluated unconditionally and selected at the end (no branches: the
+  // range tests would otherwise split the wave's control flow per call)
+  const float xc = fminf(fmaxf(x, -88.0f), 89.0f);  // keeps n in int range; result replaced below
+  float n = __builtin_rintf(xc * kLog2e);
+  float r = xc - n * kLn2Hi;
   r = r - n * kLn2Lo;
   float p = (float)(1.0 / 5040.0);
   p = p * r + (float)(1.0 / 720.0);
@@ -134,7 +135,10 @@ __device__ __forceinline__ float expf32(float x) {
   p = p * r + 1.0f;
   p = p * r + 1.0f;
   float two_n = __uint_as_float((uint32_t)((int)n + 127) << 23);
-  return p * two_n;
+  float y = p * two_n;
+  y = x > 88.0f ? __builtin_inff() : y;
+  y = x < -87.0f ? 0.0f : y;
+  return x != x ? x : y;  // NaN in, NaN out (the range tests are false for NaN)
 }
 
 __device__ __forceinline__ float silu32(float g) { return g / (1.0f + expf32(-g)); }

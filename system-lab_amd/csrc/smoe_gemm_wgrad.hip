@@ -36,23 +36,19 @@ constexpr int kWSC = (kWN + kWK) * kWChunk * 4;  // 16 KiB per chunk
 constexpr int kWSmem = 2 * kWStage + 2 * kWSC;
 static_assert(kWSmem <= 160 * 1024, "LDS budget");
 
-__global__ __launch_bounds__(kWThreads, 1) void grouped_gemm_fp8_wgrad_kernel(
-    const uint8_t* __restrict__ aT, const float* __restrict__ aTs, const uint8_t* __restrict__ bT,
-    const float* __restrict__ bTs, const int32_t* __restrict__ pad, int E, int N, int Kd, int ld,
-    float* __restrict__ dW) {
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[kWSmem];
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  // XCD-aware tile order: workgroups are dealt to the 8 XCDs round robin, so
-  // XCD x runs experts x, x+8, ... and all NT x KT tiles of one expert before
-  // the next.  An XCD's L2 then serves each aT and bT block to every tile of
-  // the expert that reads it (about 14 distinct 32 KiB slices per K step for
-  // its 32 CUs at config 5, against 37 when the k-tile was the fastest index).
-  const int KT = (Kd + kWK - 1) / kWK, NT = (N + kWN - 1) / kWN;
-  const int xcd = blockIdx.x & 7, tslot = blockIdx.x >> 3;
-  const int e = (tslot / (NT * KT)) * 8 + xcd;
-  if (e >= E) return;  // the whole workgroup leaves together
-  const int rem = tslot % (NT * KT);
-  const int n0 = (rem / KT) * kWN, k0 = (rem % KT) * kWK;
+// One 256 x 256 tile of expert e's weight gradient at (n0, k0).
+__device__ __forceinline__ void wgrad_tile(const uint8_t* __restrict__ aT,
+                                           const float* __restrict__ aTs,
+                                           const uint8_t* __restrict__ bT,
+                                           const float* __restrict__ bTs,
+                                           const int32_t* __restrict__ pad, int N, int Kd, int ld,
+                                           int e, int n0, int k0, uint8_t* smem,
+                                           float* __restrict__ dW) {
+  // opaque per tile: keeps lane-dependent address arithmetic inside the
+  // caller's tile loop instead of live (in VGPRs) across it
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  const int lane = tid & 63, wid = tid >> 6;
   // operand columns outside [0, ld) are never read, whatever pad[] holds
   const int g0 = max(pad[e], 0), g1 = min(pad[e + 1], ld);
   const int steps = g1 > g0 ? (g1 - g0) / kGroup : 0;
@@ -61,14 +57,13 @@ __global__ __launch_bounds__(kWThreads, 1) void grouped_gemm_fp8_wgrad_kernel(
 
   // DMA per wave and stage: aT segments w*4..w*4+3, bT segments w*4..w*4+3
   // (8 rows of 128 bytes each).
-  uint32_t oa[4], ob[4];
-  const int slot = lane & 7;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  // Lane offsets of segment j: row tile_row((wid*4+j)*8 + lane/8) clamped to
+  // the operand's rows, chunk (lane%8) ^ (row%8).  Recomputed at each issue
+  // (a few VALU operations) rather than held: the tile body needs the VGPRs.
+  auto seg_off = [&](int j, int lim) {
     const int row = tile_row((wid * 4 + j) * 8 + (lane >> 3));
-    oa[j] = (uint32_t)(min(row, nrows - 1) * ld + ((slot ^ (row & 7)) << 4));
-    ob[j] = (uint32_t)(min(row, krows - 1) * ld + ((slot ^ (row & 7)) << 4));
-  }
+    return (uint32_t)(min(row, lim - 1) * ld + (((lane & 7) ^ (row & 7)) << 4));
+  };
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_ptr_t)smem;
   // wave-uniform LDS destinations, computed once into scalar registers
   const uint32_t a_lds = __builtin_amdgcn_readfirstlane(lds0 + wid * 4 * 1024);
@@ -79,9 +74,9 @@ __global__ __launch_bounds__(kWThreads, 1) void grouped_gemm_fp8_wgrad_kernel(
     const uint8_t* ab = aT + (size_t)n0 * ld + r0;
     const uint8_t* bb = bT + (size_t)k0 * ld + r0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) dma16(ab, oa[j], a_lds + st + j * 1024);
+    for (int j = 0; j < 4; ++j) dma16(ab, seg_off(j, nrows), a_lds + st + j * 1024);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) dma16(bb, ob[j], b_lds + st + j * 1024);
+    for (int j = 0; j < 4; ++j) dma16(bb, seg_off(j, krows), b_lds + st + j * 1024);
   };
   // Scale chunk c (row groups g0/128 + 8c .. +8): waves 0-3 take aT rows
   // (wid&3)*64 .., waves 4-7 bT rows; instruction i moves 8 rows x 8
@@ -205,6 +200,94 @@ __global__ __launch_bounds__(kWThreads, 1) void grouped_gemm_fp8_wgrad_kernel(
   }
 }
 
+// Fixed cost of a tile in row-group steps (zeroing or writing its 256 KiB
+// fp32 output and the prologue), so that empty experts' tiles count too.
+constexpr int kTileFixed = 4;
+
+__global__ __launch_bounds__(kWThreads, 1) void grouped_gemm_fp8_wgrad_kernel(
+    const uint8_t* __restrict__ aT, const float* __restrict__ aTs, const uint8_t* __restrict__ bT,
+    const float* __restrict__ bTs, const int32_t* __restrict__ pad, int E, int N, int Kd, int ld,
+    int per_xcd, float* __restrict__ dW) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kWSmem];
+  // the cost prefix lives in the stage buffers until the tile range is known
+  long long* cpre = (long long*)smem;
+  long long* wsum = cpre + SMOE_MAX_EXPERTS + 1;
+  static_assert((SMOE_MAX_EXPERTS + 1 + kWThreads / kWave) * 8 <= kWSmem, "cost table fits");
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  // Work-balanced, XCD-aware tile order.  Tiles are numbered expert-major
+  // (expert e owns tiles e*NT*KT .. +NT*KT, n-tile major, k-tile minor); a
+  // tile of expert e costs steps(e) + kTileFixed.  The tile sequence is cut
+  // into 8 contiguous ranges of equal total cost, and XCD x (workgroups are
+  // dealt to the 8 XCDs round robin) runs range x in order, block j taking
+  // tiles T_x + j, T_x + j + per_xcd, ...  An expert's tiles therefore stay
+  // together on one XCD (its L2 serves each aT and bT slice to every tile
+  // of the expert that reads it), and a hot expert's tiles are split over
+  // as many XCDs as its share of the work needs.
+  const int KT = (Kd + kWK - 1) / kWK, NT = (N + kWN - 1) / kWN;
+  const int TE = NT * KT;  // tiles per expert
+  {
+    // cpre[e] = cost of all tiles of experts before e (64-bit: E * TE * steps)
+    const int per = (E + kWThreads - 1) / kWThreads;
+    long long loc[2], run = 0;
+    for (int i = 0; i < per; ++i) {
+      const int e = tid * per + i;
+      long long c = 0;
+      if (e < E) {
+        const int a0 = max(pad[e], 0), a1 = min(pad[e + 1], ld);
+        c = (long long)TE * ((a1 > a0 ? (a1 - a0) / kGroup : 0) + kTileFixed);
+      }
+      run += c;
+      loc[i] = run;
+    }
+    long long incl = run;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const long long v = __shfl_up(incl, o, kWave);
+      if (lane >= o) incl += v;
+    }
+    if (lane == kWave - 1) wsum[wid] = incl;
+    __syncthreads();
+    long long base = 0;
+    for (int w = 0; w < wid; ++w) base += wsum[w];
+    const long long excl = base + incl - run;
+    for (int i = 0; i < per; ++i) {
+      const int e = tid * per + i;
+      if (e < E) cpre[e + 1] = excl + loc[i];
+    }
+    if (tid == 0) cpre[0] = 0;
+    __syncthreads();
+  }
+  // first tile whose cost interval starts at or after cost c
+  auto first_tile = [&](long long c) -> long long {
+    int lo = 0, hi = E;  // largest e with cpre[e] <= c
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (cpre[mid] <= c) lo = mid;
+      else hi = mid;
+    }
+    const long long per_tile = (cpre[lo + 1] - cpre[lo]) / TE;
+    const long long r = (c - cpre[lo] + per_tile - 1) / per_tile;
+    return (long long)lo * TE + min(r, (long long)TE);
+  };
+  const long long W = cpre[E];
+  const int xcd = blockIdx.x & 7, j = blockIdx.x >> 3;
+  // XCD x's range [T_x, T_x+1) starts at the tile where its cost share
+  // starts; every workgroup computes it the same way.  Workgroup j of the
+  // XCD takes tiles T_x + j, T_x + j + per_xcd, ... (a range with more
+  // tiles than workgroups, i.e. cheap tiles, loops).  Scalar registers keep
+  // the loop off the tile body's VGPRs.
+  const int t_begin = __builtin_amdgcn_readfirstlane(xcd == 0 ? 0 : (int)first_tile(W * xcd / 8));
+  const int t_end =
+      __builtin_amdgcn_readfirstlane(xcd == 7 ? E * TE : (int)first_tile(W * (xcd + 1) / 8));
+  __syncthreads();  // the tiles' DMA overwrites the cost table
+  for (int t = t_begin + j; t < t_end; t += per_xcd) {
+    const int e = t / TE;
+    const int rem = t - e * TE;
+    wgrad_tile(aT, aTs, bT, bTs, pad, N, Kd, ld, e, (rem / KT) * kWN, (rem % KT) * kWK, smem, dW);
+    __syncthreads();  // the next tile reuses the LDS
+  }
+}
+
 }  // namespace smoe
 
 using namespace smoe;
@@ -222,11 +305,13 @@ extern "C" int smoe_grouped_gemm_fp8_wgrad(const uint8_t* aT, const float* aTs,
   SMOE_CHECK_PTR(dW);
   if (!aTs || !bTs || !pad) return SMOE_EINVAL_NULL;
   if (((uintptr_t)aTs | (uintptr_t)bTs | (uintptr_t)pad) & 3u) return SMOE_EINVAL_PTRALIGN;
-  // experts padded to a multiple of 8 (one per XCD in each round)
-  const long long nblk =
-      (long long)(E + 7) / 8 * 8 * ((Kdim + kWK - 1) / kWK) * ((N + kWN - 1) / kWN);
-  if (nblk > 0x7fffffffLL) return SMOE_EINVAL_DIM;
-  grouped_gemm_fp8_wgrad_kernel<<<dim3((unsigned)nblk), dim3(kWThreads), 0, (hipStream_t)stream>>>(
-      aT, aTs, bT, bTs, pad, E, N, Kdim, ld, dW);
+  // per_xcd workgroups per XCD, one tile each on average; a range with
+  // more tiles (cheap tiles) loops
+  const long long tiles = (long long)E * ((Kdim + kWK - 1) / kWK) * ((N + kWN - 1) / kWN);
+  const long long per_xcd = (tiles + 7) / 8;
+  if (per_xcd * 8 > 0x7fffffffLL) return SMOE_EINVAL_DIM;
+  grouped_gemm_fp8_wgrad_kernel<<<dim3((unsigned)(per_xcd * 8)), dim3(kWThreads), 0,
+                                  (hipStream_t)stream>>>(aT, aTs, bT, bTs, pad, E, N, Kdim, ld,
+                                                         (int)per_xcd, dW);
   SMOE_RETURN_LAUNCH();
 }

@@ -32,20 +32,35 @@ namespace smoe {
 constexpr int kSeg = 512;  // pairs per segment (one wave)
 
 // ------------------------------------------------------------------ router
-// One butterfly level of the arg-max: the partner at distance kO wins with a
+// A lane of the same 16-lane row for order-free reductions (max, arg-max):
+// levels 1 and 2 are quad permutes, 4 and 8 the row's half mirror (lane
+// i <-> 7-i of each 8) and full mirror (i <-> 15-i), all DPP moves with no
+// LDS round trip; after the four levels every lane of the row holds the
+// row's result.  Levels 16 and 32 (64-lane groups) are lane swaps.
+template <int kO>
+__device__ __forceinline__ int red_lanes(int v) {
+  if constexpr (kO == 4) return __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);
+  else if constexpr (kO == 8) return __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false);
+  else return xor_lanes<kO>(v);
+}
+template <int kO>
+__device__ __forceinline__ float red_lanes(float v) {
+  return __int_as_float(red_lanes<kO>(__float_as_int(v)));
+}
+
+// One level of the arg-max reduction: the partner lane (red_lanes) wins with a
 // larger score, or an equal score and a lower id (0x7fffffff marks a lane
 // with no candidate).
 template <int kO>
 __device__ __forceinline__ void argmax_step(float& bs, int& bi, float& bp) {
-  const float os = xor_lanes<kO>(bs);
-  const int oi = xor_lanes<kO>(bi);
-  const float op = xor_lanes<kO>(bp);
-  const bool take = (oi != 0x7fffffff) && (bi == 0x7fffffff || os > bs || (os == bs && oi < bi));
-  if (take) {
-    bs = os;
-    bi = oi;
-    bp = op;
-  }
+  const float os = red_lanes<kO>(bs);
+  const int oi = red_lanes<kO>(bi);
+  const float op = red_lanes<kO>(bp);
+  // bitwise, not short-circuit, operators: no branches
+  const bool take = (oi != 0x7fffffff) & ((bi == 0x7fffffff) | (os > bs) | ((os == bs) & (oi < bi)));
+  bs = take ? os : bs;
+  bi = take ? oi : bi;
+  bp = take ? op : bp;
 }
 
 // Butterfly over the kLPT lanes of a token group, top level first.
@@ -86,56 +101,114 @@ __device__ __forceinline__ TokenRoute<kLPT, kNV> route_token(const float* __rest
   float p[kNV];
   uint32_t ok = 0;  // bit q: expert i + kLPT*q is valid and not yet picked
   float m = -__builtin_inff();
+  // every load is unconditional (experts past E re-read expert E-1 and are
+  // masked afterwards): a load under a branch would get a vmcnt(0) wait at
+  // the branch join, one HBM round trip per load
+  float sc[kNV];  // the selection bias, then the selection scores
+#pragma unroll
+  for (int q = 0; q < kNV; ++q) p[q] = row[min(i + kLPT * q, E - 1)];
+  if (bias) {
+#pragma unroll
+    for (int q = 0; q < kNV; ++q) sc[q] = bias[min(i + kLPT * q, E - 1)];
+  }
 #pragma unroll
   for (int q = 0; q < kNV; ++q) {
     const int e = i + kLPT * q;
-    p[q] = e < E ? row[e] : -__builtin_inff();
     if (e < E) ok |= 1u << q;
+    else p[q] = -__builtin_inff();
     m = fmaxf(m, p[q]);
   }
-  group_levels<kLPT>([&](auto o) { m = fmaxf(m, xor_lanes<decltype(o)::value>(m)); });
+  group_levels<kLPT>([&](auto o) { m = fmaxf(m, red_lanes<decltype(o)::value>(m)); });
   float vs[kVirt];
 #pragma unroll
   for (int a = 0; a < kVirt; ++a) vs[a] = 0.0f;
 #pragma unroll
   for (int q = 0; q < kNV; ++q) {
-    p[q] = (ok >> q) & 1u ? expf32(p[q] - m) : 0.0f;
+    p[q] = expf32(p[q] - m);  // experts past E hold -inf: exp gives exactly 0
     vs[q % kVirt] = vs[q % kVirt] + p[q];
   }
   float den;
   if constexpr (kVirt == 4) den = (vs[0] + vs[2]) + (vs[1] + vs[3]);  // distances 32, 16
   else den = vs[0];
+  // the sum keeps the xor partners: its rounding is part of the contract
   group_levels<kLPT>([&](auto o) { den = den + xor_lanes<decltype(o)::value>(den); });
-  float sc[kNV];
 #pragma unroll
   for (int q = 0; q < kNV; ++q) {
     p[q] = p[q] / den;
-    sc[q] = bias ? p[q] + ((ok >> q) & 1u ? bias[i + kLPT * q] : 0.0f) : p[q];
+    sc[q] = bias ? p[q] + ((ok >> q) & 1u ? sc[q] : 0.0f) : p[q];
   }
   TokenRoute<kLPT, kNV> r;
   r.id[0] = r.id[1] = 0;
-  r.w[0] = r.w[1] = 0.0f;
-  float psum = 0.0f;
-  for (int k = 0; k < K; ++k) {
-    float bs = -__builtin_inff();
-    int bi = 0x7fffffff;
-    float bp = 0.0f;
+  r.w[0] = 0.0f;
+  r.w[1] = 0.0f;
+  // Each lane offers its best expert not yet picked; the group's arg-max
+  // picks one per round.  A lane keeps its two best remaining experts (slot
+  // 0 before slot 1) and rescans only when both are gone: the experts a lane
+  // gave up are exactly its best ones in the order (score desc, id asc), so
+  // the rest are those after the last one it gave up (ls, li).
+  constexpr int kNone = 0x7fffffff;
+  float s0 = 0.0f, s1 = 0.0f, p0 = 0.0f, p1 = 0.0f;
+  int i0 = kNone, i1 = kNone;
+  float ls = 0.0f;
+  int li = -1;  // -1: nothing given up yet
+  bool more = true;  // experts beyond the two slots may remain
+  // Experts past E hold score -inf and an id >= E, so they lose every
+  // comparison against a real expert (on equal scores the lower id wins):
+  // with K <= E they are never picked and need no separate mask.
+#pragma unroll
+  for (int q = 0; q < kNV; ++q)
+    if (!((ok >> q) & 1u)) sc[q] = -__builtin_inff();
+  auto top2 = [&](auto refill) {
+    i0 = i1 = kNone;
 #pragma unroll
     for (int q = 0; q < kNV; ++q) {
-      if (((ok >> q) & 1u) && (sc[q] > bs || bi == 0x7fffffff)) {
-        bs = sc[q];
-        bi = i + kLPT * q;
-        bp = p[q];
+      const int id = i + kLPT * q;
+      // ids ascend with q: a strict > keeps the lower id ahead on equal
+      // scores (bitwise operators: no branches)
+      bool c0 = (i0 == kNone) | (sc[q] > s0);
+      bool c1 = (i1 == kNone) | (sc[q] > s1);
+      if constexpr (decltype(refill)::value) {
+        const bool elig = (sc[q] < ls) | ((sc[q] == ls) & (id > li));
+        c0 = c0 & elig;
+        c1 = c1 & elig;
       }
+      c1 = c1 & !c0;
+      s1 = c0 ? s0 : (c1 ? sc[q] : s1);
+      i1 = c0 ? i0 : (c1 ? id : i1);
+      p1 = c0 ? p0 : (c1 ? p[q] : p1);
+      s0 = c0 ? sc[q] : s0;
+      i0 = c0 ? id : i0;
+      p0 = c0 ? p[q] : p0;
     }
+    more = i1 != kNone;
+  };
+  top2(std::false_type{});
+  float psum = 0.0f;
+  for (int k = 0; k < K; ++k) {
+    float bs = s0, bp = p0;
+    int bi = i0;
     group_levels<kLPT>([&](auto o) { argmax_step<decltype(o)::value>(bs, bi, bp); });
-#pragma unroll
-    for (int q = 0; q < kNV; ++q)
-      if (i + kLPT * q == bi) ok &= ~(1u << q);
+    if (bi == i0) {  // this lane gave the winner: advance its slots
+      ls = s0;
+      li = i0;
+      s0 = s1;
+      i0 = i1;
+      p0 = p1;
+      i1 = kNone;
+    }
+    const bool refill = i0 == kNone && more;
+    if (__builtin_amdgcn_ballot_w64(refill)) {
+      if (refill) top2(std::true_type{});
+    }
     psum = psum + bp;
-    if ((k & (kLPT - 1)) == i) {
-      r.id[k / kLPT] = bi;
-      r.w[k / kLPT] = bp;
+    if ((k & (kLPT - 1)) == i) {  // static slot indices keep r in registers
+      if (kLPT == 64 || k < kLPT) {
+        r.id[0] = bi;
+        r.w[0] = bp;
+      } else {
+        r.id[1] = bi;
+        r.w[1] = bp;
+      }
     }
   }
   r.w[0] = r.w[0] / psum;
@@ -183,9 +256,10 @@ __global__ __launch_bounds__(256) void router_topk_bwd_kernel(
   float p[kNV];
   float m = -__builtin_inff();
 #pragma unroll
+  for (int q = 0; q < kNV; ++q) p[q] = row[min(i + kLPT * q, E - 1)];  // unconditional loads
+#pragma unroll
   for (int q = 0; q < kNV; ++q) {
-    const int e = i + kLPT * q;
-    p[q] = e < E ? row[e] : -__builtin_inff();
+    if (i + kLPT * q >= E) p[q] = -__builtin_inff();
     m = fmaxf(m, p[q]);
   }
   group_levels<kLPT>([&](auto o) { m = fmaxf(m, xor_lanes<decltype(o)::value>(m)); });
@@ -194,7 +268,7 @@ __global__ __launch_bounds__(256) void router_topk_bwd_kernel(
   for (int a = 0; a < kVirt; ++a) vs[a] = 0.0f;
 #pragma unroll
   for (int q = 0; q < kNV; ++q) {
-    p[q] = i + kLPT * q < E ? expf32(p[q] - m) : 0.0f;
+    p[q] = expf32(p[q] - m);  // experts past E hold -inf: exp gives exactly 0
     vs[q % kVirt] = vs[q % kVirt] + p[q];
   }
   float den;
@@ -237,25 +311,28 @@ __global__ __launch_bounds__(256) void router_topk_bwd_kernel(
 }
 
 // Router fused with the sort's first pass: workgroup s routes every token
-// that has a pair in segment s (pairs s*kSeg .. +kSeg; a token whose pairs
+// that has a pair in segment s (pairs s*kSegR .. +kSegR; a token whose pairs
 // straddle two segments is routed by both workgroups, and each writes only
 // its own pairs), counts the segment's picks per expert in LDS and writes
 // the histogram column hist[e][s] that route_rowscan and route_rank consume.
-constexpr int kSegR = 512;  // pairs per segment; equals kSeg below
+// A segment of 128 pairs is 16 tokens at top-8, one pass of a 256-thread
+// workgroup: as many workgroups as the plain router launches.
+constexpr int kSegR = 128;  // pairs per segment of the fused path
+constexpr int kHistThreads = 256;
 template <int kLPT, int kNV>
-__global__ __launch_bounds__(1024) void router_hist_kernel(
+__global__ __launch_bounds__(kHistThreads) void router_hist_kernel(
     const float* __restrict__ logits, const float* __restrict__ bias, int T, int E, int K,
     int nseg, int32_t* __restrict__ topk_idx, float* __restrict__ topk_w,
     int32_t* __restrict__ hist) {
   extern __shared__ int32_t hh[];  // [E]
   const int seg = blockIdx.x;
   const int R = T * K;
-  for (int e = threadIdx.x; e < E; e += 1024) hh[e] = 0;
+  for (int e = threadIdx.x; e < E; e += kHistThreads) hh[e] = 0;
   __syncthreads();
   const int p0 = seg * kSegR, p1 = min(R, p0 + kSegR);
   const int t0 = p0 / K, t1 = (p1 - 1) / K;  // tokens with a pair in [p0, p1)
   const int i = threadIdx.x & (kLPT - 1);
-  for (int t = t0 + threadIdx.x / kLPT; t <= t1; t += 1024 / kLPT) {
+  for (int t = t0 + threadIdx.x / kLPT; t <= t1; t += kHistThreads / kLPT) {
     const TokenRoute<kLPT, kNV> r = route_token<kLPT, kNV>(logits + (size_t)t * E, bias, E, K, i);
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
@@ -269,7 +346,7 @@ __global__ __launch_bounds__(1024) void router_hist_kernel(
     }
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < E; e += 1024) hist[(size_t)e * nseg + seg] = hh[e];
+  for (int e = threadIdx.x; e < E; e += kHistThreads) hist[(size_t)e * nseg + seg] = hh[e];
 }
 
 // ------------------------------------------------------------------- sort
@@ -308,24 +385,43 @@ __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
   return v;
 }
 
+// One wave per expert scans its histogram row: each lane takes 16
+// consecutive entries per pass of 1024 (one wave-wide scan per pass instead
+// of one per 64 entries).  Loads are unconditional (indices clamped to the
+// row) so that they are all in flight before the first use.
 __global__ __launch_bounds__(256) void route_rowscan_kernel(int32_t* __restrict__ hist, int E,
                                                             int nseg,
                                                             int32_t* __restrict__ counts) {
+  constexpr int kPer = 16;
   const int lane = threadIdx.x & 63;
   const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (e >= E) return;
   int32_t* row = hist + (size_t)e * nseg;
   int carry = 0;
-  for (int s0 = 0; s0 < nseg; s0 += kWave) {
-    const int s = s0 + lane;
-    const int v = s < nseg ? row[s] : 0;
-    const int inc = wave_incl_scan(v, lane);
-    if (s < nseg) row[s] = carry + inc - v;
+  for (int s0 = 0; s0 < nseg; s0 += kWave * kPer) {
+    const int b = s0 + lane * kPer;
+    int v[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) v[i] = row[min(b + i, nseg - 1)];
+    int tot = 0;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      v[i] = b + i < nseg ? v[i] : 0;
+      tot += v[i];
+    }
+    const int inc = wave_incl_scan(tot, lane);
+    int run = carry + inc - tot;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      if (b + i < nseg) row[b + i] = run;
+      run += v[i];
+    }
     carry += __shfl(inc, kWave - 1, kWave);
   }
   if (lane == 0) counts[e] = carry;
 }
 
+template <int kSegT>
 __global__ __launch_bounds__(256) void route_rank_kernel(const int32_t* __restrict__ idx,
                                                          const int32_t* __restrict__ rowpre,
                                                          const int32_t* __restrict__ counts,
@@ -369,10 +465,11 @@ __global__ __launch_bounds__(256) void route_rank_kernel(const int32_t* __restri
 
   const int seg = blockIdx.x * 4 + w;
   if (seg >= nseg) return;
-  const int p0 = seg * kSeg;
-  int v[kPerLane];
+  constexpr int kPL = kSegT / kWave;
+  const int p0 = seg * kSegT;
+  int v[kPL];
 #pragma unroll
-  for (int i = 0; i < kPerLane; ++i) {
+  for (int i = 0; i < kPL; ++i) {
     const int p = p0 + i * kWave + lane;
     v[i] = p < R ? idx[p] : E;  // E is a sentinel id no valid lane has
   }
@@ -380,7 +477,7 @@ __global__ __launch_bounds__(256) void route_rank_kernel(const int32_t* __restri
   __builtin_amdgcn_wave_barrier();
   const uint64_t lt = (1ull << lane) - 1ull;
 #pragma unroll
-  for (int i = 0; i < kPerLane; ++i) {
+  for (int i = 0; i < kPL; ++i) {
     const int p = p0 + i * kWave + lane;
     const bool valid = (unsigned)v[i] < (unsigned)E;
     const int e = valid ? v[i] : E;  // out-of-range ids rank as the sentinel
@@ -404,7 +501,7 @@ __global__ __launch_bounds__(256) void route_rank_kernel(const int32_t* __restri
   }
 }
 
-static inline int seg_count(int R) { return (R + kSeg - 1) / kSeg; }
+static inline int seg_count(int R, int seg = kSeg) { return (R + seg - 1) / seg; }
 
 }  // namespace smoe
 
@@ -470,15 +567,20 @@ extern "C" int smoe_router_topk_bwd(const float* logits, const int32_t* topk_idx
 // the per-segment histogram hist[E][nseg].
 constexpr size_t kStatusBytes = 16;
 
+static size_t sort_ws_bytes(int T, int K, int E, int seg) {
+  return kStatusBytes + (size_t)E * seg_count(T * K, seg) * sizeof(int32_t);
+}
+
 extern "C" size_t smoe_route_sort_workspace_size(int T, int K, int E) {
-  if (T <= 0 || K <= 0 || E <= 0) return 0;
-  const size_t R = (size_t)T * K;
-  return kStatusBytes + (size_t)E * seg_count((int)R) * sizeof(int32_t);
+  if (T <= 0 || K <= 0 || E <= 0 || (long long)T * K > 0x7fffffffLL) return 0;
+  // enough for both sorts: the fused router's 128-pair segments need the
+  // larger histogram
+  return sort_ws_bytes(T, K, E, kSegR);
 }
 
 static int check_sort_args(int T, int K, int E, const int32_t* row_map, const int32_t* inv_map,
                            const int32_t* counts, const int32_t* offsets, const void* ws,
-                           size_t ws_bytes) {
+                           size_t ws_bytes, int seg) {
   if (T <= 0) return SMOE_EINVAL_DIM;
   if (E <= 0 || E > SMOE_MAX_EXPERTS) return SMOE_EINVAL_EXPERTS;
   if (K <= 0 || K > E || K > 32) return SMOE_EINVAL_TOPK;
@@ -487,11 +589,13 @@ static int check_sort_args(int T, int K, int E, const int32_t* row_map, const in
   if (((uintptr_t)row_map | (uintptr_t)inv_map | (uintptr_t)counts | (uintptr_t)offsets) & 3u)
     return SMOE_EINVAL_PTRALIGN;
   if (!ws || ((uintptr_t)ws & 15u)) return ws ? SMOE_EINVAL_PTRALIGN : SMOE_EINVAL_WORKSPACE;
-  if (ws_bytes < smoe_route_sort_workspace_size(T, K, E)) return SMOE_EINVAL_WORKSPACE;
+  if (ws_bytes < sort_ws_bytes(T, K, E, seg)) return SMOE_EINVAL_WORKSPACE;
   return SMOE_OK;
 }
 
-// Passes 2 and 3 of the sort, from a filled histogram.
+// Passes 2 and 3 of the sort, from a filled histogram of nseg segments of
+// kSegT pairs.
+template <int kSegT>
 static void sort_tail(const int32_t* topk_idx, int R, int E, int nseg, int32_t* row_map,
                       int32_t* inv_map, int32_t* counts, int32_t* offsets, void* ws,
                       hipStream_t s) {
@@ -500,14 +604,14 @@ static void sort_tail(const int32_t* topk_idx, int R, int E, int nseg, int32_t* 
   int32_t* status = (int32_t*)ws;
   int32_t* hist = (int32_t*)((char*)ws + kStatusBytes);
   route_rowscan_kernel<<<dim3((E + 3) / 4), dim3(256), 0, s>>>(hist, E, nseg, counts);
-  route_rank_kernel<<<dim3((nseg + 3) / 4), dim3(256), (size_t)5 * E * sizeof(int32_t), s>>>(
+  route_rank_kernel<kSegT><<<dim3((nseg + 3) / 4), dim3(256), (size_t)5 * E * sizeof(int32_t), s>>>(
       topk_idx, hist, counts, R, E, nseg, nbits, offsets, row_map, inv_map, status);
 }
 
 extern "C" int smoe_route_sort(const int32_t* topk_idx, int T, int K, int E, int32_t* row_map,
                                int32_t* inv_map, int32_t* counts, int32_t* offsets, void* ws,
                                size_t ws_bytes, void* stream) {
-  int st = check_sort_args(T, K, E, row_map, inv_map, counts, offsets, ws, ws_bytes);
+  int st = check_sort_args(T, K, E, row_map, inv_map, counts, offsets, ws, ws_bytes, kSeg);
   if (st) return st;
   if (!topk_idx) return SMOE_EINVAL_NULL;
   if ((uintptr_t)topk_idx & 3u) return SMOE_EINVAL_PTRALIGN;
@@ -517,7 +621,7 @@ extern "C" int smoe_route_sort(const int32_t* topk_idx, int T, int K, int E, int
   hipStream_t s = (hipStream_t)stream;
   route_hist_kernel<<<dim3((nseg + 3) / 4), dim3(256), (size_t)4 * E * sizeof(int32_t), s>>>(
       topk_idx, R, E, nseg, hist);
-  sort_tail(topk_idx, R, E, nseg, row_map, inv_map, counts, offsets, ws, s);
+  sort_tail<kSeg>(topk_idx, R, E, nseg, row_map, inv_map, counts, offsets, ws, s);
   SMOE_RETURN_LAUNCH();
 }
 
@@ -527,19 +631,18 @@ extern "C" int smoe_route_topk_sort(const float* logits, const float* bias, int 
                                     void* ws, size_t ws_bytes, void* stream) {
   int st = check_router_args(logits, bias, T, E, K, topk_idx, topk_w);
   if (st) return st;
-  st = check_sort_args(T, K, E, row_map, inv_map, counts, offsets, ws, ws_bytes);
+  st = check_sort_args(T, K, E, row_map, inv_map, counts, offsets, ws, ws_bytes, kSegR);
   if (st) return st;
   const int R = T * K;
-  const int nseg = seg_count(R);
+  const int nseg = seg_count(R, kSegR);
   int32_t* hist = (int32_t*)((char*)ws + kStatusBytes);
   hipStream_t s = (hipStream_t)stream;
-  static_assert(kSegR == kSeg, "fused router segments are the sort's segments");
 #define SMOE_RHIST(LPT, NV)                                                                \
-  router_hist_kernel<LPT, NV><<<dim3(nseg), dim3(1024), (size_t)E * sizeof(int32_t), s>>>( \
+  router_hist_kernel<LPT, NV><<<dim3(nseg), dim3(kHistThreads), (size_t)E * sizeof(int32_t), s>>>( \
       logits, bias, T, E, K, nseg, topk_idx, topk_w, hist)
   SMOE_ROUTE_DISPATCH(E, SMOE_RHIST);
 #undef SMOE_RHIST
-  sort_tail(topk_idx, R, E, nseg, row_map, inv_map, counts, offsets, ws, s);
+  sort_tail<kSegR>(topk_idx, R, E, nseg, row_map, inv_map, counts, offsets, ws, s);
   SMOE_RETURN_LAUNCH();
 }
 
@@ -589,7 +692,7 @@ extern "C" int smoe_route_sort_noalloc(const int32_t* topk_idx, int T, int K, in
   if ((long long)T * K > 0x7fffffffLL) return SMOE_EINVAL_DIM;
   // the sort needs E * ceil(T*K / 512) histogram words: reject what the
   // static array cannot hold
-  if (smoe_route_sort_workspace_size(T, K, E) > kScratchBytes) return SMOE_EINVAL_WORKSPACE;
+  if (sort_ws_bytes(T, K, E, kSeg) > kScratchBytes) return SMOE_EINVAL_WORKSPACE;
   hipError_t err = hipSuccess;
   void* ws = scratch_ptr(&err);
   if (!ws) return err == hipSuccess ? SMOE_EINVAL_WORKSPACE : (int)err;
