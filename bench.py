@@ -318,8 +318,8 @@ def bench_ceiling(dev, c, iters=20):
     dst = torch.empty(c.T * 8 * row_bytes // 2, dtype=torch.uint8, device=dev)
     sink = torch.zeros(4, dtype=torch.int32, device=dev)
     flush = Flush()
-    out = {"bytes_in": c.T * row_bytes, "pattern": "permute_quant's (one wave per row, 1 KiB "
-           "scattered non-temporal row writes)"}
+    out = {"bytes_in": c.T * row_bytes, "pattern": "permute_quant's (one wave per row, whole "
+           "row loaded, each scattered destination row written front to back)"}
     for fanout in (0, 2, 4, 8):
         fn = lambda: smoe._C.call("smoe_bw_probe", src.data_ptr(), c.T, row_bytes, fanout,
                                   dst.data_ptr(), dst.numel(), sink.data_ptr(),

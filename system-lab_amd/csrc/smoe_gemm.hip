@@ -289,14 +289,7 @@ __global__ __launch_bounds__(C::kThreads, 1) void grouped_gemm_fp8_kernel(
     // the next scale chunk goes out at the first step of the current one, into
     // the half whose chunk was last read before the previous barrier
     if (kChunkS && (kb & (kSChunk - 1)) == 0 && kb + kSChunk < ksb) issue_sc(kb / kSChunk + 1);
-#ifdef SMOE_GEMM_LATE_ISSUE
-    // experiment: the upper half of the waves issues its stage loads after
-    // row block SMOE_GEMM_LATE_ISSUE instead of at the top of the step
-    const bool late = __builtin_amdgcn_readfirstlane(wid) >= C::kWaves / 2;
-    if (!late && nxt < ksb) issue(nxt, nxt % kStages);
-#else
     if (nxt < ksb) issue(nxt, nxt % kStages);
-#endif
     const uint8_t* sA = smem + buf * kStage;
     const uint8_t* sB = sA + kABytes;
     const float* sS = (const float*)(sB + kBBytes);
@@ -321,9 +314,6 @@ __global__ __launch_bounds__(C::kThreads, 1) void grouped_gemm_fp8_kernel(
         for (int v = 0; v < 4; ++v) acc[i][j][v] = __builtin_fmaf(p[v], sc, acc[i][j][v]);
       }
       fx = fxn;
-#ifdef SMOE_GEMM_LATE_ISSUE
-      if (i == SMOE_GEMM_LATE_ISSUE && late && nxt < ksb) issue(nxt, nxt % kStages);
-#endif
     }
     // stage kb+1 must have landed for every wave; later stages may still fly
     if (kStages > 2 && kb + kStages - 1 < ksb) {

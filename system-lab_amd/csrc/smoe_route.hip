@@ -244,7 +244,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
 // the forward computes it; every lane evaluates the K-term sums itself (the
 // picked probabilities from their logits), so no lane exchange is needed
 // beyond the softmax reductions.
-template <int kLPT, int kNV>
+template <int kLPT, int kNV, int kMaxK>
 __global__ __launch_bounds__(256) void router_topk_bwd_kernel(
     const float* __restrict__ logits, const int32_t* __restrict__ topk_idx,
     const float* __restrict__ dtopk_w, int T, int E, int K, float* __restrict__ dlogits) {
@@ -279,28 +279,37 @@ __global__ __launch_bounds__(256) void router_topk_bwd_kernel(
   for (int q = 0; q < kNV; ++q) p[q] = p[q] / den;
   const int32_t* ids = topk_idx + (size_t)t * K;
   const float* g = dtopk_w + (size_t)t * K;
+  // the picked probabilities, once each.  K <= kMaxK: static indices keep
+  // the arrays in registers, and the loads are unconditional (index clamped
+  // to K-1, the extra terms masked) so that all of them are in flight at once.
+  float pk[kMaxK], gk[kMaxK];
+  int ek[kMaxK];
+#pragma unroll
+  for (int k = 0; k < kMaxK; ++k) {
+    ek[k] = min(max(ids[min(k, K - 1)], 0), E - 1);
+    gk[k] = g[min(k, K - 1)];
+  }
+#pragma unroll
+  for (int k = 0; k < kMaxK; ++k) pk[k] = row[ek[k]];
   float psum = 0.0f;
-  for (int k = 0; k < K; ++k) {
-    const int e = min(max(ids[k], 0), E - 1);
-    psum = psum + expf32(row[e] - m) / den;
+#pragma unroll
+  for (int k = 0; k < kMaxK; ++k) {
+    pk[k] = expf32(pk[k] - m) / den;
+    psum = k < K ? psum + pk[k] : psum;
   }
   float c = 0.0f;
-  for (int k = 0; k < K; ++k) {
-    const int e = min(max(ids[k], 0), E - 1);
-    c = c + g[k] * ((expf32(row[e] - m) / den) / psum);
-  }
+#pragma unroll
+  for (int k = 0; k < kMaxK; ++k) c = k < K ? c + gk[k] * (pk[k] / psum) : c;
   float dot = 0.0f;
   float dp[kNV];
 #pragma unroll
   for (int q = 0; q < kNV; ++q) dp[q] = 0.0f;
-  for (int k = 0; k < K; ++k) {
-    const int e = min(max(ids[k], 0), E - 1);
-    const float pk = expf32(row[e] - m) / den;
-    const float d = (g[k] - c) / psum;
-    dot = dot + pk * d;
 #pragma unroll
-    for (int q = 0; q < kNV; ++q)
-      if (i + kLPT * q == e) dp[q] = d;
+  for (int k = 0; k < kMaxK; ++k) {
+    const float d = (gk[k] - c) / psum;
+    dot = k < K ? dot + pk[k] * d : dot;
+#pragma unroll
+    for (int q = 0; q < kNV; ++q) dp[q] = (k < K && i + kLPT * q == ek[k]) ? d : dp[q];
   }
   float* out = dlogits + (size_t)t * E;
 #pragma unroll
@@ -555,10 +564,17 @@ extern "C" int smoe_router_topk_bwd(const float* logits, const int32_t* topk_idx
   if (((uintptr_t)logits | (uintptr_t)topk_idx | (uintptr_t)dtopk_w | (uintptr_t)dlogits) & 3u)
     return SMOE_EINVAL_PTRALIGN;
   hipStream_t s = (hipStream_t)stream;
-#define SMOE_RBWD(LPT, NV)                                                                \
-  router_topk_bwd_kernel<LPT, NV><<<dim3((T + 256 / LPT - 1) / (256 / LPT)), dim3(256), 0, s>>>( \
+#define SMOE_RBWD_K(LPT, NV, MK)                                                              \
+  router_topk_bwd_kernel<LPT, NV, MK><<<dim3((T + 256 / LPT - 1) / (256 / LPT)), dim3(256), 0, s>>>( \
       logits, topk_idx, dtopk_w, T, E, K, dlogits)
+#define SMOE_RBWD(LPT, NV)                          \
+  do {                                              \
+    if (K <= 2) SMOE_RBWD_K(LPT, NV, 2);            \
+    else if (K <= 8) SMOE_RBWD_K(LPT, NV, 8);       \
+    else SMOE_RBWD_K(LPT, NV, 32);                  \
+  } while (0)
   SMOE_ROUTE_DISPATCH(E, SMOE_RBWD);
+#undef SMOE_RBWD_K
 #undef SMOE_RBWD
   SMOE_RETURN_LAUNCH();
 }
