@@ -85,6 +85,8 @@ def timed_median(fn, iters=20, warmup=5, flush=None):
     """Median ms of ``iters`` single calls, each bracketed by its own HIP
     events on the current stream; with ``flush`` (a Flush), each call runs
     after the caches were flushed, so no call finds its inputs cached.  The
+    stream is kept busy (the flush, or a short device spin) while fn is
+    submitted, so the host's launch latency is not timed.  The
     benchmark contract's timing: median of >= 20 event-timed calls after 5
     warm-ups, flushed for the HBM-bound kernels."""
     import numpy as np
@@ -96,9 +98,15 @@ def timed_median(fn, iters=20, warmup=5, flush=None):
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     times = []
     for _ in range(iters):
+        torch.cuda.synchronize()
+        # queued ahead of the start event with no host wait: the stream is
+        # busy (the flush read, >100 us, or a device spin of about 50 us)
+        # while the host records the start event and submits fn, so the timed
+        # region holds fn's GPU work and not the host's submission latency
         if flush:
             flush()
-        torch.cuda.synchronize()
+        else:
+            torch.cuda._sleep(100_000)
         s.record()
         fn()
         e.record()

@@ -116,13 +116,12 @@ __device__ __forceinline__ float quot_bf16(float x, const QDiv& d) {
 // r = (x - n*LN2_HI) - n*LN2_LO with LN2_HI holding 16 significant bits (so
 // n*LN2_HI is exact), degree-7 Taylor polynomial by Horner, times 2^n built
 // from the exponent field.  x > 88 -> +inf, x < -87 -> 0.  About 1.2 ulp.
-__device__ __forceinline__ float expf32(float x) {
+// The common part of expf32: xc is x clamped to [-88, 89] (or a subrange
+// that holds every x the caller can pass).
+__device__ __forceinline__ float expf32_core(float x, float xc) {
   const float kLog2e = 1.4426950408889634f;
   const float kLn2Hi = __uint_as_float(0x3f317200u);
   const float kLn2Lo = __uint_as_float(0x35bfbe8eu);
-  // evaluated unconditionally and selected at the end (no branches: the
-  // range tests would otherwise split the wave's control flow per call)
-  const float xc = fminf(fmaxf(x, -88.0f), 89.0f);  // keeps n in int range; result replaced below
   float n = __builtin_rintf(xc * kLog2e);
   float r = xc - n * kLn2Hi;
   r = r - n * kLn2Lo;
@@ -136,9 +135,34 @@ __device__ __forceinline__ float expf32(float x) {
   p = p * r + 1.0f;
   float two_n = __uint_as_float((uint32_t)((int)n + 127) << 23);
   float y = p * two_n;
-  y = x > 88.0f ? __builtin_inff() : y;
   y = x < -87.0f ? 0.0f : y;
   return x != x ? x : y;  // NaN in, NaN out (the range tests are false for NaN)
+}
+
+__device__ __forceinline__ float expf32(float x) {
+  // evaluated unconditionally and selected at the end (no branches: the
+  // range tests would otherwise split the wave's control flow per call)
+  const float xc = fminf(fmaxf(x, -88.0f), 89.0f);  // keeps n in int range; result replaced below
+  const float y = expf32_core(x, xc);
+  return x > 88.0f ? __builtin_inff() : y;
+}
+
+// expf32 for x <= 0, -inf or NaN (a softmax's x - max): the upper clamp and
+// the overflow select never apply there, so the bits equal expf32(x).
+__device__ __forceinline__ float expf32_nonpos(float x) {
+  return expf32_core(x, fmaxf(x, -88.0f));
+}
+
+// a / b correctly rounded, from y = RN(1/b): q0 = RN(a*y), the remainder
+// a - q0*b is exact in one fma, and RN(q0 + rem*y) is RN(a/b) whenever the
+// quotient and the remainder are normal (Markstein's division theorem; Muller
+// et al., Handbook of Floating-Point Arithmetic, the fma-based division
+// section).  The callers keep a >= 2^-100 or a == 0 and b in [1, 2048], and
+// send any other a to the IEEE division.
+__device__ __forceinline__ float div_by_recip(float a, float b, float y) {
+  const float q0 = a * y;
+  const float rem = __builtin_fmaf(-q0, b, a);
+  return __builtin_fmaf(rem, y, q0);
 }
 
 __device__ __forceinline__ float silu32(float g) { return g / (1.0f + expf32(-g)); }
@@ -169,8 +193,8 @@ __device__ __forceinline__ float row16_max(float v) {
 template <int kO>
 __device__ __forceinline__ int xor_lanes(int v) {
   static_assert(kO == 1 || kO == 2 || kO == 4 || kO == 8 || kO == 16 || kO == 32, "xor distance");
-  if constexpr (kO == 1) return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
-  else if constexpr (kO == 2) return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
+  if constexpr (kO == 1) return __builtin_amdgcn_update_dpp(v, v, 0xB1, 0xF, 0xF, false);
+  else if constexpr (kO == 2) return __builtin_amdgcn_update_dpp(v, v, 0x4E, 0xF, 0xF, false);
   else if constexpr (kO < 32) return __builtin_amdgcn_ds_swizzle(v, (kO << 10) | 0x1F);
   else return __shfl_xor(v, 32, kWave);
 }

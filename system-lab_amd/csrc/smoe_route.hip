@@ -39,13 +39,27 @@ constexpr int kSeg = 512;  // pairs per segment (one wave)
 // row's result.  Levels 16 and 32 (64-lane groups) are lane swaps.
 template <int kO>
 __device__ __forceinline__ int red_lanes(int v) {
-  if constexpr (kO == 4) return __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);
-  else if constexpr (kO == 8) return __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false);
+  // every lane is written (full masks), so the old value is v itself: no
+  // register needs clearing first
+  if constexpr (kO == 4) return __builtin_amdgcn_update_dpp(v, v, 0x141, 0xF, 0xF, false);
+  else if constexpr (kO == 8) return __builtin_amdgcn_update_dpp(v, v, 0x140, 0xF, 0xF, false);
   else return xor_lanes<kO>(v);
 }
 template <int kO>
 __device__ __forceinline__ float red_lanes(float v) {
   return __int_as_float(red_lanes<kO>(__float_as_int(v)));
+}
+
+// max(v, partner lane's v) for red_lanes' partners.  Rows of 16 use
+// mov_dpp (old value undefined: every lane is written under full masks), so
+// the compiler folds the lane move into the max as a DPP operand.
+template <int kO>
+__device__ __forceinline__ uint32_t max_lanes(uint32_t v) {
+  if constexpr (kO == 1) return max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false));
+  else if constexpr (kO == 2) return max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false));
+  else if constexpr (kO == 4) return max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x141, 0xF, 0xF, false));
+  else if constexpr (kO == 8) return max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x140, 0xF, 0xF, false));
+  else return max(v, (uint32_t)xor_lanes<kO>((int)v));
 }
 
 // One level of the arg-max reduction: the partner lane (red_lanes) wins with a
@@ -74,16 +88,70 @@ __device__ __forceinline__ void group_levels(F&& f) {
   f(std::integral_constant<int, 1>{});
 }
 
-// Routing of one token by a group of kLPT (16 or 64) lanes; lane i of the
-// group holds experts e = i + kLPT*q, q < kNV.
+// Unsigned key of a selection score: larger score -> larger key, NaN (1)
+// below every number, 0 for "no expert".  The order of a stable descending
+// sort that puts NaN last (the oracle's argsort).  A score is p or p + bias
+// with p >= +0, so it is never -0 (+0 + -0 is +0) and equal scores have
+// equal keys.
+__device__ __forceinline__ uint32_t score_key(float s) {
+  const uint32_t u = __float_as_uint(s);
+  const uint32_t k = u ^ ((uint32_t)((int32_t)u >> 31) | 0x80000000u);
+  return s != s ? 1u : k;
+}
+
+// Softmax probabilities of one token's experts e = i + kLPT*q (q < kNV) held
+// by lane i of a kLPT-lane group, from the logits already loaded into p[].
 //
-// Bit-reproducibility: the softmax denominator is the reduction tree of a
-// 64-lane wave in which "virtual lane" j (0..63) sums experts j, j+64, ...
-// in order and a butterfly at distances 32, 16, ..., 1 combines the lanes.
-// With 16 lanes per token, virtual lane j = i + 16a lives in physical lane i
+// Bit-reproducibility: the denominator is the reduction tree of a 64-lane
+// wave in which "virtual lane" j (0..63) sums experts j, j+64, ... in order
+// and a butterfly at distances 32, 16, ..., 1 combines the lanes.  With 16
+// lanes per token, virtual lane j = i + 16a lives in physical lane i
 // (a = q mod 4), so distances 32 and 16 are additions between a lane's own
 // four partial sums and distances 8..1 are lane exchanges: the same
 // operations on the same operands as the 64-lane tree, hence the same bits.
+// The quotients p/den are correctly rounded (div_by_recip, or the IEEE
+// division when some p is below 2^-100 anywhere in the wave).
+template <int kLPT, int kNV, class Red>
+__device__ __forceinline__ void token_softmax(float (&p)[kNV], Red red, float& m_out,
+                                              float& den_out) {
+  constexpr int kVirt = 64 / kLPT;
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int q = 0; q < kNV; ++q) m = fmaxf(m, p[q]);
+  group_levels<kLPT>([&](auto o) { m = fmaxf(m, red(o, m)); });
+  float vs[kVirt];
+#pragma unroll
+  for (int a = 0; a < kVirt; ++a) vs[a] = 0.0f;
+#pragma unroll
+  for (int q = 0; q < kNV; ++q) {
+    p[q] = expf32_nonpos(p[q] - m);  // experts past E hold -inf: exp gives exactly 0
+    vs[q % kVirt] = vs[q % kVirt] + p[q];
+  }
+  float den;
+  if constexpr (kVirt == 4) den = (vs[0] + vs[2]) + (vs[1] + vs[3]);  // distances 32, 16
+  else den = vs[0];
+  // the sum keeps the xor partners: its rounding is part of the contract
+  group_levels<kLPT>([&](auto o) { den = den + xor_lanes<decltype(o)::value>(den); });
+  bool tiny = false;
+#pragma unroll
+  for (int q = 0; q < kNV; ++q) tiny = tiny | ((p[q] > 0.0f) & (p[q] < 0x1p-100f));
+  if (__builtin_amdgcn_ballot_w64(tiny)) {
+#pragma unroll
+    for (int q = 0; q < kNV; ++q) p[q] = p[q] / den;
+  } else {
+    const float y = 1.0f / den;
+#pragma unroll
+    for (int q = 0; q < kNV; ++q) p[q] = div_by_recip(p[q], den, y);
+  }
+  m_out = m;
+  den_out = den;
+}
+
+// Routing of one token by a group of kLPT (16 or 64) lanes; lane i of the
+// group holds experts e = i + kLPT*q, q < kNV.  ptab is the group's E-float
+// LDS table (a wave's LDS accesses complete in order, so no barrier guards
+// it within the group).
+//
 // Top-K is a total order (score desc, id asc), so the arg-max tree shape
 // does not change the picks; the K picked probabilities are summed in pick
 // order.  Lane (k mod kLPT) returns pick k in slot k / kLPT.
@@ -96,110 +164,103 @@ struct TokenRoute {
 template <int kLPT, int kNV>
 __device__ __forceinline__ TokenRoute<kLPT, kNV> route_token(const float* __restrict__ row,
                                                              const float* __restrict__ bias,
-                                                             int E, int K, int i) {
-  constexpr int kVirt = 64 / kLPT;  // virtual lanes per physical lane
+                                                             int E, int K, int i,
+                                                             float* __restrict__ ptab) {
   float p[kNV];
-  uint32_t ok = 0;  // bit q: expert i + kLPT*q is valid and not yet picked
-  float m = -__builtin_inff();
+  float b[kNV];  // the selection bias
   // every load is unconditional (experts past E re-read expert E-1 and are
   // masked afterwards): a load under a branch would get a vmcnt(0) wait at
   // the branch join, one HBM round trip per load
-  float sc[kNV];  // the selection bias, then the selection scores
+  if (E == kLPT * kNV) {  // every expert index is valid: constant offsets
 #pragma unroll
-  for (int q = 0; q < kNV; ++q) p[q] = row[min(i + kLPT * q, E - 1)];
-  if (bias) {
+    for (int q = 0; q < kNV; ++q) p[q] = row[i + kLPT * q];
+    if (bias) {
 #pragma unroll
-    for (int q = 0; q < kNV; ++q) sc[q] = bias[min(i + kLPT * q, E - 1)];
+      for (int q = 0; q < kNV; ++q) b[q] = bias[i + kLPT * q];
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < kNV; ++q) p[q] = row[min(i + kLPT * q, E - 1)];
+    if (bias) {
+#pragma unroll
+      for (int q = 0; q < kNV; ++q) b[q] = bias[min(i + kLPT * q, E - 1)];
+    }
+#pragma unroll
+    for (int q = 0; q < kNV; ++q)
+      if (i + kLPT * q >= E) p[q] = -__builtin_inff();
   }
+  float m, den;
+  token_softmax<kLPT, kNV>(p, [](auto o, float v) { return red_lanes<decltype(o)::value>(v); }, m,
+                           den);
+  uint32_t key[kNV];
 #pragma unroll
   for (int q = 0; q < kNV; ++q) {
     const int e = i + kLPT * q;
-    if (e < E) ok |= 1u << q;
-    else p[q] = -__builtin_inff();
-    m = fmaxf(m, p[q]);
+    ptab[e] = p[q];  // the table has kLPT*kNV entries: no test needed
+    key[q] = e < E ? score_key(bias ? p[q] + b[q] : p[q]) : 0u;
   }
-  group_levels<kLPT>([&](auto o) { m = fmaxf(m, red_lanes<decltype(o)::value>(m)); });
-  float vs[kVirt];
-#pragma unroll
-  for (int a = 0; a < kVirt; ++a) vs[a] = 0.0f;
-#pragma unroll
-  for (int q = 0; q < kNV; ++q) {
-    p[q] = expf32(p[q] - m);  // experts past E hold -inf: exp gives exactly 0
-    vs[q % kVirt] = vs[q % kVirt] + p[q];
-  }
-  float den;
-  if constexpr (kVirt == 4) den = (vs[0] + vs[2]) + (vs[1] + vs[3]);  // distances 32, 16
-  else den = vs[0];
-  // the sum keeps the xor partners: its rounding is part of the contract
-  group_levels<kLPT>([&](auto o) { den = den + xor_lanes<decltype(o)::value>(den); });
-#pragma unroll
-  for (int q = 0; q < kNV; ++q) {
-    p[q] = p[q] / den;
-    sc[q] = bias ? p[q] + ((ok >> q) & 1u ? sc[q] : 0.0f) : p[q];
-  }
-  TokenRoute<kLPT, kNV> r;
-  r.id[0] = r.id[1] = 0;
-  r.w[0] = 0.0f;
-  r.w[1] = 0.0f;
   // Each lane offers its best expert not yet picked; the group's arg-max
-  // picks one per round.  A lane keeps its two best remaining experts (slot
-  // 0 before slot 1) and rescans only when both are gone: the experts a lane
-  // gave up are exactly its best ones in the order (score desc, id asc), so
-  // the rest are those after the last one it gave up (ls, li).
-  constexpr int kNone = 0x7fffffff;
-  float s0 = 0.0f, s1 = 0.0f, p0 = 0.0f, p1 = 0.0f;
-  int i0 = kNone, i1 = kNone;
-  float ls = 0.0f;
-  int li = -1;  // -1: nothing given up yet
-  bool more = true;  // experts beyond the two slots may remain
-  // Experts past E hold score -inf and an id >= E, so they lose every
-  // comparison against a real expert (on equal scores the lower id wins):
-  // with K <= E they are never picked and need no separate mask.
-#pragma unroll
-  for (int q = 0; q < kNV; ++q)
-    if (!((ok >> q) & 1u)) sc[q] = -__builtin_inff();
-  auto top2 = [&](auto refill) {
-    i0 = i1 = kNone;
+  // picks one per round.  A lane keeps its three best remaining experts
+  // (slot 0 first) and rescans only when all three are gone: the experts a
+  // lane gave up are exactly its best ones in the order (score desc, id
+  // asc), so the rest are those after the last one it gave up (lk, li).
+  uint32_t s0 = 0, s1 = 0, s2 = 0;  // keys; 0 = empty slot
+  int i0 = -1, i1 = -1, i2 = -1;
+  uint32_t lk = 0;
+  int li = -1;
+  auto top3 = [&](auto refill) {
+    s0 = s1 = s2 = 0;
+    i0 = i1 = i2 = -1;
 #pragma unroll
     for (int q = 0; q < kNV; ++q) {
       const int id = i + kLPT * q;
-      // ids ascend with q: a strict > keeps the lower id ahead on equal
-      // scores (bitwise operators: no branches)
-      bool c0 = (i0 == kNone) | (sc[q] > s0);
-      bool c1 = (i1 == kNone) | (sc[q] > s1);
-      if constexpr (decltype(refill)::value) {
-        const bool elig = (sc[q] < ls) | ((sc[q] == ls) & (id > li));
-        c0 = c0 & elig;
-        c1 = c1 & elig;
-      }
-      c1 = c1 & !c0;
-      s1 = c0 ? s0 : (c1 ? sc[q] : s1);
+      uint32_t u = key[q];
+      if constexpr (decltype(refill)::value)
+        u = ((u < lk) | ((u == lk) & (id > li))) ? u : 0u;  // experts not yet given up
+      // ids ascend with q: a strict > keeps the lower id ahead on equal keys
+      const bool c0 = u > s0, c1 = u > s1, c2 = u > s2;
+      s2 = c1 ? s1 : (c2 ? u : s2);
+      i2 = c1 ? i1 : (c2 ? id : i2);
+      s1 = c0 ? s0 : (c1 ? u : s1);
       i1 = c0 ? i0 : (c1 ? id : i1);
-      p1 = c0 ? p0 : (c1 ? p[q] : p1);
-      s0 = c0 ? sc[q] : s0;
+      s0 = c0 ? u : s0;
       i0 = c0 ? id : i0;
-      p0 = c0 ? p[q] : p0;
     }
-    more = i1 != kNone;
   };
-  top2(std::false_type{});
+  top3(std::false_type{});
+  bool more = s2 != 0;  // experts beyond the three slots may remain
+  TokenRoute<kLPT, kNV> r;
+  r.id[0] = r.id[1] = 0;
+  r.w[0] = r.w[1] = 0.0f;
   float psum = 0.0f;
   for (int k = 0; k < K; ++k) {
-    float bs = s0, bp = p0;
-    int bi = i0;
-    group_levels<kLPT>([&](auto o) { argmax_step<decltype(o)::value>(bs, bi, bp); });
+    // arg-max of (key, -id) over the group in two order-free max passes:
+    // the largest key, then the largest ~id among the lanes offering it.
+    // An empty lane offers key 0 and loses to every expert (K <= E
+    // guarantees a real winner).
+    uint32_t hi = s0;
+    group_levels<kLPT>([&](auto o) { hi = max_lanes<decltype(o)::value>(hi); });
+    uint32_t lo = s0 == hi ? ~(uint32_t)i0 : 0u;
+    group_levels<kLPT>([&](auto o) { lo = max_lanes<decltype(o)::value>(lo); });
+    const int bi = (int)~lo;
     if (bi == i0) {  // this lane gave the winner: advance its slots
-      ls = s0;
+      lk = s0;
       li = i0;
       s0 = s1;
       i0 = i1;
-      p0 = p1;
-      i1 = kNone;
+      s1 = s2;
+      i1 = i2;
+      s2 = 0;
+      i2 = -1;
     }
-    const bool refill = i0 == kNone && more;
+    const bool refill = (s0 == 0) & more;
     if (__builtin_amdgcn_ballot_w64(refill)) {
-      if (refill) top2(std::true_type{});
+      if (refill) {
+        top3(std::true_type{});
+        more = s2 != 0;
+      }
     }
+    const float bp = ptab[bi];
     psum = psum + bp;
     if ((k & (kLPT - 1)) == i) {  // static slot indices keep r in registers
       if (kLPT == 64 || k < kLPT) {
@@ -221,10 +282,13 @@ template <int kLPT, int kNV>
 __global__ __launch_bounds__(256) void router_topk_kernel(
     const float* __restrict__ logits, const float* __restrict__ bias, int T, int E, int K,
     int32_t* __restrict__ topk_idx, float* __restrict__ topk_w) {
+  __shared__ float ptab[256 * kNV];  // E <= kLPT*kNV probabilities per token group
   const int i = threadIdx.x & (kLPT - 1);
-  const int t = blockIdx.x * (256 / kLPT) + threadIdx.x / kLPT;
+  const int g = threadIdx.x / kLPT;
+  const int t = blockIdx.x * (256 / kLPT) + g;
   if (t >= T) return;  // whole token groups leave; no workgroup barrier below
-  const TokenRoute<kLPT, kNV> r = route_token<kLPT, kNV>(logits + (size_t)t * E, bias, E, K, i);
+  const TokenRoute<kLPT, kNV> r =
+      route_token<kLPT, kNV>(logits + (size_t)t * E, bias, E, K, i, ptab + g * kLPT * kNV);
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
     const int k = s * kLPT + i;
@@ -248,38 +312,20 @@ template <int kLPT, int kNV, int kMaxK>
 __global__ __launch_bounds__(256) void router_topk_bwd_kernel(
     const float* __restrict__ logits, const int32_t* __restrict__ topk_idx,
     const float* __restrict__ dtopk_w, int T, int E, int K, float* __restrict__ dlogits) {
-  constexpr int kVirt = 64 / kLPT;
   const int i = threadIdx.x & (kLPT - 1);
   const int t = blockIdx.x * (256 / kLPT) + threadIdx.x / kLPT;
   if (t >= T) return;
   const float* row = logits + (size_t)t * E;
   float p[kNV];
-  float m = -__builtin_inff();
 #pragma unroll
   for (int q = 0; q < kNV; ++q) p[q] = row[min(i + kLPT * q, E - 1)];  // unconditional loads
 #pragma unroll
-  for (int q = 0; q < kNV; ++q) {
+  for (int q = 0; q < kNV; ++q)
     if (i + kLPT * q >= E) p[q] = -__builtin_inff();
-    m = fmaxf(m, p[q]);
-  }
-  group_levels<kLPT>([&](auto o) { m = fmaxf(m, xor_lanes<decltype(o)::value>(m)); });
-  float vs[kVirt];
-#pragma unroll
-  for (int a = 0; a < kVirt; ++a) vs[a] = 0.0f;
-#pragma unroll
-  for (int q = 0; q < kNV; ++q) {
-    p[q] = expf32(p[q] - m);  // experts past E hold -inf: exp gives exactly 0
-    vs[q % kVirt] = vs[q % kVirt] + p[q];
-  }
-  float den;
-  if constexpr (kVirt == 4) den = (vs[0] + vs[2]) + (vs[1] + vs[3]);
-  else den = vs[0];
-  group_levels<kLPT>([&](auto o) { den = den + xor_lanes<decltype(o)::value>(den); });
-#pragma unroll
-  for (int q = 0; q < kNV; ++q) p[q] = p[q] / den;
   const int32_t* ids = topk_idx + (size_t)t * K;
   const float* g = dtopk_w + (size_t)t * K;
-  // the picked probabilities, once each.  K <= kMaxK: static indices keep
+  // the picked logits, loaded before the softmax so that their latency
+  // overlaps it; their probabilities are formed once each.  K <= kMaxK: static indices keep
   // the arrays in registers, and the loads are unconditional (index clamped
   // to K-1, the extra terms masked) so that all of them are in flight at once.
   float pk[kMaxK], gk[kMaxK];
@@ -291,10 +337,13 @@ __global__ __launch_bounds__(256) void router_topk_bwd_kernel(
   }
 #pragma unroll
   for (int k = 0; k < kMaxK; ++k) pk[k] = row[ek[k]];
+  float m, den;
+  token_softmax<kLPT, kNV>(p, [](auto o, float v) { return xor_lanes<decltype(o)::value>(v); }, m,
+                           den);
   float psum = 0.0f;
 #pragma unroll
   for (int k = 0; k < kMaxK; ++k) {
-    pk[k] = expf32(pk[k] - m) / den;
+    pk[k] = expf32_nonpos(pk[k] - m) / den;
     psum = k < K ? psum + pk[k] : psum;
   }
   float c = 0.0f;
@@ -334,6 +383,7 @@ __global__ __launch_bounds__(kHistThreads) void router_hist_kernel(
     int nseg, int32_t* __restrict__ topk_idx, float* __restrict__ topk_w,
     int32_t* __restrict__ hist) {
   extern __shared__ int32_t hh[];  // [E]
+  __shared__ float ptab[kHistThreads * kNV];  // E <= kLPT*kNV probabilities per token group
   const int seg = blockIdx.x;
   const int R = T * K;
   for (int e = threadIdx.x; e < E; e += kHistThreads) hh[e] = 0;
@@ -342,7 +392,8 @@ __global__ __launch_bounds__(kHistThreads) void router_hist_kernel(
   const int t0 = p0 / K, t1 = (p1 - 1) / K;  // tokens with a pair in [p0, p1)
   const int i = threadIdx.x & (kLPT - 1);
   for (int t = t0 + threadIdx.x / kLPT; t <= t1; t += kHistThreads / kLPT) {
-    const TokenRoute<kLPT, kNV> r = route_token<kLPT, kNV>(logits + (size_t)t * E, bias, E, K, i);
+    const TokenRoute<kLPT, kNV> r = route_token<kLPT, kNV>(
+        logits + (size_t)t * E, bias, E, K, i, ptab + (threadIdx.x / kLPT) * kLPT * kNV);
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       const int k = s * kLPT + i;

@@ -95,6 +95,43 @@ def test_router_ties(dev):
     assert np.array_equal(w.cpu().numpy(), rw)
 
 
+@pytest.mark.parametrize("E,K,bias", [(256, 8, True), (256, 8, False), (64, 32, True),
+                                     (16, 16, False), (1024, 32, True), (37, 32, False)])
+def test_router_extremes(dev, E, K, bias):
+    """Rows that reach every branch of the selection: logits spread over
+    hundreds of nats (probabilities that underflow to 0 or sit below 2^-100,
+    where the quotient is formed by the IEEE division), integer ties in
+    logits and bias, K up to E (lanes that exhaust their candidate slots and
+    rescan), and one all-NaN row (ids 0..K-1 and NaN weights, as the
+    oracle's stable argsort gives)."""
+    say("router extremes", E, K, bias)
+    rng = np.random.default_rng(E * 100 + K)
+    T = 256
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    lg[0:64] *= 60.0                                            # huge spreads
+    lg[64:128] = rng.integers(-2, 3, (64, E)).astype(np.float32)  # ties
+    lg[128:160] = -1e30                                         # one expert per row survives
+    lg[128:160, 0] = 0.0
+    lg[200] = np.nan
+    b = None
+    if bias:
+        b = rng.integers(-1, 2, E).astype(np.float32) * np.float32(0.25)
+    with np.errstate(invalid="ignore"):
+        ri, rw = O.router_topk(lg, K, b)
+    idx, w = ops.router_topk(torch.from_numpy(lg).to(dev), K,
+                             None if b is None else torch.from_numpy(b).to(dev))
+    gi, gw = idx.cpu().numpy(), w.cpu().numpy()
+    assert np.array_equal(gi, ri)
+    fin = ~np.isnan(rw)
+    assert np.array_equal(np.isnan(gw), ~fin)
+    assert np.array_equal(gw[fin].view(np.uint32), rw[fin].view(np.uint32))
+    got = ops.route_topk_sort(torch.from_numpy(lg).to(dev), K,
+                              None if b is None else torch.from_numpy(b).to(dev))
+    assert np.array_equal(got[0].cpu().numpy(), ri)
+    gw2 = got[1].cpu().numpy()
+    assert np.array_equal(gw2[fin].view(np.uint32), rw[fin].view(np.uint32))
+
+
 # -------------------------------------------------------------------- sort
 def _check_sort(dev, idx_np, E):
     T, K = idx_np.shape
