@@ -273,13 +273,19 @@ def bench_layer(dev, steps, warmup):
     m.refresh_fp8_cache()
     x, lg = W.tokens(c.T, c.H, device=dev), W.logits(c.T, c.E, device=dev)
     # a whole layer is ~10 launches from Python: back-to-back calls measure
-    # its throughput with the host enqueueing ahead of the GPU
-    t = timed(lambda: m(x, lg), steps, warmup)
+    # its throughput with the host enqueueing ahead of the GPU.  Without
+    # autograd the layer runs fc1 with the fused SwiGLU epilogue; with it,
+    # the forward also keeps what the backward needs (c1, bf16 h).
+    with torch.no_grad():
+        t = timed(lambda: m(x, lg), steps, warmup)
+    t_train = timed(lambda: m(x, lg), steps, warmup)
     fl = 2.0 * c.T * c.K * (2 * c.I) * c.H + 2.0 * c.T * c.K * c.H * c.I
     del m
     torch.cuda.empty_cache()
     return {"workload": "mixtral layer fwd T=8192 H=4096 I=14336 E=8 top2",
-            "ms": round(t, 4), "tflops": round(fl / (t * 1e-3) / 1e12, 1)}
+            "ms": round(t, 4), "tflops": round(fl / (t * 1e-3) / 1e12, 1),
+            "ms_with_autograd": round(t_train, 4),
+            "tflops_with_autograd": round(fl / (t_train * 1e-3) / 1e12, 1)}
 
 
 def bench_fwd_bwd(dev, steps, warmup):
@@ -368,7 +374,9 @@ def run_only(args, dev, c):
     combine = config-2 sized combine, copy = a plain 1 GiB device copy
     (calibrates the FETCH_SIZE / WRITE_SIZE counters against known traffic),
     ceiling = the HBM traffic-mix probe, blaslt = hipBLASLt's dense fp8 GEMM
-    at the config-4 shapes, router = the fused router + sort at config 2."""
+    at the config-4 shapes, router = the fused router + sort at config 2,
+    wgrad = the config-5 fc1 weight gradient, fwdbwd = the config-5 layer
+    forward + backward, layer = the config-3 (Mixtral) layer forward."""
     import torch
     from smoe import ops, workloads as W
     if args.only == "copy":
@@ -388,6 +396,8 @@ def run_only(args, dev, c):
         print(json.dumps({"only": "router", **bench_router(dev, c, args.steps, args.warmup)}))
     elif args.only == "fwdbwd":
         print(json.dumps({"only": "fwdbwd", **bench_fwd_bwd(dev, args.steps, args.warmup)}))
+    elif args.only == "layer":
+        print(json.dumps({"only": "layer", **bench_layer(dev, args.steps, args.warmup)}))
     elif args.only == "gemm":
         print(json.dumps({"only": "gemm", **bench_gemm(dev, args.steps, args.warmup)}))
     elif args.only == "ceiling":
@@ -455,7 +465,7 @@ def main():
     ap.add_argument("--skip-extra", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--only", choices=["permute", "gemm", "combine", "copy", "fwdbwd", "ceiling",
-                                       "blaslt", "router", "wgrad"],
+                                       "blaslt", "router", "wgrad", "layer"],
                     help="run one kernel family only (for rocprofv3 runs) and print its timing")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
