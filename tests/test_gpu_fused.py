@@ -79,7 +79,11 @@ def test_fused_swiglu_row_window(dev):
 
 def test_fused_swiglu_dsv3_full_shape(dev):
     """Benchmark config 4's fc1 (R=65536, 32 Zipf-loaded experts with
-    zero-token ones, I=2048, K=7168) at full size against the two-kernel path."""
+    zero-token ones, I=2048, K=7168) at full size: the fused epilogue's
+    bytes against the two-kernel path over every row, and directly against
+    the float64 oracle on 10 sampled rows of every non-empty expert (first
+    and last included): c1 within the GEMM bar, hq/hs bit-exact to the
+    oracle's SwiGLU requantisation of those c1 rows."""
     say("fused swiglu dsv3 full")
     c = W.CONFIGS["dsv3"]
     off = W.offsets_from_counts(W.zipf_counts()).to(dev)
@@ -88,7 +92,29 @@ def test_fused_swiglu_dsv3_full_shape(dev):
     del x
     wq, ws = ops.quantize_weight_blockwise(W.weights(c.E, 2 * c.I, c.H, device=dev, seed=3))
     _check_same(dev, xq, xs, wq, ws, off)
-    del wq, ws
+    hq, hs, c1 = ops.grouped_gemm_fp8_swiglu(xq, xs, wq, ws, off, save_c1=True)
+    off_np = off.cpu().numpy()
+    rng = np.random.default_rng(12)
+    rows = []
+    for e in range(c.E):
+        lo, hi = int(off_np[e]), int(off_np[e + 1])
+        if hi > lo:
+            rows += [lo, hi - 1] + list(rng.integers(lo, hi, 8))
+    rows = np.unique(np.array(rows))
+    ex = np.searchsorted(off_np, rows, side="right") - 1
+    soff = np.concatenate([[0], np.cumsum(np.bincount(ex, minlength=c.E))]).astype(np.int32)
+    ridx = torch.from_numpy(rows).to(dev)
+    ref = O.grouped_gemm_fp8(_bytes(xq[ridx]).cpu().numpy(), xs[ridx].cpu().numpy(),
+                             _bytes(wq).cpu().numpy(), ws.cpu().numpy(), soff)
+    c1_s = c1[ridx].view(torch.int16).cpu().numpy().view(np.uint16)
+    ref = O.bf16_to_f32(O.f32_to_bf16(ref.astype(np.float32))).astype(np.float64)
+    got = O.bf16_to_f32(c1_s).astype(np.float64)
+    d = np.abs(got - ref)
+    assert d.max() <= 1e-2 * np.abs(ref).max() and d.mean() <= 1e-3 * np.abs(ref).mean()
+    oq, os_ = O.swiglu_quant(c1_s)
+    assert np.array_equal(_bytes(hq[ridx]).cpu().numpy(), oq), "fused SwiGLU bytes vs oracle"
+    assert np.array_equal(hs[ridx].cpu().numpy().view(np.uint32), os_.view(np.uint32))
+    del wq, ws, hq, hs, c1
     torch.cuda.empty_cache()
 
 
