@@ -5,10 +5,52 @@ Python host code over a C-ABI library of hand-written HIP kernels
 """
 from . import _C, ops, workloads  # noqa: F401
 from .layer import SimpleMoE  # noqa: F401
-from .ops import (grouped_gemm_fp8, permute_quant, permute_quant_rows,  # noqa: F401
-                  quantize_weight_blockwise, route_sort, router_topk, swiglu_quant,
-                  unpermute_combine)
+from .ops import (  # noqa: F401
+    router_topk,
+    router_topk_bwd,
+    last_route_status,
+    check_route_status,
+    route_sort,
+    route_topk_sort,
+    permute_quant_rows,
+    permute_quant,
+    quantize_weight_blockwise,
+    grouped_gemm_fp8,
+    grouped_gemm_fp8_swiglu,
+    swiglu_quant,
+    unpermute_combine,
+    quant_rows,
+    transpose_blockwise,
+    quant_cols,
+    quant_rows_cols,
+    swiglu_bwd_quant,
+    grouped_gemm_fp8_wgrad,
+    swiglu_bwd,
+    unpermute_combine_bwd,
+    unpermute_combine_bwd_quant,
+)
 
-__all__ = ["SimpleMoE", "router_topk", "route_sort", "permute_quant", "permute_quant_rows",
-           "quantize_weight_blockwise", "grouped_gemm_fp8", "swiglu_quant",
-           "unpermute_combine", "workloads"]
+__all__ = ["SimpleMoE", "workloads",
+           "router_topk",
+           "router_topk_bwd",
+           "last_route_status",
+           "check_route_status",
+           "route_sort",
+           "route_topk_sort",
+           "permute_quant_rows",
+           "permute_quant",
+           "quantize_weight_blockwise",
+           "grouped_gemm_fp8",
+           "grouped_gemm_fp8_swiglu",
+           "swiglu_quant",
+           "unpermute_combine",
+           "quant_rows",
+           "transpose_blockwise",
+           "quant_cols",
+           "quant_rows_cols",
+           "swiglu_bwd_quant",
+           "grouped_gemm_fp8_wgrad",
+           "swiglu_bwd",
+           "unpermute_combine_bwd",
+           "unpermute_combine_bwd_quant",
+           ]
