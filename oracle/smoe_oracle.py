@@ -28,6 +28,7 @@ oracle evaluates those in exactly the order the kernels do, in float32.
 Pinning (what checks each function; tests/test_oracle.py):
   e4m3_encode      torch.float8_e4m3fn cast (library RNE) after clamp, over
                    every bf16 pattern and every e4m3 rounding midpoint +-1 ulp.
+  fma32            C's fmaf (correctly rounded) on random and cancelling triples.
   expf32           numpy float64 exp (error bound <= 2 ulp), special values.
   router_topk      brute-force python sort on tiny inputs; closed-form softmax.
   route_sort       the reference's worked 16-token routing example
@@ -137,28 +138,58 @@ _TAYLOR = [F32(1.0 / 5040.0), F32(1.0 / 720.0), F32(1.0 / 120.0), F32(1.0 / 24.0
            F32(1.0 / 6.0), F32(0.5), F32(1.0), F32(1.0)]
 
 
+def fma32(a, b, c) -> np.ndarray:
+    """Fused multiply-add in float32: RN32(a*b + c) with one rounding, the
+    result of the GPU's v_fma_f32.  Emulated in float64: a*b is exact there
+    (24 + 24 bits), s = RN64(a*b + c) and its error err = (a*b + c) - s
+    come from Knuth's TwoSum, and when err != 0 the last bit of s is forced
+    to 1 toward the exact sum (round to odd).  Rounding that 53-bit value to
+    24 bits is then the correct rounding of the exact sum (Boldo and
+    Melquiond, "Emulation of FMA and correctly rounded sums: proved
+    algorithms using rounding to odd", IEEE TC 2008), float32 subnormals
+    included since float64 has the exponent range to hold them exactly.
+    Finite inputs whose sum stays in float64 range only (the exp routine's
+    domain).  Pinned against C's fmaf in tests/test_oracle.py."""
+    a = np.asarray(a, np.float32).astype(np.float64)
+    b = np.asarray(b, np.float32).astype(np.float64)
+    c = np.asarray(c, np.float32).astype(np.float64)
+    p = a * b                         # exact
+    s = p + c
+    bv = s - p
+    err = (p - (s - bv)) + (c - bv)   # TwoSum: p + c = s + err exactly
+    bits = np.ascontiguousarray(s).view(np.int64)
+    even = (bits & 1) == 0
+    # one ulp of s toward the exact sum: away from zero when err has the
+    # sign of s, toward zero otherwise (s == 0 only when the sum is exact)
+    step = np.where(np.signbit(err) == np.signbit(s), 1, -1).astype(np.int64)
+    bits = np.where((err != 0) & even, bits + step, bits)
+    return bits.view(np.float64).astype(np.float32)
+
+
 def expf32(x: np.ndarray) -> np.ndarray:
     """exp in float32 by Cody-Waite range reduction and a degree-7 Taylor
-    polynomial (Horner), every operation a separately rounded fp32 op:
-      n = rint(x*log2e); r = (x - n*LN2_HI) - n*LN2_LO; p(r); p * 2^n.
-    x > 88 -> +inf, x < -87 -> 0.  Max error about 2 ulp over [-87, 88].
-    The HIP kernels evaluate the identical sequence (compiled with
-    -ffp-contract=off), so results are bit-identical.
+    polynomial (Horner), evaluated with fused multiply-adds:
+      n = rint(x*log2e); r = fma(-n, LN2_LO, fma(-n, LN2_HI, x));
+      p = fma(...fma(1/5040, r, 1/720)..., r, 1); p * 2^n.
+    x > 88 -> +inf, x < -87 -> 0, NaN in -> NaN out.  Max error about 1 ulp
+    over [-87, 88].  The HIP kernels evaluate the identical sequence (v_fma_f32
+    for each fma, everything else separately rounded), so results are
+    bit-identical.
     """
     x = np.asarray(x, np.float32)
     xc = np.clip(x, _EXP_LO, _EXP_HI)
     n = np.rint(xc * _LOG2E).astype(np.float32)
-    r = (xc - n * _LN2_HI).astype(np.float32)
-    r = (r - n * _LN2_LO).astype(np.float32)
-    p = _TAYLOR[0]
+    r = fma32(-n, _LN2_HI, xc)
+    r = fma32(-n, _LN2_LO, r)
+    p = np.full(x.shape, _TAYLOR[0], np.float32)
     for c in _TAYLOR[1:]:
-        p = (p * r + c).astype(np.float32)
-    ni = n.astype(np.int32)
+        p = fma32(p, r, np.full(x.shape, c, np.float32))
+    ni = np.where(np.isnan(n), F32(0.0), n).astype(np.int32)  # NaN: replaced below
     two_n = ((ni + 127).astype(np.uint32) << 23).view(np.float32)
     out = (p * two_n).astype(np.float32)
     out = np.where(x > _EXP_HI, F32(np.inf), out)
     out = np.where(x < _EXP_LO, F32(0.0), out)
-    return out.astype(np.float32)
+    return np.where(np.isnan(x), x, out).astype(np.float32)
 
 
 # ---------------------------------------------------------------------------

@@ -32,7 +32,7 @@ namespace smoe {
 constexpr int kSeg = 512;  // pairs per segment (one wave)
 
 // ------------------------------------------------------------------ router
-// A lane of the same 16-lane row for order-free reductions (max, arg-max):
+// A lane of the same 16-lane row for order-free reductions (max):
 // levels 1 and 2 are quad permutes, 4 and 8 the row's half mirror (lane
 // i <-> 7-i of each 8) and full mirror (i <-> 15-i), all DPP moves with no
 // LDS round trip; after the four levels every lane of the row holds the
@@ -60,21 +60,6 @@ __device__ __forceinline__ uint32_t max_lanes(uint32_t v) {
   else if constexpr (kO == 4) return max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x141, 0xF, 0xF, false));
   else if constexpr (kO == 8) return max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x140, 0xF, 0xF, false));
   else return max(v, (uint32_t)xor_lanes<kO>((int)v));
-}
-
-// One level of the arg-max reduction: the partner lane (red_lanes) wins with a
-// larger score, or an equal score and a lower id (0x7fffffff marks a lane
-// with no candidate).
-template <int kO>
-__device__ __forceinline__ void argmax_step(float& bs, int& bi, float& bp) {
-  const float os = red_lanes<kO>(bs);
-  const int oi = red_lanes<kO>(bi);
-  const float op = red_lanes<kO>(bp);
-  // bitwise, not short-circuit, operators: no branches
-  const bool take = (oi != 0x7fffffff) & ((bi == 0x7fffffff) | (os > bs) | ((os == bs) & (oi < bi)));
-  bs = take ? os : bs;
-  bi = take ? oi : bi;
-  bp = take ? op : bp;
 }
 
 // Butterfly over the kLPT lanes of a token group, top level first.
