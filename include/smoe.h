@@ -182,6 +182,16 @@ int smoe_quantize_weight_blockwise(const uint16_t* w, int E, int N, int Kdim, ui
 int smoe_selftest_quant(unsigned long long* counts, void* stream);
 
 /*
+ * No counterpart in the reference: a check of the sigmoid's reciprocal in
+ * the SwiGLU backward.  The kernels form 1/b as v_rcp_f32 plus one Newton
+ * step instead of the IEEE division; this compares the two, on the GPU, for
+ * every fp32 b in [2^-126, 2^126) and for +inf (about 2.11e9 values).
+ * counts [2] u64 on the device, zeroed by the caller, receives: mismatches,
+ * values checked.
+ */
+int smoe_selftest_recip(unsigned long long* counts, void* stream);
+
+/*
  * Dropless fp8 grouped GEMM with blockwise scales.  For each expert e and each
  * row r in [offsets[e], offsets[e+1]):
  *   c[r,n] = bf16( sum_kb as[r,kb]*bs[e,n/128,kb] * sum_{k in kb} a[r,k]*b[e,n,k] )

@@ -260,7 +260,7 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(
           const float g = h ? __uint_as_float(vG[j][i] & 0xffff0000u) : __uint_as_float(vG[j][i] << 16);
           const float u = h ? __uint_as_float(vU[j][i] & 0xffff0000u) : __uint_as_float(vU[j][i] << 16);
           const float d = h ? __uint_as_float(vD[j][i] & 0xffff0000u) : __uint_as_float(vD[j][i] << 16);
-          const float sg = 1.0f / (1.0f + expf32(-g));
+          const float sg = recip_rn(1.0f + expf32(-g));  // = the IEEE 1 / b (smoe_selftest_recip)
           const float silu = g * sg;
           const float ds = sg * (1.0f + g * (1.0f - sg));
           ou[h] = d * silu;
@@ -362,7 +362,7 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(const uint16_t* __restr
         const float g = h ? __uint_as_float(g4[i] & 0xffff0000u) : __uint_as_float(g4[i] << 16);
         const float u = h ? __uint_as_float(u4[i] & 0xffff0000u) : __uint_as_float(u4[i] << 16);
         const float d = h ? __uint_as_float(d4[i] & 0xffff0000u) : __uint_as_float(d4[i] << 16);
-        const float s = 1.0f / (1.0f + expf32(-g));
+        const float s = recip_rn(1.0f + expf32(-g));  // = the IEEE 1 / b (smoe_selftest_recip)
         const float silu = g * s;
         const float ds = s * (1.0f + g * (1.0f - s));
         ub[h] = d * silu;

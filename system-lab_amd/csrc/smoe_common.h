@@ -156,6 +156,17 @@ __device__ __forceinline__ float expf32_nonpos(float x) {
   return expf32_core(x, fmaxf(x, -88.0f));
 }
 
+// 1/b correctly rounded: v_rcp_f32's approximation y0 and one Newton step
+// y0 + y0*(1 - b*y0), both in fmas.  Equal to the IEEE quotient 1.0f / b for
+// every fp32 b in [2^-126, 2^126) (smoe_selftest_recip checks each of those
+// values on the GPU); +inf gives +0 and NaN gives NaN, as the quotient does.
+__device__ __forceinline__ float recip_rn(float b) {
+  const float y0 = __builtin_amdgcn_rcpf(b);
+  const float e = __builtin_fmaf(-b, y0, 1.0f);
+  const float y1 = __builtin_fmaf(e, y0, y0);
+  return b == __builtin_inff() ? 0.0f : y1;
+}
+
 // a / b correctly rounded, from y = RN(1/b): q0 = RN(a*y), the remainder
 // a - q0*b is exact in one fma, and RN(q0 + rem*y) is RN(a/b) whenever the
 // quotient and the remainder are normal (Markstein's division theorem; Muller

@@ -323,6 +323,33 @@ __global__ __launch_bounds__(256) void selftest_bf16_kernel(unsigned long long* 
   }
 }
 
+// recip_rn against the IEEE quotient 1.0f / b for every fp32 b in
+// [2^-126, 2^126) (exponent fields 1..252, every significand), and for +inf.
+// counts[0] gets the mismatches, counts[1] the values checked.
+__global__ __launch_bounds__(256) void selftest_recip_kernel(unsigned long long* __restrict__ counts) {
+  constexpr uint64_t kFirst = 1ull << 23, kEnd = 253ull << 23;  // bit patterns
+  unsigned long long bad = 0, n = 0;
+  for (uint64_t i = kFirst + (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < kEnd;
+       i += (uint64_t)gridDim.x * blockDim.x) {
+    const float b = __uint_as_float((uint32_t)i);
+    bad += __float_as_uint(recip_rn(b)) != __float_as_uint(1.0f / b);
+    ++n;
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    const float inf = __builtin_inff();
+    bad += __float_as_uint(recip_rn(inf)) != __float_as_uint(1.0f / inf);
+    ++n;
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    bad += __shfl_xor(bad, o, kWave);
+    n += __shfl_xor(n, o, kWave);
+  }
+  if ((threadIdx.x & 63) == 0) {
+    atomicAdd(&counts[0], bad);
+    atomicAdd(&counts[1], n);
+  }
+}
+
 }  // namespace smoe
 
 using namespace smoe;
@@ -334,6 +361,13 @@ extern "C" int smoe_selftest_quant(unsigned long long* counts, void* stream) {
   selftest_quant_bf16_kernel<<<dim3(64, 0x7f7f), dim3(256), 0, st>>>(counts);
   selftest_e4m3_kernel<<<dim3(4096), dim3(256), 0, st>>>(counts);
   selftest_bf16_kernel<<<dim3(8192), dim3(256), 0, st>>>(counts);
+  SMOE_RETURN_LAUNCH();
+}
+
+extern "C" int smoe_selftest_recip(unsigned long long* counts, void* stream) {
+  if (!counts) return SMOE_EINVAL_NULL;
+  if ((uintptr_t)counts & 7u) return SMOE_EINVAL_PTRALIGN;
+  selftest_recip_kernel<<<dim3(8192), dim3(256), 0, (hipStream_t)stream>>>(counts);
   SMOE_RETURN_LAUNCH();
 }
 

@@ -32,6 +32,7 @@ SIGNATURES = {
     "smoe_dispatch_quant": (c_int, [P, P, c_int, c_int, c_int, c_int, P, P, P, P, P, P, P,
                                     c_size_t, P]),
     "smoe_selftest_quant": (c_int, [P, P]),
+    "smoe_selftest_recip": (c_int, [P, P]),
     "smoe_bw_probe": (c_int, [P, c_int, c_int, c_int, P, c_size_t, P, P]),
     "smoe_quantize_weight_blockwise": (c_int, [P, c_int, c_int, c_int, P, P, P]),
     "smoe_grouped_gemm_fp8_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int]),

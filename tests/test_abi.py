@@ -172,3 +172,5 @@ def test_remaining_entry_points_reject():
     assert lib.smoe_swiglu_quant_h(FAKE, 10, 128, FAKE, FAKE, MIS, None) == -6
     assert lib.smoe_selftest_quant(None, None) == -1
     assert lib.smoe_selftest_quant(MIS, None) == -6
+    assert lib.smoe_selftest_recip(None, None) == -1
+    assert lib.smoe_selftest_recip(MIS, None) == -6

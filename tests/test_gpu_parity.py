@@ -278,6 +278,18 @@ def test_fast_quantiser_exhaustive(dev):
     assert bad_div == 0 and bad_enc == 0 and bad_bf == 0
 
 
+def test_reciprocal_exhaustive(dev):
+    """The SwiGLU backward's sigmoid forms 1/b as v_rcp_f32 plus one Newton
+    step instead of an IEEE division.  The library's self-test compares the
+    two for every fp32 b in [2^-126, 2^126) and for +inf: no mismatch."""
+    say("reciprocal exhaustive")
+    counts = torch.zeros(2, dtype=torch.int64, device=dev)
+    smoe._C.call("smoe_selftest_recip", counts.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    bad, n = counts.cpu().tolist()
+    assert n == 252 * 2**23 + 1
+    assert bad == 0
+
+
 @pytest.mark.parametrize("T,H,E,K,outl", [(2048, 1024, 8, 2, False), (1024, 7168, 256, 8, True),
                                           (333, 4096, 8, 2, False), (512, 2048, 128, 8, False),
                                           (5, 1152, 4, 3, True), (64, 9216, 16, 4, True)])
