@@ -140,6 +140,8 @@ class SimpleMoE(nn.Module):
     def _forward_impl(self, x: torch.Tensor, logits: torch.Tensor, save: bool):
         x = x.detach().to(torch.bfloat16).contiguous()
         logits = logits.detach().float().contiguous()
+        if x.shape[0] == 0:
+            return self._empty_forward(x, logits, save)
         w1q, w1s, w2q, w2s = self.fp8_weights()
         # router and expert sort in three launches (the sort's histogram is
         # counted inside the router launch)
@@ -162,6 +164,46 @@ class SimpleMoE(nn.Module):
                              c1=c1, hq=hq, hs=hs, h=h, y=y)
         return out
 
+    def _empty_forward(self, x: torch.Tensor, logits: torch.Tensor, save: bool):
+        """An empty batch (T = 0): no kernel runs (the C ABI rejects T = 0);
+        the outputs and intermediates are empty tensors of the usual shapes,
+        with every expert's count 0."""
+        dev, H, I = x.device, self.hidden, self.intermediate
+        E, K = self.num_experts, self.top_k
+        out = torch.empty((0, H), dtype=torch.bfloat16, device=dev)
+        if not save:
+            return out
+        i32 = dict(dtype=torch.int32, device=dev)
+        inter = dict(x=x, logits=logits, topk_idx=torch.empty((0, K), **i32),
+                     topk_w=torch.empty((0, K), dtype=torch.float32, device=dev),
+                     row_map=torch.empty(0, **i32), inv_map=torch.empty(0, **i32),
+                     counts=torch.zeros(E, **i32), offsets=torch.zeros(E + 1, **i32),
+                     xq=torch.empty((0, H), dtype=ops.FP8, device=dev),
+                     xs=torch.empty((0, H // ops.GROUP), dtype=torch.float32, device=dev),
+                     c1=torch.empty((0, 2 * I), dtype=torch.bfloat16, device=dev),
+                     hq=torch.empty((0, I), dtype=ops.FP8, device=dev),
+                     hs=torch.empty((0, I // ops.GROUP), dtype=torch.float32, device=dev),
+                     h=torch.empty((0, I), dtype=torch.bfloat16, device=dev),
+                     y=torch.empty((0, H), dtype=torch.bfloat16, device=dev))
+        return out, inter
+
+    def _empty_backward(self, inter: dict) -> dict:
+        """Gradients of an empty batch: empty dx / dlogits / dtopk_w and zero
+        weight gradients, with the keys ``backward_from`` returns."""
+        dev, H, I = inter["x"].device, self.hidden, self.intermediate
+        E, K = self.num_experts, self.top_k
+        f32 = dict(dtype=torch.float32, device=dev)
+        out = dict(dx=torch.empty((0, H), dtype=torch.bfloat16, device=dev),
+                   dw1=torch.zeros((E, 2 * I, H), **f32), dw2=torch.zeros((E, H, I), **f32),
+                   dtopk_w=torch.empty((0, K), **f32), dlogits=torch.empty((0, E), **f32),
+                   dyq=torch.empty((0, H), dtype=ops.FP8, device=dev),
+                   dys=torch.empty((0, H // ops.GROUP), **f32),
+                   dh=torch.empty((0, I), dtype=torch.bfloat16, device=dev),
+                   dxs=torch.empty((0, H), dtype=torch.bfloat16, device=dev))
+        if inter.get("logits_from_gate"):
+            out["dw_gate"] = torch.zeros((H, E), **f32)
+        return out
+
     @torch.no_grad()
     def backward_from(self, inter: dict, dout: torch.Tensor) -> dict:
         """Backward of one forward call given its intermediates
@@ -180,6 +222,8 @@ class SimpleMoE(nn.Module):
         gating linear's contribution and dw_gate [H,E] f32 is returned.
         Every expert stage is a HIP kernel; the gating linear's two small
         fp32 matmuls are library GEMMs.  Nothing synchronises with the host."""
+        if inter["x"].shape[0] == 0:
+            return self._empty_backward(inter)
         w1tq, w1ts, w2tq, w2ts = self.fp8_weights_t()
         off, inv = inter["offsets"], inter["inv_map"]
         K = self.top_k

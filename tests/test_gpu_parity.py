@@ -616,3 +616,32 @@ def test_simple_moe_config1_end_to_end(dev):
     # downstream of fc1 the fp8 requant may flip an ulp where c1 differs in
     # its last bf16 bit; the layer output is held to the GEMM tolerance
     gemm_close(f(np_u16(out)), f(r["out"]), "layer out")
+
+
+def test_simple_moe_empty_batch(dev):
+    """T = 0 tokens: the layer returns [0, H] without launching a kernel (the
+    C ABI refuses T = 0), under autograd the weight gradients are zeros, and
+    a normal batch right after still matches the no-autograd forward."""
+    say("SimpleMoE empty batch")
+    H, I, E, K = 256, 256, 8, 2
+    m = smoe.SimpleMoE(H, I, E, K, device=dev)
+    m.reset_parameters(torch.Generator(device=dev).manual_seed(3))
+    x0 = torch.empty((0, H), dtype=torch.bfloat16, device=dev)
+    with torch.no_grad():
+        out = m(x0)
+    assert out.shape == (0, H) and out.dtype == torch.bfloat16
+    out, st = m(x0, return_intermediates=True)
+    assert out.shape == (0, H) and st["offsets"].shape == (E + 1,)
+    assert int(st["offsets"].abs().sum()) == 0 and st["xq"].shape == (0, H)
+    g = m.backward_from(st, torch.empty((0, H), dtype=torch.bfloat16, device=dev))
+    assert g["dx"].shape == (0, H) and g["dlogits"].shape == (0, E)
+    assert not g["dw1"].any() and not g["dw2"].any() and not g["dw_gate"].any()
+    xg = x0.clone().requires_grad_(True)
+    m(xg).float().sum().backward()
+    assert xg.grad.shape == (0, H)
+    assert not m.w1.grad.any() and not m.w2.grad.any() and not m.w_gate.grad.any()
+    x = W.tokens(64, H).to(dev)
+    with torch.no_grad():
+        ref = m(x)
+    again = m(x)
+    assert torch.equal(ref.view(torch.int16), again.detach().view(torch.int16))
