@@ -102,8 +102,9 @@ def test_router_extremes(dev, E, K, bias):
     hundreds of nats (probabilities that underflow to 0 or sit below 2^-100,
     where the quotient is formed by the IEEE division), integer ties in
     logits and bias, K up to E (lanes that exhaust their candidate slots and
-    rescan), and one all-NaN row (ids 0..K-1 and NaN weights, as the
-    oracle's stable argsort gives)."""
+    rescan), rows made NaN by a NaN, a +inf or all -inf logits (ids 0..K-1
+    and NaN weights, as the oracle's stable argsort gives) and a row with
+    one -inf logit."""
     say("router extremes", E, K, bias)
     rng = np.random.default_rng(E * 100 + K)
     T = 256
@@ -113,6 +114,10 @@ def test_router_extremes(dev, E, K, bias):
     lg[128:160] = -1e30                                         # one expert per row survives
     lg[128:160, 0] = 0.0
     lg[200] = np.nan
+    lg[201, E // 3] = np.nan                                    # one NaN: the whole row is NaN
+    lg[202, E // 2] = np.inf                                    # +inf: inf - inf, the row is NaN
+    lg[203] = -np.inf                                           # all -inf: NaN row
+    lg[204, E - 1] = -np.inf                                    # one -inf: probability 0
     b = None
     if bias:
         b = rng.integers(-1, 2, E).astype(np.float32) * np.float32(0.25)
