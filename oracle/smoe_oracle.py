@@ -14,7 +14,10 @@ and is binding for the kernels too:
      (score desc, expert id asc); w = probs[sel] / sum(probs[sel]).
   C2 sort:   pair p = t*K + k; stable counting sort by expert id.
   C3 quant:  per 1x128 group: amax = max|x|, s = amax/448 (s = 1 if amax == 0),
-     q = e4m3_rne(clamp(x/s, +-448)); s is stored.
+     q = e4m3_rne(clamp(x/s, +-448)); s is stored.  The rule is for finite
+     inputs: the notes define no bytes for a group holding NaN or +-inf, and
+     neither does this oracle (the kernels compute through such a group
+     without faulting, its bytes and scale are unspecified).
   C4 weights: C3 over each 128x128 block of W[e] stored [N, K].
   C5 GEMM:   c[r,n] = sum_kb as[r,kb]*bs[e,n/128,kb]*sum_k a[r,k]*b[e,n,k].
   C6 SwiGLU: h = silu(g)*u in fp32, g = c1[:, :I], u = c1[:, I:]; C3 on h.
