@@ -357,6 +357,45 @@ def test_permute_quant_zero_and_saturating_groups(dev):
     assert (rs[0] == 1.0).all()
 
 
+def test_non_finite_groups_stay_local(dev):
+    """A 128-wide group holding a NaN or +-inf has unspecified bytes (the
+    quantisation rule is for finite inputs), but the kernels run through it
+    and every finite group, in the same row or elsewhere, keeps its exact
+    bytes and scale: permute_quant, row quantisation and the SwiGLU
+    requantisation."""
+    say("non-finite groups")
+    rng = np.random.default_rng(21)
+    T, H, K = 64, 1024, 2
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    x[3, 5], x[7, 300], x[9, 1000], x[11, :128] = np.nan, np.inf, -np.inf, np.nan
+    xb = O.f32_to_bf16(x)
+    bad = ~np.isfinite(O.bf16_to_f32(xb)).reshape(T, H // 128, 128).all(axis=2)  # [T, groups]
+    idx = np.stack([rng.permutation(8)[:K] for _ in range(T)]).astype(np.int32)
+    rm, im, _, _ = O.route_sort(idx, 8)
+    xq, xs = ops.permute_quant_rows(to_bf16(xb, dev), torch.from_numpy(im).to(dev), K)
+    xf = np.where(np.repeat(bad, 128, axis=1), np.float32(0), O.bf16_to_f32(xb))
+    rq, rs = O.permute_quant(O.f32_to_bf16(xf), im, K)
+    ok = ~bad[rm // K]                                   # [R, groups] of finite groups
+    gq = np_u8(xq).reshape(-1, H // 128, 128)
+    assert np.array_equal(gq[ok], rq.reshape(-1, H // 128, 128)[ok])
+    assert np.array_equal(xs.cpu().numpy()[ok], rs[ok])
+    q, s = ops.quant_rows(to_bf16(xb, dev))
+    rq2, rs2 = O.quant_1x128(xf)
+    assert np.array_equal(np_u8(q).reshape(T, -1, 128)[~bad], rq2.reshape(T, -1, 128)[~bad])
+    assert np.array_equal(s.cpu().numpy()[~bad], rs2[~bad])
+    # SwiGLU: c1 = [g | u] with non-finite values in a few g and u groups
+    c1 = rng.standard_normal((T, 2 * H)).astype(np.float32)
+    c1[2, 7], c1[4, H + 200], c1[6, 600] = np.nan, np.inf, -np.inf
+    cb = O.f32_to_bf16(c1)
+    hq, hs = ops.swiglu_quant(to_bf16(cb, dev))
+    cf = O.bf16_to_f32(cb)
+    hbad = ~(np.isfinite(cf[:, :H]) & np.isfinite(cf[:, H:])).reshape(T, H // 128, 128).all(axis=2)
+    cf = np.where(np.repeat(np.concatenate([hbad, hbad], axis=1), 128, axis=1), np.float32(0), cf)
+    rhq, rhs = O.swiglu_quant(O.f32_to_bf16(cf))
+    assert np.array_equal(np_u8(hq).reshape(T, -1, 128)[~hbad], rhq.reshape(T, -1, 128)[~hbad])
+    assert np.array_equal(hs.cpu().numpy()[~hbad], rhs[~hbad])
+
+
 def test_permute_quant_config2_full(dev):
     """Benchmark config 2 at full size (T=16384, H=7168, E=256, top-8, bias,
     outliers): ids, maps, counts, fp8 bytes and scales all bit-exact."""
