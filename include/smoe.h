@@ -229,6 +229,44 @@ int smoe_grouped_gemm_fp8_swiglu(const uint8_t* a, const float* as, const uint8_
                                  int Kdim, uint8_t* hq, float* hs, uint16_t* c1, void* stream);
 
 /*
+ * Weights packed for the register-loaded grouped GEMM: wq [E,N,Kdim] u8 (the
+ * output of smoe_quantize_weight_blockwise) -> wp [E,N,Kdim] bytes in MFMA
+ * fragment order: [E][N/16][Kdim/128][2][64][16 B], where half h, lane l holds
+ * row 16*nb + l%16 at K offsets 128*kb + 64*h + 16*(l/16) .. +16.  The scales
+ * are unchanged.  Requires N % 128 == 0 and Kdim % 128 == 0.
+ * Replaces the fp8 weight cache refresh that keeps each layout the kernels
+ * need (_refresh_fp8_weight_cache caching KN and NK,
+ * summary/fp8_expert_gemm_optimization.md:133-137).
+ */
+int smoe_pack_weight_fp8(const uint8_t* wq, int E, int N, int Kdim, uint8_t* wp, void* stream);
+
+/*
+ * smoe_grouped_gemm_fp8 on packed weights (smoe_pack_weight_fp8): the same
+ * c [R,N] bf16, bit for bit, from a kernel that loads each wave's weights
+ * straight into registers and keeps activation tiles three K steps ahead in
+ * LDS.  Requires Kdim % 512 == 0 and N*Kdim < 2^32 (other shapes use
+ * smoe_grouped_gemm_fp8).  Needs no workspace.
+ * Replaces fp8_grouped_gemm_forward_prequantized_w(...) on cached weights
+ * (summary/fp8_expert_gemm_optimization.md:121-131).
+ */
+int smoe_grouped_gemm_fp8_packed(const uint8_t* a, const float* as, const uint8_t* wp,
+                                 const float* ws, const int32_t* offsets, int E, int R, int N,
+                                 int Kdim, uint16_t* c, void* stream);
+
+/*
+ * smoe_grouped_gemm_fp8_swiglu on packed W1 (smoe_pack_weight_fp8 of w1
+ * [E,2I,Kdim]): the same hq, hs (and c1 when not NULL), bit for bit.
+ * Requires Kdim % 512 == 0, I % 128 == 0 and 2*I*Kdim < 2^32.
+ * Replaces the same grouped GEMM + activation pair as
+ * smoe_grouped_gemm_fp8_swiglu, on cached weights
+ * (summary/fp8_expert_gemm_optimization.md:121-131).
+ */
+int smoe_grouped_gemm_fp8_packed_swiglu(const uint8_t* a, const float* as, const uint8_t* w1p,
+                                        const float* w1s, const int32_t* offsets, int E, int R,
+                                        int I, int Kdim, uint8_t* hq, float* hs, uint16_t* c1,
+                                        void* stream);
+
+/*
  * SwiGLU + 1x128 requantisation.  c1 [R,2I] bf16 with gate columns [0,I) and
  * up columns [I,2I): h = silu(g)*u in fp32 -> hq [R,I] u8, hs [R,I/128] f32.
  * silu(g) = g / (1 + exp(-g)) with exp evaluated by the library's own

@@ -40,6 +40,10 @@ SIGNATURES = {
                                       c_size_t, P]),
     "smoe_grouped_gemm_fp8_swiglu": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int, P, P,
                                              P, P]),
+    "smoe_pack_weight_fp8": (c_int, [P, c_int, c_int, c_int, P, P]),
+    "smoe_grouped_gemm_fp8_packed": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int, P, P]),
+    "smoe_grouped_gemm_fp8_packed_swiglu": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int,
+                                                    P, P, P, P]),
     "smoe_swiglu_quant": (c_int, [P, c_int, c_int, P, P, P]),
     "smoe_swiglu_quant_h": (c_int, [P, c_int, c_int, P, P, P, P]),
     "smoe_unpermute_combine": (c_int, [P, P, P, c_int, c_int, c_int, P, P]),

@@ -20,7 +20,7 @@ LIB = os.path.join(PKG, "libsmoe.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 SOURCES = ["smoe_api.cpp", "smoe_route.hip", "smoe_quant.hip", "smoe_gemm.hip",
-           "smoe_gemm_wgrad.hip", "smoe_combine.hip", "smoe_backward.hip",
+           "smoe_gemm_wgrad.hip", "smoe_gemm_packed.hip", "smoe_combine.hip", "smoe_backward.hip",
            "smoe_probe.hip"]
 
 HIP_FLAGS = [

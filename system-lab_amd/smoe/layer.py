@@ -57,7 +57,10 @@ class SimpleMoE(nn.Module):
     is fc2.  ``w_gate`` [H, E] is the router's gating linear.
     Weights are quantised to fp8 with 128x128 block scales on first use; the
     cache is keyed on the parameters' storage and version counters, so an
-    in-place update (an optimizer step) re-quantises on the next call.
+    in-place update (an optimizer step) re-quantises on the next call.  Where
+    a GEMM's K is a multiple of 512 its weights are also cached packed in MFMA
+    fragment order for the register-loaded kernel (``ops.pack_weight_fp8``;
+    the same bytes out), which adds the packed copy's E*N*K bytes.
 
     Under autograd (grad mode on and an input or parameter requiring grad),
     ``forward`` records one graph node whose backward runs the fp8 backward
@@ -79,6 +82,8 @@ class SimpleMoE(nn.Module):
         self._fp8 = None
         self._fp8_key = None
         self._fp8_t = None
+        self._gemm = None
+        self._gemm_t = None
 
     @torch.no_grad()
     def reset_parameters(self, generator: torch.Generator | None = None, std: float = 0.02):
@@ -96,7 +101,17 @@ class SimpleMoE(nn.Module):
         self._fp8 = (w1q, w1s, w2q, w2s)
         self._fp8_key = self._weights_key()
         self._fp8_t = None
+        self._gemm = (self._for_gemm(w1q), w1s, self._for_gemm(w2q), w2s)
+        self._gemm_t = None
         return self._fp8
+
+    @staticmethod
+    def _for_gemm(wq):
+        """The form the GEMM ops take: packed in MFMA fragment order where the
+        register-loaded kernel covers the shape (K a multiple of 512; the same
+        bytes out, faster), else the plain [E, N, K] weights."""
+        E, N, Kd = wq.shape
+        return ops.pack_weight_fp8(wq) if ops.packed_gemm_ok(N, Kd) else wq
 
     def fp8_weights(self):
         """(w1q, w1s, w2q, w2s), re-quantised when w1 or w2 changed since the
@@ -112,6 +127,20 @@ class SimpleMoE(nn.Module):
         if self._fp8_t is None:
             self._fp8_t = ops.transpose_blockwise(w1q, w1s) + ops.transpose_blockwise(w2q, w2s)
         return self._fp8_t
+
+    def gemm_weights(self):
+        """(w1, w1s, w2, w2s) as the forward GEMMs take them: fp8_weights()
+        with w1 / w2 packed where the packed kernel covers their shape."""
+        self.fp8_weights()
+        return self._gemm
+
+    def gemm_weights_t(self):
+        """The dgrad weights of fp8_weights_t() in the form the GEMM ops take
+        (packed where covered), cached with them."""
+        w1tq, w1ts, w2tq, w2ts = self.fp8_weights_t()
+        if self._gemm_t is None:
+            self._gemm_t = (self._for_gemm(w1tq), w1ts, self._for_gemm(w2tq), w2ts)
+        return self._gemm_t
 
     def forward(self, x: torch.Tensor, logits: torch.Tensor | None = None,
                 return_intermediates: bool = False):
@@ -142,7 +171,7 @@ class SimpleMoE(nn.Module):
         logits = logits.detach().float().contiguous()
         if x.shape[0] == 0:
             return self._empty_forward(x, logits, save)
-        w1q, w1s, w2q, w2s = self.fp8_weights()
+        w1q, w1s, w2q, w2s = self.gemm_weights()
         # router and expert sort in three launches (the sort's histogram is
         # counted inside the router launch)
         idx, w, row_map, inv_map, counts, offsets = ops.route_topk_sort(logits, self.top_k,
@@ -224,7 +253,7 @@ class SimpleMoE(nn.Module):
         fp32 matmuls are library GEMMs.  Nothing synchronises with the host."""
         if inter["x"].shape[0] == 0:
             return self._empty_backward(inter)
-        w1tq, w1ts, w2tq, w2ts = self.fp8_weights_t()
+        w1tq, w1ts, w2tq, w2ts = self.gemm_weights_t()
         off, inv = inter["offsets"], inter["inv_map"]
         K = self.top_k
         # The weight gradients are off the dx critical path.  They run on a

@@ -221,20 +221,74 @@ def quantize_weight_blockwise(w: torch.Tensor):
 
 
 # -------------------------------------------------------------------- GEMM
+class PackedWeight:
+    """fp8 expert weights rearranged in MFMA fragment order for the
+    register-loaded grouped GEMM (``pack_weight_fp8``).  ``data`` holds the
+    same E*N*K bytes as the [E, N, K] weights, in the packed order; the
+    128x128 scales are unchanged and passed alongside as before.  The GEMM ops
+    take a PackedWeight wherever they take wq and then run the packed kernel
+    (bit-identical output)."""
+
+    __slots__ = ("data",)
+
+    def __init__(self, data: torch.Tensor):
+        self.data = data
+
+    @property
+    def shape(self):
+        return self.data.shape
+
+    @property
+    def device(self):
+        return self.data.device
+
+
+def packed_gemm_ok(N: int, Kd: int) -> bool:
+    """Whether the packed GEMM covers a weight of N rows and K = Kd: it needs
+    K a multiple of 512 and N*K < 2^32 (other weights use the plain kernel)."""
+    return Kd % (4 * GROUP) == 0 and N % GROUP == 0 and N * Kd < (1 << 32)
+
+
+def pack_weight_fp8(wq: torch.Tensor) -> PackedWeight:
+    """[E, N, K] fp8 weights -> PackedWeight (smoe_pack_weight_fp8).  Raises
+    unless ``packed_gemm_ok(N, K)``."""
+    _check(wq, "wq", (FP8, torch.uint8), 3)
+    E, N, Kd = wq.shape
+    if not packed_gemm_ok(N, Kd):
+        raise ValueError(f"packed weights need K % 512 == 0, N % 128 == 0 and N*K < 2^32 "
+                         f"(N={N}, K={Kd})")
+    wp = torch.empty((E, N, Kd), dtype=torch.uint8, device=wq.device)
+    _C.call("smoe_pack_weight_fp8", _ptr(_bytes(wq)), E, N, Kd, _ptr(wp), _stream())
+    return PackedWeight(wp)
+
+
+def _weight(wq, name):
+    """(tensor, packed?) of a GEMM weight argument."""
+    if isinstance(wq, PackedWeight):
+        _check(wq.data, name, (torch.uint8,), 3)
+        return wq.data, True
+    _check(wq, name, (FP8, torch.uint8))
+    return wq, False
+
+
 def grouped_gemm_fp8(xq: torch.Tensor, xs: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor,
                      offsets: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """Dropless fp8 grouped GEMM: rows [offsets[e], offsets[e+1]) of xq times
     W[e]^T with 1x128 / 128x128 scales -> bf16 [R, N].  Rows outside
-    [offsets[0], offsets[E]) are not written."""
-    for t, n in ((xq, "xq"), (wq, "wq")):
-        _check(t, n, (FP8, torch.uint8))
+    [offsets[0], offsets[E]) are not written.  ``wq`` is [E, N, K] fp8, or a
+    PackedWeight (``pack_weight_fp8``) for the register-loaded kernel, which
+    gives the same bytes."""
+    _check(xq, "xq", (FP8, torch.uint8))
+    wt, packed = _weight(wq, "wq")
     _check(xs, "xs", (torch.float32,), 2)
     _check(ws, "ws", (torch.float32,), 3)
     _check(offsets, "offsets", (torch.int32,), 1)
     R, Kd = xq.shape
-    E, N, Kw = wq.shape
+    E, N, Kw = wt.shape
     if Kw != Kd:
         raise ValueError(f"K mismatch: xq has {Kd}, wq has {Kw}")
+    if packed and not packed_gemm_ok(N, Kd):
+        raise ValueError(f"packed weights need K % 512 == 0 and N*K < 2^32 (N={N}, K={Kd})")
     if offsets.numel() != E + 1:
         raise ValueError("offsets must have E+1 entries")
     if xs.shape != (R, Kd // GROUP) or ws.shape != (E, N // GROUP, Kd // GROUP):
@@ -245,8 +299,12 @@ def grouped_gemm_fp8(xq: torch.Tensor, xs: torch.Tensor, wq: torch.Tensor, ws: t
         _check(out, "out", (torch.bfloat16,), 2)
         if out.shape != (R, N):
             raise ValueError("out must be [R, N]")
-    _C.call("smoe_grouped_gemm_fp8", _ptr(_bytes(xq)), _ptr(xs), _ptr(_bytes(wq)), _ptr(ws),
-            _ptr(offsets), E, R, N, Kd, _ptr(out), None, 0, _stream())
+    if packed:
+        _C.call("smoe_grouped_gemm_fp8_packed", _ptr(_bytes(xq)), _ptr(xs), _ptr(wt), _ptr(ws),
+                _ptr(offsets), E, R, N, Kd, _ptr(out), _stream())
+    else:
+        _C.call("smoe_grouped_gemm_fp8", _ptr(_bytes(xq)), _ptr(xs), _ptr(_bytes(wt)), _ptr(ws),
+                _ptr(offsets), E, R, N, Kd, _ptr(out), None, 0, _stream())
     return out
 
 
@@ -255,16 +313,19 @@ def grouped_gemm_fp8_swiglu(xq: torch.Tensor, xs: torch.Tensor, w1q: torch.Tenso
     """fc1 GEMM with SwiGLU + 1x128 requantisation fused into the epilogue.
     Same bytes as ``swiglu_quant(grouped_gemm_fp8(xq, xs, w1q, w1s, offsets))``;
     returns (hq [R,I] fp8, hs [R,I/128] f32), plus c1 [R,2I] bf16 when
-    ``save_c1``.  Rows outside [offsets[0], offsets[E]) are not written."""
-    for t, n in ((xq, "xq"), (w1q, "w1q")):
-        _check(t, n, (FP8, torch.uint8))
+    ``save_c1``.  Rows outside [offsets[0], offsets[E]) are not written.
+    ``w1q`` may be a PackedWeight (same bytes out)."""
+    _check(xq, "xq", (FP8, torch.uint8))
+    wt, packed = _weight(w1q, "w1q")
     _check(xs, "xs", (torch.float32,), 2)
     _check(w1s, "w1s", (torch.float32,), 3)
     _check(offsets, "offsets", (torch.int32,), 1)
     R, Kd = xq.shape
-    E, N, Kw = w1q.shape
+    E, N, Kw = wt.shape
     if Kw != Kd:
         raise ValueError(f"K mismatch: xq has {Kd}, w1q has {Kw}")
+    if packed and not packed_gemm_ok(N, Kd):
+        raise ValueError(f"packed weights need K % 512 == 0 and N*K < 2^32 (N={N}, K={Kd})")
     if N % (2 * GROUP):
         raise ValueError("w1q rows must be gate | up halves of a multiple of 128 each")
     if offsets.numel() != E + 1:
@@ -275,8 +336,9 @@ def grouped_gemm_fp8_swiglu(xq: torch.Tensor, xs: torch.Tensor, w1q: torch.Tenso
     hq = torch.empty((R, I), dtype=FP8, device=xq.device)
     hs = torch.empty((R, I // GROUP), dtype=torch.float32, device=xq.device)
     c1 = torch.empty((R, N), dtype=torch.bfloat16, device=xq.device) if save_c1 else None
-    _C.call("smoe_grouped_gemm_fp8_swiglu", _ptr(_bytes(xq)), _ptr(xs), _ptr(_bytes(w1q)),
-            _ptr(w1s), _ptr(offsets), E, R, I, Kd, _ptr(hq), _ptr(hs), _ptr(c1), _stream())
+    fn = "smoe_grouped_gemm_fp8_packed_swiglu" if packed else "smoe_grouped_gemm_fp8_swiglu"
+    _C.call(fn, _ptr(_bytes(xq)), _ptr(xs), _ptr(wt if packed else _bytes(wt)), _ptr(w1s),
+            _ptr(offsets), E, R, I, Kd, _ptr(hq), _ptr(hs), _ptr(c1), _stream())
     return (hq, hs, c1) if save_c1 else (hq, hs)
 
 

@@ -1,0 +1,147 @@
+"""Packed-weight grouped GEMM (smoe_pack_weight_fp8,
+smoe_grouped_gemm_fp8_packed[_swiglu]): the packed layout byte by byte, and
+the packed kernels held bit-identical to the plain ones (which the oracle
+pins: tests/test_gpu_parity.py) over ragged, empty and skewed experts, tile
+edges and the config-4 shape."""
+import numpy as np
+import pytest
+import torch
+
+import smoe
+from smoe import _C, ops
+from smoe import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print("[packed]", *a, flush=True)
+
+
+def _operands(dev, counts, N, K, extra_rows=0, seed=0):
+    off = W.offsets_from_counts(counts, dev)
+    R = int(sum(counts)) + extra_rows
+    xq, xs = ops.permute_quant_rows(W.tokens(R, K, device=dev, seed=30 + seed),
+                                    torch.arange(R, dtype=torch.int32, device=dev), 1)
+    wq, ws = ops.quantize_weight_blockwise(W.weights(len(counts), N, K, device=dev, seed=40 + seed))
+    return off, xq, xs, wq, ws
+
+
+def test_pack_layout(dev):
+    """wp[e][nb][kb][h][l] = wq[e, 16nb + l%16, 128kb + 64h + 16(l/16) .. +16]."""
+    say("layout")
+    E, N, K = 2, 256, 512
+    g = torch.Generator(device=dev).manual_seed(9)
+    wq = torch.randint(0, 256, (E, N, K), dtype=torch.uint8, device=dev, generator=g)
+    wp = ops.pack_weight_fp8(wq).data.cpu().numpy().reshape(E, N // 16, K // 128, 2, 64, 16)
+    w = wq.cpu().numpy()
+    nb, kb, h, ln = np.meshgrid(np.arange(N // 16), np.arange(K // 128), np.arange(2),
+                                np.arange(64), indexing="ij")
+    rows = nb * 16 + ln % 16
+    cols = kb * 128 + h * 64 + (ln // 16) * 16
+    for e in range(E):
+        exp = np.stack([w[e][rows, cols + b] for b in range(16)], axis=-1)
+        assert np.array_equal(wp[e], exp)
+
+
+@pytest.mark.parametrize("counts,N,K,extra", [
+    ([300, 0, 513, 1], 512, 512, 0),
+    ([256, 256, 256], 384, 1024, 37),       # N % 256 == 128, rows past offsets[E]
+    ([1000], 256, 2048, 0),
+    ([0, 700, 0, 5, 1300, 0, 256, 1], 1024, 4096, 11),
+    ([17, 600], 2048, 7168, 0),
+])
+def test_packed_gemm_bit_identical(dev, counts, N, K, extra):
+    say("gemm", counts, N, K, extra)
+    off, xq, xs, wq, ws = _operands(dev, counts, N, K, extra)
+    R = xq.shape[0]
+    ref = torch.full((R, N), 7.0, dtype=torch.bfloat16, device=dev)   # rows past offsets[E] keep 7
+    got = ref.clone()
+    ops.grouped_gemm_fp8(xq, xs, wq, ws, off, out=ref)
+    ops.grouped_gemm_fp8(xq, xs, ops.pack_weight_fp8(wq), ws, off, out=got)
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    if extra:
+        assert (got[-extra:].float() == 7.0).all()
+
+
+@pytest.mark.parametrize("counts,I,K", [([200, 0, 333], 256, 1024), ([513, 64], 768, 2048)])
+def test_packed_swiglu_bit_identical(dev, counts, I, K):
+    say("swiglu", counts, I, K)
+    off, xq, xs, w1q, w1s = _operands(dev, counts, 2 * I, K, seed=3)
+    w1p = ops.pack_weight_fp8(w1q)
+    hq, hs, c1 = ops.grouped_gemm_fp8_swiglu(xq, xs, w1q, w1s, off, save_c1=True)
+    phq, phs, pc1 = ops.grouped_gemm_fp8_swiglu(xq, xs, w1p, w1s, off, save_c1=True)
+    assert torch.equal(phq.view(torch.uint8), hq.view(torch.uint8))
+    assert torch.equal(phs, hs)
+    assert torch.equal(pc1.view(torch.int16), c1.view(torch.int16))
+    qhq, qhs = ops.grouped_gemm_fp8_swiglu(xq, xs, w1p, w1s, off)
+    assert torch.equal(qhq.view(torch.uint8), hq.view(torch.uint8)) and torch.equal(qhs, hs)
+
+
+def test_packed_config4_full(dev):
+    """The config-4 GEMMs (R=65536 rows over 32 Zipf-loaded experts, fc1
+    N=4096 K=7168 with and without the SwiGLU epilogue, fc2 N=7168 K=2048)."""
+    say("config 4")
+    c = W.CONFIGS["dsv3"]
+    off = W.offsets_from_counts(W.zipf_counts(), dev)
+    R = c.T
+    inv = torch.arange(R, dtype=torch.int32, device=dev)
+    xq, xs = ops.permute_quant_rows(W.tokens(R, c.H, device=dev), inv, 1)
+    w1q, w1s = ops.quantize_weight_blockwise(W.weights(c.E, 2 * c.I, c.H, device=dev))
+    w1p = ops.pack_weight_fp8(w1q)
+    a = ops.grouped_gemm_fp8(xq, xs, w1q, w1s, off)
+    b = ops.grouped_gemm_fp8(xq, xs, w1p, w1s, off)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    hq, hs = ops.grouped_gemm_fp8_swiglu(xq, xs, w1q, w1s, off)
+    phq, phs = ops.grouped_gemm_fp8_swiglu(xq, xs, w1p, w1s, off)
+    assert torch.equal(phq.view(torch.uint8), hq.view(torch.uint8)) and torch.equal(phs, hs)
+    del a, b, xq, xs, w1q, w1p
+    w2q, w2s = ops.quantize_weight_blockwise(W.weights(c.E, c.H, c.I, device=dev, seed=13))
+    a = ops.grouped_gemm_fp8(hq, hs, w2q, w2s, off)
+    b = ops.grouped_gemm_fp8(hq, hs, ops.pack_weight_fp8(w2q), w2s, off)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def test_packed_validation(dev):
+    say("validation")
+    off, xq, xs, wq, ws = _operands(dev, [100, 50], 256, 640)
+    with pytest.raises(ValueError):
+        ops.pack_weight_fp8(wq)                       # K = 640 is not a multiple of 512
+    assert not ops.packed_gemm_ok(256, 640) and ops.packed_gemm_ok(256, 512)
+    st = torch.cuda.current_stream().cuda_stream
+    c = torch.empty((150, 256), dtype=torch.bfloat16, device=dev)
+    rc = _C.lib().smoe_grouped_gemm_fp8_packed(xq.data_ptr(), xs.data_ptr(), wq.data_ptr(),
+                                               ws.data_ptr(), off.data_ptr(), 2, 150, 256, 640,
+                                               c.data_ptr(), st)
+    assert rc == -3                                   # SMOE_EINVAL_ALIGN128
+    off, xq, xs, wq, ws = _operands(dev, [100, 50], 256, 512)
+    wp = ops.pack_weight_fp8(wq)
+    xq2, xs2 = ops.permute_quant_rows(W.tokens(150, 1024, device=dev),
+                                      torch.arange(150, dtype=torch.int32, device=dev), 1)
+    with pytest.raises(ValueError):
+        ops.grouped_gemm_fp8(xq2, xs2, wp, ws, off)   # K mismatch
+
+
+def test_simple_moe_uses_packed_weights(dev):
+    """SimpleMoE packs a GEMM's weights exactly when the packed kernel covers
+    them, and its forward matches the plain kernels' composition."""
+    say("SimpleMoE packed")
+    H, I, E, K, T = 512, 256, 4, 2, 300
+    m = smoe.SimpleMoE(H, I, E, K, device=dev)
+    m.reset_parameters(torch.Generator(device=dev).manual_seed(2))
+    w1g, _, w2g, _ = m.gemm_weights()
+    assert isinstance(w1g, ops.PackedWeight)          # K = H = 512
+    assert not isinstance(w2g, ops.PackedWeight)      # K = I = 256
+    w1t, _, w2t, _ = m.gemm_weights_t()
+    assert isinstance(w1t, ops.PackedWeight)          # dgrad fc1: K = 2I = 512
+    assert isinstance(w2t, ops.PackedWeight)          # dgrad fc2: K = H = 512
+    x = W.tokens(T, H).to(dev)
+    lg = W.logits(T, E).to(dev)
+    with torch.no_grad():
+        out = m(x, lg)
+    w1q, w1s, w2q, w2s = m.fp8_weights()
+    idx, w, rm, im, cnt, off = ops.route_topk_sort(lg, K)
+    xq, xs = ops.permute_quant_rows(x, im, K)
+    hq, hs = ops.grouped_gemm_fp8_swiglu(xq, xs, w1q, w1s, off)
+    ref = ops.unpermute_combine(ops.grouped_gemm_fp8(hq, hs, w2q, w2s, off), im, w)
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
