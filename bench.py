@@ -209,31 +209,38 @@ def bench_gemm(dev, steps, warmup, skip_cpu=True):
     w1q, w1s = ops.quantize_weight_blockwise(W.weights(c.E, 2 * c.I, c.H, device=dev))
     w2q, w2s = ops.quantize_weight_blockwise(W.weights(c.E, c.H, c.I, device=dev, seed=13))
     torch.cuda.empty_cache()
+    # the weights as SimpleMoE caches them for these shapes (K % 512 == 0):
+    # packed in MFMA fragment order for the register-loaded kernel
+    w1p, w2p = ops.pack_weight_fp8(w1q), ops.pack_weight_fp8(w2q)
     c1 = torch.empty((R, 2 * c.I), dtype=torch.bfloat16, device=dev)
     y = torch.empty((R, c.H), dtype=torch.bfloat16, device=dev)
-    f1 = lambda: ops.grouped_gemm_fp8(xq, xs, w1q, w1s, off, out=c1)
-    f2 = lambda: ops.grouped_gemm_fp8(hq, hs, w2q, w2s, off, out=y)
     # median of per-launch event timings (MFMA-bound: no cache flush)
-    t1 = timed_median(f1, steps, warmup)
-    t2 = timed_median(f2, steps, warmup)
+    t1 = timed_median(lambda: ops.grouped_gemm_fp8(xq, xs, w1p, w1s, off, out=c1), steps, warmup)
+    t2 = timed_median(lambda: ops.grouped_gemm_fp8(hq, hs, w2p, w2s, off, out=y), steps, warmup)
+    # the plain kernel (smoe_grouped_gemm_fp8 on [E, N, K] weights, the C-ABI
+    # drop-in, which every shape can use)
+    t1u = timed_median(lambda: ops.grouped_gemm_fp8(xq, xs, w1q, w1s, off, out=c1), steps, warmup)
+    t2u = timed_median(lambda: ops.grouped_gemm_fp8(hq, hs, w2q, w2s, off, out=y), steps, warmup)
     # fc1 with SwiGLU + requant fused into the epilogue (the inference path),
     # against fc1 followed by the stand-alone SwiGLU kernel
-    fsw = lambda: ops.swiglu_quant(c1)
-    t_sw = timed_median(fsw, steps, warmup)
-    f1s = lambda: ops.grouped_gemm_fp8_swiglu(xq, xs, w1q, w1s, off)
-    t1s = timed_median(f1s, steps, warmup)
+    t_sw = timed_median(lambda: ops.swiglu_quant(c1), steps, warmup)
+    t1s = timed_median(lambda: ops.grouped_gemm_fp8_swiglu(xq, xs, w1p, w1s, off), steps, warmup)
     fl1 = 2.0 * R * (2 * c.I) * c.H
     fl2 = 2.0 * R * c.H * c.I
     tf = (fl1 + fl2) / ((t1 + t2) * 1e-3) / 1e12
+    tfu = (fl1 + fl2) / ((t1u + t2u) * 1e-3) / 1e12
     out = {"workload": "dsv3 local experts R=65536 H=7168 I=2048 E=32 zipf1.2",
+           "weights": "packed (smoe_grouped_gemm_fp8_packed)",
            "fc1_ms": round(t1, 4), "fc1_tflops": round(fl1 / (t1 * 1e-3) / 1e12, 1),
            "fc2_ms": round(t2, 4), "fc2_tflops": round(fl2 / (t2 * 1e-3) / 1e12, 1),
            "fc1_swiglu_fused_ms": round(t1s, 4), "fc1_then_swiglu_ms": round(t1 + t_sw, 4),
            "tflops": round(tf, 1), "roofline_frac": round(tf / FP8_PEAK_TFLOPS, 4),
+           "plain_fc1_ms": round(t1u, 4), "plain_fc2_ms": round(t2u, 4),
+           "plain_tflops": round(tfu, 1), "plain_roofline_frac": round(tfu / FP8_PEAK_TFLOPS, 4),
            "peak_tflops": FP8_PEAK_TFLOPS}
     if not skip_cpu:
         out["cpu_baseline"] = cpu_gemm_baseline(xq, xs, w1q, w1s, c)
-    del xq, xs, hq, hs, w1q, w1s, w2q, w2s, c1, y
+    del xq, xs, hq, hs, w1q, w1s, w2q, w2s, w1p, w2p, c1, y
     torch.cuda.empty_cache()
     return out
 
