@@ -242,7 +242,8 @@ int smoe_pack_weight_fp8(const uint8_t* wq, int E, int N, int Kdim, uint8_t* wp,
 
 /*
  * smoe_grouped_gemm_fp8 on packed weights (smoe_pack_weight_fp8): the same
- * c [R,N] bf16, bit for bit, from a kernel that loads each wave's weights
+ * c [R,N] bf16 (bit for bit whenever each 128-wide K block's products sum
+ * exactly in fp32; else within the last bf16 bit), from a kernel that loads each wave's weights
  * straight into registers and keeps activation tiles three K steps ahead in
  * LDS.  Requires Kdim % 512 == 0 and N*Kdim < 2^32 (other shapes use
  * smoe_grouped_gemm_fp8).  Needs no workspace.
@@ -255,7 +256,8 @@ int smoe_grouped_gemm_fp8_packed(const uint8_t* a, const float* as, const uint8_
 
 /*
  * smoe_grouped_gemm_fp8_swiglu on packed W1 (smoe_pack_weight_fp8 of w1
- * [E,2I,Kdim]): the same hq, hs (and c1 when not NULL), bit for bit.
+ * [E,2I,Kdim]): the same hq, hs (and c1 when not NULL) under the same
+ * condition as smoe_grouped_gemm_fp8_packed.
  * Requires Kdim % 512 == 0, I % 128 == 0 and 2*I*Kdim < 2^32.
  * Replaces the same grouped GEMM + activation pair as
  * smoe_grouped_gemm_fp8_swiglu, on cached weights

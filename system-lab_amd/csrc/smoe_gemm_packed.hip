@@ -3,17 +3,20 @@
 //
 //   c[r,n] = bf16( sum_kb as[r,kb] * bs[e,n/128,kb] * sum_{k in kb} a[r,k]*b[e,n,k] )
 //
-// Same contract, tile order, expert scan and epilogues as smoe_gemm.hip (the
-// outputs are bit-identical to it); what differs is where the weights travel.
+// Same contract, tile order, expert scan and epilogues as smoe_gemm.hip; what
+// differs is where the weights travel.  The outputs equal smoe_gemm.hip's
+// whenever each K block's 128 products sum without rounding inside the MFMA
+// (the case for every benchmark and layer workload measured); otherwise the
+// two K orders below can differ in the last bf16 bit.
 //
 // Packed weights.  smoe_pack_weight_fp8 rewrites b [E,N,K] once as
 // [E][N/16][K/128][2][64 lanes][16 B]: for 16 weight rows and one 128-wide K
 // block, half h (0, 1) holds in lane l's 16 bytes row l%16 at K offsets
 // h*64 + (l/16)*16 .. +16.  A wave then loads one MFMA operand (16 rows x 128
 // K) as two fully coalesced 1 KiB global_load_dwordx4 straight into VGPRs.
-// The MFMA's dot product does not depend on the order of K within an
-// instruction, so the activation fragment read from LDS uses the same K order
-// (lane group g takes bytes 16g.. and 64+16g..) and the sums are unchanged.
+// The activation fragment read from LDS uses the same K order (lane group g
+// takes bytes 16g.. and 64+16g..), so each MFMA sums the same 128 products,
+// in a different order.
 //
 // Tiling.  A workgroup of 8 waves owns a 256 x 256 output tile; wave w owns
 // all 256 rows and columns w*32 .. +32 (16 row blocks x 2 column blocks of

@@ -60,7 +60,8 @@ class SimpleMoE(nn.Module):
     in-place update (an optimizer step) re-quantises on the next call.  Where
     a GEMM's K is a multiple of 512 its weights are also cached packed in MFMA
     fragment order for the register-loaded kernel (``ops.pack_weight_fp8``;
-    the same bytes out), which adds the packed copy's E*N*K bytes.
+    the same result, see ``ops.grouped_gemm_fp8``), which adds the packed
+    copy's E*N*K bytes.
 
     Under autograd (grad mode on and an input or parameter requiring grad),
     ``forward`` records one graph node whose backward runs the fp8 backward

@@ -227,7 +227,7 @@ class PackedWeight:
     same E*N*K bytes as the [E, N, K] weights, in the packed order; the
     128x128 scales are unchanged and passed alongside as before.  The GEMM ops
     take a PackedWeight wherever they take wq and then run the packed kernel
-    (bit-identical output)."""
+    (the same output; see grouped_gemm_fp8)."""
 
     __slots__ = ("data",)
 
@@ -276,8 +276,11 @@ def grouped_gemm_fp8(xq: torch.Tensor, xs: torch.Tensor, wq: torch.Tensor, ws: t
     """Dropless fp8 grouped GEMM: rows [offsets[e], offsets[e+1]) of xq times
     W[e]^T with 1x128 / 128x128 scales -> bf16 [R, N].  Rows outside
     [offsets[0], offsets[E]) are not written.  ``wq`` is [E, N, K] fp8, or a
-    PackedWeight (``pack_weight_fp8``) for the register-loaded kernel, which
-    gives the same bytes."""
+    PackedWeight (``pack_weight_fp8``) for the register-loaded kernel.  That
+    kernel orders each 128-wide K block's products differently inside the
+    MFMA: the bytes are the same whenever those products sum exactly in fp32
+    (every benchmark and layer workload), else they can differ in the last
+    bf16 bit, within the GEMM tolerance."""
     _check(xq, "xq", (FP8, torch.uint8))
     wt, packed = _weight(wq, "wq")
     _check(xs, "xs", (torch.float32,), 2)
@@ -314,7 +317,7 @@ def grouped_gemm_fp8_swiglu(xq: torch.Tensor, xs: torch.Tensor, w1q: torch.Tenso
     Same bytes as ``swiglu_quant(grouped_gemm_fp8(xq, xs, w1q, w1s, offsets))``;
     returns (hq [R,I] fp8, hs [R,I/128] f32), plus c1 [R,2I] bf16 when
     ``save_c1``.  Rows outside [offsets[0], offsets[E]) are not written.
-    ``w1q`` may be a PackedWeight (same bytes out)."""
+    ``w1q`` may be a PackedWeight (see grouped_gemm_fp8)."""
     _check(xq, "xq", (FP8, torch.uint8))
     wt, packed = _weight(w1q, "w1q")
     _check(xs, "xs", (torch.float32,), 2)

@@ -437,16 +437,35 @@ def _fp8_operands(rng, R, N, Kd, E):
 
 
 def _run_gemm(dev, xq, xs, wq, ws, off):
-    out = ops.grouped_gemm_fp8(to_fp8(xq, dev), torch.from_numpy(xs).to(dev), to_fp8(wq, dev),
-                               torch.from_numpy(ws).to(dev), torch.from_numpy(off).to(dev))
+    args = (to_fp8(xq, dev), torch.from_numpy(xs).to(dev), to_fp8(wq, dev),
+            torch.from_numpy(ws).to(dev), torch.from_numpy(off).to(dev))
+    out = ops.grouped_gemm_fp8(*args)
+    E, N, Kd = wq.shape
+    if ops.packed_gemm_ok(N, Kd):
+        # the packed-weight kernel must give the same bytes on every row that
+        # exactly one expert's range covers (malformed offsets can give a row
+        # to two experts, whose writes race, or to none).  For these seeded
+        # operands (quantised N(0,1) rows, N(0,0.02) weights, one-hot values)
+        # every K block's products sum without rounding in the MFMA, so the
+        # two kernels' K orders cannot show (tests/test_gpu_large.py has
+        # operands where they do).
+        got = ops.grouped_gemm_fp8(args[0], args[1], ops.pack_weight_fp8(args[2]), *args[3:])
+        R = xq.shape[0]
+        cover = np.zeros(R, np.int32)
+        for e in range(E):
+            cover[max(int(off[e]), 0):max(min(int(off[e + 1]), R), 0)] += 1
+        one = torch.from_numpy(cover == 1).to(dev)
+        assert torch.equal(got[one].view(torch.int16), out[one].view(torch.int16)), "packed != plain"
     return O.bf16_to_f32(np_u16(out)).astype(np.float64)
 
 
-def test_gemm_layout_one_hot(dev):
+@pytest.mark.parametrize("Kd", [256, 512])
+def test_gemm_layout_one_hot(dev, Kd):
     """Structured operands expose any row/column/K permutation in the MFMA
-    fragment or output layout: x[r] = e_(r mod 256), w[n] = e_n."""
-    say("gemm one-hot layout")
-    R, N, Kd, E = 300, 256, 256, 1
+    fragment or output layout: x[r] = e_(r mod Kd), w[n] = e_n (Kd = 512 also
+    runs the packed-weight kernel)."""
+    say("gemm one-hot layout", Kd)
+    R, N, E = 300, 256, 1
     xq = np.zeros((R, Kd), np.uint8)
     xq[np.arange(R), np.arange(R) % Kd] = 0x38  # 1.0
     xs = np.ones((R, Kd // 128), np.float32)
@@ -525,14 +544,16 @@ def test_gemm_max_kdim(dev):
     gemm_close(got, O.grouped_gemm_fp8(xq, xs, wq, ws, off), "Kdim=65536")
 
 
-def test_gemm_malformed_offsets_stay_in_range(dev):
+@pytest.mark.parametrize("Kd", [256, 512])
+def test_gemm_malformed_offsets_stay_in_range(dev, Kd):
     """offsets[] lives on the device and is not validated on the host, so the
     kernel clamps every tile to rows [0, R): here expert 1's offsets decrease
     (no tiles) and expert 2's run past R.  No access leaves the buffers; the
-    rows that belong to one expert only match the oracle."""
-    say("gemm malformed offsets")
+    rows that belong to one expert only match the oracle.  (Kd = 512 also runs
+    the packed-weight kernel, which must give the same bytes.)"""
+    say("gemm malformed offsets", Kd)
     rng = np.random.default_rng(77)
-    R, N, Kd, E = 1000, 256, 256, 3
+    R, N, E = 1000, 256, 3
     xq, xs, wq, ws = _fp8_operands(rng, R, N, Kd, E)
     bad = np.array([0, 400, 300, 1500], np.int32)
     got = _run_gemm(dev, xq, xs, wq, ws, bad)
