@@ -426,10 +426,11 @@ int smoe_unpermute_combine_bwd_quant(const uint16_t* dout, const uint16_t* y,
 
 /*
  * Measurement utility (no counterpart in the reference): the access pattern
- * of smoe_permute_quant without its arithmetic.  One wave per source row of
- * row_bytes bytes (a multiple of 2048, at most 16384) reads it with 128-bit
- * loads and writes half as many bytes, derived from it, to each of `fanout`
- * destination rows (scattered, each front to back) with 128-bit stores; fanout = 0
+ * of smoe_permute_quant without its arithmetic.  One or two waves per source
+ * row of row_bytes bytes (a multiple of 2048, at most 16384; two waves above
+ * 8192, as in smoe_permute_quant) read it with 128-bit loads and write half
+ * as many bytes, derived from it, to each of `fanout` destination rows
+ * (scattered, each front to back) with 128-bit stores; fanout = 0
  * only reads.  fanout = 8 moves the dispatch step's 1:4 read:write byte mix,
  * so its rate is the HBM ceiling for that mix.  dst must hold
  * rows * fanout * row_bytes / 2 bytes; sink: one device word.

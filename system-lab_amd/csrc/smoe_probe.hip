@@ -1,11 +1,13 @@
 // smoe_probe.hip — HBM traffic-mix probe (gfx950), a measurement utility.
 //
-// The access pattern of permute_quant without its arithmetic: one wave per
-// source row of row_bytes (<= 16 KiB) bytes; each lane loads 32 bytes (two
-// 128-bit loads) per 2 KiB of the row, the whole row in flight, and writes
-// one 16-byte word derived from them (their xor, standing in for the fp8
-// bytes of 32 bf16 bytes) to each of `fanout` destination rows of
-// row_bytes / 2 bytes, each row front to back, with cached 128-bit stores.  Destination row of (row t, copy
+// The access pattern of permute_quant without its arithmetic: a source row of
+// row_bytes (<= 16 KiB) bytes is split over the same number of waves as in
+// permute_quant (two for rows of more than 4 chunks of 2 KiB, else one);
+// each lane loads 32 bytes (two 128-bit loads) per 2 KiB chunk its wave
+// owns, all of them in flight, and writes one 16-byte word derived from them
+// (their xor, standing in for the fp8 bytes of 32 bf16 bytes) to each of
+// `fanout` destination rows of row_bytes / 2 bytes, its part of each row
+// front to back, with cached 128-bit stores.  Destination row of (row t, copy
 // k) is (t*fanout + k) * 0x9E3779B1 mod (rows*fanout) when rows*fanout is a
 // power of two (a scatter like the expert-sorted rows), t*fanout + k
 // otherwise.  fanout = 0 only reads.  Bytes moved: rows*row_bytes read,
@@ -19,15 +21,17 @@ typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
 constexpr int kProbeMaxC = 8;  // 2 KiB chunks per row, all in flight
 
-// The whole-row permute_quant pattern: all kC chunks of the row are loaded
-// before any store, then each destination row is written front to back.
-template <int kC>
+// The whole-row permute_quant pattern: wave j of a row's kW waves loads
+// chunks j*kC .. j*kC + kC - 1 before any store, then writes its part of each
+// destination row front to back.
+template <int kC, int kW>
 __global__ __launch_bounds__(256) void bw_probe_kernel(const uint8_t* __restrict__ src, int rows,
                                                        int row_bytes, int fanout,
                                                        uint8_t* __restrict__ dst,
                                                        uint32_t* __restrict__ sink) {
   const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const unsigned wv = blockIdx.x * 4u + (threadIdx.x >> 6);
+  const int t = (int)(wv / kW), c0 = (int)(wv % kW) * kC;
   if (t >= rows) return;
   const int out_bytes = row_bytes / 2;
   const uint32_t nrows_out = (uint32_t)rows * (uint32_t)max(fanout, 1);
@@ -36,7 +40,7 @@ __global__ __launch_bounds__(256) void bw_probe_kernel(const uint8_t* __restrict
   uint4 w[kC];
 #pragma unroll
   for (int c = 0; c < kC; ++c) {
-    const int off = min(c * 2048 + lane * 32, row_bytes - 32);
+    const int off = min((c0 + c) * 2048 + lane * 32, row_bytes - 32);
     const uint4 a = *(const uint4*)(srow + off);
     const uint4 b = *(const uint4*)(srow + off + 16);
     w[c] = make_uint4(a.x ^ b.x, a.y ^ b.y, a.z ^ b.z, a.w ^ b.w);
@@ -54,7 +58,7 @@ __global__ __launch_bounds__(256) void bw_probe_kernel(const uint8_t* __restrict
     uint8_t* drow = dst + (size_t)d * out_bytes;
 #pragma unroll
     for (int c = 0; c < kC; ++c) {
-      const int off = c * 2048 + lane * 32;
+      const int off = (c0 + c) * 2048 + lane * 32;
       if (off < row_bytes) *(uint4*)(drow + off / 2) = w[c];
     }
   }
@@ -75,14 +79,14 @@ extern "C" int smoe_bw_probe(const void* src, int rows, int row_bytes, int fanou
     if (dst_bytes < (size_t)rows * fanout * (row_bytes / 2)) return SMOE_EINVAL_WORKSPACE;
   }
   if (!sink) return SMOE_EINVAL_NULL;
-  const dim3 grid((rows + 3) / 4), block(256);
   hipStream_t s = (hipStream_t)stream;
-#define SMOE_BP(C) \
-  bw_probe_kernel<C><<<grid, block, 0, s>>>((const uint8_t*)src, rows, row_bytes, fanout, (uint8_t*)dst, (uint32_t*)sink)
+#define SMOE_BP(C, W)                                                                              \
+  bw_probe_kernel<C, W><<<dim3((unsigned)(((long long)rows * W + 3) / 4)), dim3(256), 0, s>>>( \
+      (const uint8_t*)src, rows, row_bytes, fanout, (uint8_t*)dst, (uint32_t*)sink)
   switch (row_bytes / 2048) {
-    case 1: SMOE_BP(1); break; case 2: SMOE_BP(2); break; case 3: SMOE_BP(3); break;
-    case 4: SMOE_BP(4); break; case 5: SMOE_BP(5); break; case 6: SMOE_BP(6); break;
-    case 7: SMOE_BP(7); break; default: SMOE_BP(8); break;
+    case 1: SMOE_BP(1, 1); break; case 2: SMOE_BP(2, 1); break; case 3: SMOE_BP(3, 1); break;
+    case 4: SMOE_BP(4, 1); break; case 5: SMOE_BP(3, 2); break; case 6: SMOE_BP(3, 2); break;
+    default: SMOE_BP(4, 2); break;
   }
 #undef SMOE_BP
   SMOE_RETURN_LAUNCH();

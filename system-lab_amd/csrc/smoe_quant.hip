@@ -81,16 +81,20 @@ __global__ __launch_bounds__(256) void permute_quant_kernel(
   }
 }
 
-// Whole-row variant for rows of at most 8 chunks (H <= 8192): every chunk of
-// the token row is loaded before any arithmetic, and each destination row
-// is then written front to back (its kC 1 KiB pieces consecutively) before
-// the next, so each wave's write stream is kC KiB sequential per row.
-template <int kC, bool kNT>
+// Whole-row variant for rows of at most 8 chunks (H <= 8192): a token's row
+// is split over kW waves, wave j taking chunks j*kC .. j*kC + kC - 1.  Every
+// chunk a wave owns is loaded before any arithmetic, and its part of each
+// destination row is then written front to back (kC 1 KiB pieces
+// consecutively) before the next.  kW = 2 halves the registers a wave holds
+// (88 VGPRs for 4 chunks against 156 for 7 chunks in one wave), so 5 waves
+// per SIMD instead of 3 keep loads in flight.
+template <int kC, int kW, bool kNT>
 __global__ __launch_bounds__(256) void permute_quant_row_kernel(
     const uint16_t* __restrict__ x, const int32_t* __restrict__ inv_map, int T, int H, int K,
     uint8_t* __restrict__ xq, float* __restrict__ xs) {
   const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const unsigned wv = blockIdx.x * 4u + (threadIdx.x >> 6);
+  const int t = (int)(wv / kW), c0 = (int)(wv % kW) * kC;
   if (t >= T) return;
   const int G = H / kGroup;
   const int R = T * K;
@@ -100,7 +104,7 @@ __global__ __launch_bounds__(256) void permute_quant_row_kernel(
   uint4 v[kC][2];
 #pragma unroll
   for (int c = 0; c < kC; ++c) {
-    const int g = min(c * 8 + gl, G - 1);  // unconditional: every load in flight
+    const int g = min((c0 + c) * 8 + gl, G - 1);  // unconditional: every load in flight
     const uint4* src = (const uint4*)(xrow + g * kGroup + sub * 16);
     v[c][0] = src[0];
     v[c][1] = src[1];
@@ -118,7 +122,7 @@ __global__ __launch_bounds__(256) void permute_quant_row_kernel(
     if ((unsigned)r >= (unsigned)R) continue;  // malformed map: never write out of range
 #pragma unroll
     for (int c = 0; c < kC; ++c) {
-      const int g = c * 8 + gl;
+      const int g = (c0 + c) * 8 + gl;
       if (g < G) {
         store16<kNT>(xq + (size_t)r * H + g * kGroup + sub * 16, q[c].q);
         if (sub == 0) xs[(size_t)r * G + g] = q[c].scale;
@@ -382,26 +386,30 @@ extern "C" int smoe_permute_quant(const uint16_t* x, const int32_t* inv_map, int
   SMOE_CHECK_PTR(xq);
   SMOE_CHECK_PTR(xs);
   const int chunks = (H / kGroup + 7) / 8;
-  const dim3 grid((T + 3) / 4), block(256);
   hipStream_t s = (hipStream_t)stream;
   // Rows of up to 8 chunks (H <= 8192): the whole-row kernel with cached
-  // stores.  Each destination row is written front to back before the next;
-  // measured with cold caches at config 2 (T=16384, H=7168, top-8) it takes
-  // 212 us (71% of 8 TB/s) against 229 us with non-temporal stores in the
-  // same order and 232 us for the chunk-interleaved kernel below.
-#define SMOE_PR(C) permute_quant_row_kernel<C, false><<<grid, block, 0, s>>>(x, inv_map, T, H, K, xq, xs)
+  // stores, rows of 5..8 chunks split over two waves.  Measured with cold
+  // caches at config 2 (T=16384, H=7168, top-8) on one box: 0.214 ms for
+  // 4 chunks x 2 waves against 0.222 ms for 7 chunks in one wave and
+  // 0.214 ms for 2 chunks x 4 waves.  On another box, where one wave per
+  // row took 212 us, its non-temporal stores took 229 us and the
+  // chunk-interleaved kernel below 232 us.
+#define SMOE_PR(C, W) \
+  permute_quant_row_kernel<C, W, false><<<dim3((unsigned)(((long long)T * W + 3) / 4)), dim3(256), 0, s>>>( \
+      x, inv_map, T, H, K, xq, xs)
   if (chunks <= 8) {
     switch (chunks) {
-      case 1: SMOE_PR(1); break; case 2: SMOE_PR(2); break; case 3: SMOE_PR(3); break;
-      case 4: SMOE_PR(4); break; case 5: SMOE_PR(5); break; case 6: SMOE_PR(6); break;
-      case 7: SMOE_PR(7); break; default: SMOE_PR(8); break;
+      case 1: SMOE_PR(1, 1); break; case 2: SMOE_PR(2, 1); break; case 3: SMOE_PR(3, 1); break;
+      case 4: SMOE_PR(4, 1); break; case 5: SMOE_PR(3, 2); break; case 6: SMOE_PR(3, 2); break;
+      default: SMOE_PR(4, 2); break;
     }
     SMOE_RETURN_LAUNCH();
   }
 #undef SMOE_PR
   // longer rows: kUnroll = 4 chunks (128 B per lane) in flight keeps 2+
   // waves per SIMD
-#define SMOE_PQ(U) permute_quant_kernel<U, true><<<grid, block, 0, s>>>(x, inv_map, T, H, K, xq, xs)
+#define SMOE_PQ(U) \
+  permute_quant_kernel<U, true><<<dim3((unsigned)(((long long)T + 3) / 4)), dim3(256), 0, s>>>(x, inv_map, T, H, K, xq, xs)
   SMOE_PQ(4);
 #undef SMOE_PQ
   SMOE_RETURN_LAUNCH();

@@ -297,7 +297,12 @@ def test_reciprocal_exhaustive(dev):
 
 @pytest.mark.parametrize("T,H,E,K,outl", [(2048, 1024, 8, 2, False), (1024, 7168, 256, 8, True),
                                           (333, 4096, 8, 2, False), (512, 2048, 128, 8, False),
-                                          (5, 1152, 4, 3, True), (64, 9216, 16, 4, True)])
+                                          (5, 1152, 4, 3, True), (64, 9216, 16, 4, True),
+                                          # rows split over two waves: 5 chunks (the second wave's
+                                          # last chunk past the row, one of its groups live), 6, 8,
+                                          # and an odd T (a block's last waves past the tokens)
+                                          (7, 4224, 16, 3, True), (9, 6144, 8, 2, False),
+                                          (130, 8192, 64, 8, True), (3, 7168, 256, 8, True)])
 def test_permute_quant_bit_exact(dev, T, H, E, K, outl):
     say("permute_quant", T, H, E, K, outl)
     x = W.tokens(T, H, outliers=outl)
