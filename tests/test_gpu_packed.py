@@ -68,6 +68,30 @@ def test_packed_gemm_bit_identical(dev, counts, N, K, extra):
         assert (got[-extra:].float() == 7.0).all()
 
 
+def test_packed_gemm_many_small_and_empty_experts(dev):
+    """256 experts of 0-40 rows (each such expert's one m-tile is mostly
+    masked rows) plus one of 300, and a call whose experts are all empty
+    (nothing is written)."""
+    say("many small experts")
+    rng = np.random.default_rng(5)
+    counts = [int(c) for c in rng.integers(0, 41, 256)]
+    counts[7] = 0
+    counts[100] = 300
+    off, xq, xs, wq, ws = _operands(dev, counts, 256, 512, 9, seed=6)
+    R = xq.shape[0]
+    ref = torch.full((R, 256), 3.0, dtype=torch.bfloat16, device=dev)
+    got = ref.clone()
+    ops.grouped_gemm_fp8(xq, xs, wq, ws, off, out=ref)
+    ops.grouped_gemm_fp8(xq, xs, ops.pack_weight_fp8(wq), ws, off, out=got)
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    assert (got[-9:].float() == 3.0).all()
+    zero = torch.zeros_like(off)
+    got.fill_(5.0)
+    ops.grouped_gemm_fp8(xq, xs, ops.pack_weight_fp8(wq), ws, zero, out=got)
+    torch.cuda.synchronize()
+    assert (got.float() == 5.0).all()
+
+
 @pytest.mark.parametrize("counts,I,K", [([200, 0, 333], 256, 1024), ([513, 64], 768, 2048)])
 def test_packed_swiglu_bit_identical(dev, counts, I, K):
     say("swiglu", counts, I, K)
