@@ -401,6 +401,8 @@ def run_only(args, dev, c):
                           "gbs": dispatch_bytes(c.T, c.H, c.E, c.K) / (ms * 1e-3) / 1e9}))
     elif args.only == "wgrad":
         print(json.dumps({"only": "wgrad", **bench_wgrad(dev, max(20, args.steps), args.warmup)}))
+    elif args.only == "bwdparts":
+        print(json.dumps({"only": "bwdparts", **bench_backward_parts(dev, args.steps, args.warmup)}))
     elif args.only == "refshapes":
         print(json.dumps({"only": "refshapes", **bench_reference_shapes(dev, args.steps, args.warmup)}))
     elif args.only == "router":
@@ -530,6 +532,58 @@ def bench_reference_shapes(dev, steps, warmup):
     return out
 
 
+def bench_backward_parts(dev, steps, warmup):
+    """The config-5 layer's HBM-bound forward and backward kernels one at a
+    time (inputs from one forward with saved intermediates), median of
+    per-call event timings warm and after the 1 GiB flush, with each call's
+    unique algorithmic bytes.  The gathered column quantisers read every
+    token row K times through row_map (T*H*2 unique bytes, R*H*2 requested)."""
+    import torch
+    import smoe
+    from smoe import ops, workloads as W
+    c = W.CONFIGS["qwen3"]
+    m = smoe.SimpleMoE(c.H, c.I, c.E, c.K, device=dev)
+    with torch.no_grad():
+        m.w1.copy_(W.weights(c.E, 2 * c.I, c.H, device=dev))
+        m.w2.copy_(W.weights(c.E, c.H, c.I, device=dev, seed=13))
+    m.refresh_fp8_cache()
+    x, lg = W.tokens(c.T, c.H, device=dev), W.logits(c.T, c.E, device=dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(4)
+    dout = (torch.randn((c.T, c.H), generator=g, device=dev) * 1e-3).to(torch.bfloat16)
+    with torch.no_grad():
+        _, st = m(x, lg, return_intermediates=True)
+    off, inv, rm, K = st["offsets"], st["inv_map"], st["row_map"], c.K
+    R, H, I, T = c.T * c.K, c.H, c.I, c.T
+    dh = (torch.randn((R, I), generator=g, device=dev) * 1e-3).to(torch.bfloat16)
+    dxs = torch.randn((R, H), generator=g, device=dev).to(torch.bfloat16)
+    ones = torch.ones_like(st["topk_w"])
+    parts = {
+        "swiglu_quant_save_h": (lambda: ops.swiglu_quant(st["c1"], save_h=True),
+                                R * 2 * I * 2 + R * I + R * (I // 128) * 4 + R * I * 2),
+        "quant_cols_h": (lambda: ops.quant_cols(st["h"], off), R * I * 2 + R * I),
+        "quant_cols_x_gathered": (lambda: ops.quant_cols(st["x"], off, gather=rm, gather_div=K),
+                                  T * H * 2 + R * H),
+        "combine_bwd_quant": (lambda: ops.unpermute_combine_bwd_quant(dout, st["y"], inv, rm,
+                                                                      st["topk_w"], off),
+                              T * H * 2 + R * H * 2 + 2 * R * H + R * 4),
+        "swiglu_bwd_quant": (lambda: ops.swiglu_bwd_quant(st["c1"], dh, off),
+                             R * 2 * I * 2 + R * I * 2 + 2 * R * 2 * I),
+        "combine_dx": (lambda: ops.unpermute_combine(dxs, inv, ones), R * H * 2 + T * H * 2),
+    }
+    flush = Flush()
+    out = {"workload": "qwen3 layer T=16384 H=2048 I=768 E=128 top8"}
+    for name, (fn, nb) in parts.items():
+        warm = timed_median(fn, steps, warmup)
+        cold = timed_median(fn, steps, warmup, flush)
+        out[name] = {"unique_bytes": nb, "warm_us": round(warm * 1e3, 1),
+                     "warm_gbs": round(nb / (warm * 1e-3) / 1e9, 1),
+                     "cold_us": round(cold * 1e3, 1), "cold_gbs": round(nb / (cold * 1e-3) / 1e9, 1)}
+    del m, st, flush
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -538,7 +592,8 @@ def main():
     ap.add_argument("--skip-extra", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--only", choices=["permute", "gemm", "combine", "copy", "fwdbwd", "ceiling",
-                                       "blaslt", "router", "wgrad", "layer", "refshapes"],
+                                       "blaslt", "router", "wgrad", "layer", "refshapes",
+                                       "bwdparts"],
                     help="run one kernel family only (for rocprofv3 runs) and print its timing")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
