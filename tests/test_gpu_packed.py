@@ -54,6 +54,7 @@ def test_pack_layout(dev):
     ([1000], 256, 2048, 0),
     ([0, 700, 0, 5, 1300, 0, 256, 1], 1024, 4096, 11),
     ([17, 600], 2048, 7168, 0),
+    ([100, 200], 128, 512, 5),              # N = 128: one half-filled column tile
 ])
 def test_packed_gemm_bit_identical(dev, counts, N, K, extra):
     say("gemm", counts, N, K, extra)
@@ -92,7 +93,8 @@ def test_packed_gemm_many_small_and_empty_experts(dev):
     assert (got.float() == 5.0).all()
 
 
-@pytest.mark.parametrize("counts,I,K", [([200, 0, 333], 256, 1024), ([513, 64], 768, 2048)])
+@pytest.mark.parametrize("counts,I,K", [([200, 0, 333], 256, 1024), ([513, 64], 768, 2048),
+                                        ([300, 0, 77], 128, 512), ([1000], 1408, 1024)])
 def test_packed_swiglu_bit_identical(dev, counts, I, K):
     say("swiglu", counts, I, K)
     off, xq, xs, w1q, w1s = _operands(dev, counts, 2 * I, K, seed=3)
