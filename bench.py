@@ -359,9 +359,9 @@ def bench_ceiling(dev, c, iters=20):
     out = {"bytes_in": c.T * row_bytes, "pattern": "permute_quant's (a row split over 2 waves, each part "
            "loaded whole, then written front to back into each scattered destination row)"}
     for fanout in (0, 2, 4, 8):
-        fn = lambda: smoe._C.call("smoe_bw_probe", src.data_ptr(), c.T, row_bytes, fanout,
-                                  dst.data_ptr(), dst.numel(), sink.data_ptr(),
-                                  torch.cuda.current_stream().cuda_stream)
+        fn = lambda: smoe._C.probe_call("smoe_bw_probe", src.data_ptr(), c.T, row_bytes, fanout,
+                                        dst.data_ptr(), dst.numel(), sink.data_ptr(),
+                                        torch.cuda.current_stream().cuda_stream)
         ms = timed_median(fn, iters, 3, flush)
         nb = c.T * row_bytes * (2 + fanout) // 2
         out[f"read2_write{fanout}"] = {"ms": round(ms, 4), "gbs": round(nb / (ms * 1e-3) / 1e9, 1),

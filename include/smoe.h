@@ -47,6 +47,7 @@ enum {
   SMOE_EINVAL_WORKSPACE = -5, /* workspace NULL or smaller than required     */
   SMOE_EINVAL_PTRALIGN = -6,  /* a pointer is not 16-byte aligned            */
   SMOE_EINVAL_TOPK = -7,      /* K <= 0, K > E or K > 32                     */
+  SMOE_EINVAL_MODE = -8,      /* an enumerated mode argument is out of range */
 };
 
 /* Human-readable text for a status code (never NULL). */
@@ -87,7 +88,8 @@ int smoe_router_topk_bwd(const float* logits, const int32_t* topk_idx, const flo
  * smoe_route_sort_workspace_size() bytes.
  * Ids outside [0, E) are an error the call cannot report synchronously (they
  * live on the device): such a pair gets no row and inv_map[p] = -1, so
- * offsets[E] = T*K minus their number, and the int32 at byte
+ * offsets[E] = T*K minus their number (row_map[offsets[E] ..] is then left
+ * unwritten), and the int32 at byte
  * SMOE_ROUTE_STATUS_OFFSET of ws receives that number (0 when every id is
  * valid).  The status word is rewritten by every call.
  * Replaces the pack sort phase that yields pack_perm "sorted pair index ->
@@ -389,6 +391,30 @@ int smoe_grouped_gemm_fp8_wgrad(const uint8_t* aT, const float* aTs, const uint8
                                 int ld, float* dW, void* stream);
 
 /*
+ * smoe_grouped_gemm_fp8_wgrad with a choice of output (the same fp32 tile
+ * sums in every mode):
+ *   SMOE_WGRAD_F32      dW f32, written (what smoe_grouped_gemm_fp8_wgrad does);
+ *   SMOE_WGRAD_F32_ACC  dW f32 += tile (one fp32 addition per value);
+ *   SMOE_WGRAD_BF16     dW bf16 = RNE(tile);
+ *   SMOE_WGRAD_BF16_ACC dW bf16 = RNE(float(dW) + tile).
+ * The accumulating modes add into a framework's gradient-accumulation
+ * buffer in the wgrad epilogue (experts without rows leave it untouched), in
+ * place of a separate fp32 gradient and an add pass: Megatron's
+ * gradient_accumulation_fusion, which writes the weight gradient straight into
+ * the fp32 main_grad (notes/mlperf-llama/2026-04-29_nemo_vs_primus_config_diff.md:233-235),
+ * and the bf16 main_grads_dtype of the reference's GPT-OSS runs
+ * (notes/2026-04/2026-04-20_gptoss_05_borrow_from_deepseek_v3_config.md:23,48).
+ * Any other mode returns SMOE_EINVAL_MODE.
+ */
+#define SMOE_WGRAD_F32 0
+#define SMOE_WGRAD_F32_ACC 1
+#define SMOE_WGRAD_BF16 2
+#define SMOE_WGRAD_BF16_ACC 3
+int smoe_grouped_gemm_fp8_wgrad_ex(const uint8_t* aT, const float* aTs, const uint8_t* bT,
+                                   const float* bTs, const int32_t* pad, int E, int N, int Kdim,
+                                   int ld, void* dW, int mode, void* stream);
+
+/*
  * SwiGLU backward: c1 [R,2I] (gate | up) and dh [R,I] bf16 -> dc1 [R,2I]
  * bf16 = [dg | du] with s = 1/(1+exp(-g)), du = dh*(g*s),
  * dg = (dh*u)*(s*(1 + g*(1-s))) in fp32 (library exp).  Replaces the SwiGLU
@@ -423,20 +449,6 @@ int smoe_unpermute_combine_bwd_quant(const uint16_t* dout, const uint16_t* y,
                                      const float* w, int T, int K, int H, const int32_t* offsets,
                                      int E, int ld, uint8_t* dyq, float* dys, uint8_t* dyTq,
                                      float* dyTs, int32_t* pad, float* dw, void* stream);
-
-/*
- * Measurement utility (no counterpart in the reference): the access pattern
- * of smoe_permute_quant without its arithmetic.  One or two waves per source
- * row of row_bytes bytes (a multiple of 2048, at most 16384; two waves above
- * 8192, as in smoe_permute_quant) read it with 128-bit loads and write half
- * as many bytes, derived from it, to each of `fanout` destination rows
- * (scattered, each front to back) with 128-bit stores; fanout = 0
- * only reads.  fanout = 8 moves the dispatch step's 1:4 read:write byte mix,
- * so its rate is the HBM ceiling for that mix.  dst must hold
- * rows * fanout * row_bytes / 2 bytes; sink: one device word.
- */
-int smoe_bw_probe(const void* src, int rows, int row_bytes, int fanout, void* dst,
-                  size_t dst_bytes, void* sink, void* stream);
 
 #ifdef __cplusplus
 }

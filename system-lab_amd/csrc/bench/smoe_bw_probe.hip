@@ -1,4 +1,13 @@
-// smoe_probe.hip — HBM traffic-mix probe (gfx950), a measurement utility.
+// smoe_bw_probe.hip — HBM traffic-mix probe (gfx950), a measurement utility
+// for the benchmark only: it is built into its own library,
+// libsmoe_probe.so, and is not part of libsmoe.so or its header.
+//
+//   int smoe_bw_probe(const void* src, int rows, int row_bytes, int fanout,
+//                     void* dst, size_t dst_bytes, void* sink, void* stream);
+//
+// returns 0 or a negative SMOE_EINVAL_* code (row_bytes a multiple of 2048,
+// at most 16384; dst must hold rows * fanout * row_bytes / 2 bytes; sink is
+// one device word).
 //
 // The access pattern of permute_quant without its arithmetic: a source row of
 // row_bytes (<= 16 KiB) bytes is split over the same number of waves as in
@@ -13,7 +22,7 @@
 // otherwise.  fanout = 0 only reads.  Bytes moved: rows*row_bytes read,
 // rows*fanout*row_bytes/2 written; fanout 8 is the dispatch step's 1:4 mix.
 // Its rate is the ceiling the HBM offers that mix to this access pattern.
-#include "smoe_common.h"
+#include "../smoe_common.h"
 
 namespace smoe {
 

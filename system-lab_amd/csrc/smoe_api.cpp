@@ -11,6 +11,7 @@ extern "C" const char* smoe_strerror(int status) {
     case SMOE_EINVAL_WORKSPACE: return "smoe: workspace missing or too small";
     case SMOE_EINVAL_PTRALIGN: return "smoe: pointer not 16-byte aligned";
     case SMOE_EINVAL_TOPK: return "smoe: top-k must be in [1, min(E, 32)]";
+    case SMOE_EINVAL_MODE: return "smoe: mode argument out of range";
     default: return status > 0 ? "smoe: HIP error (value is a hipError_t)" : "smoe: unknown error";
   }
 }

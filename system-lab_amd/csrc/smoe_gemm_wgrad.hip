@@ -6,7 +6,8 @@
 // over expert e's 128-row groups g in [pad[e], pad[e+1]) of the transposed,
 // 128x1-quantised operands aT [N, ld] (e.g. output grads) and bT [K, ld]
 // (e.g. activations), both with the reduction index r contiguous.  Output is
-// fp32 [E, N, K]; experts without rows get zeros.
+// [E, N, K], fp32 or bf16, written (experts without rows get zeros) or added
+// into the buffer's contents.
 //
 // A workgroup of 8 waves owns a 256 (n) x 256 (k) tile of one expert; each
 // wave owns 64 n x 128 k, i.e. 4 x 8 blocks of v_mfma_f32_16x16x128_f8f6f4,
@@ -36,14 +37,25 @@ constexpr int kWSC = (kWN + kWK) * kWChunk * 4;  // 16 KiB per chunk
 constexpr int kWSmem = 2 * kWStage + 2 * kWSC;
 static_assert(kWSmem <= 160 * 1024, "LDS budget");
 
+// Output modes of the weight gradient (SMOE_WGRAD_*): fp32 or
+// bf16, written or added into what the buffer holds (a framework's
+// gradient-accumulation buffer, "main_grad").
+enum WgradOut {
+  kOutF32 = SMOE_WGRAD_F32,
+  kOutF32Acc = SMOE_WGRAD_F32_ACC,
+  kOutBF16 = SMOE_WGRAD_BF16,
+  kOutBF16Acc = SMOE_WGRAD_BF16_ACC
+};
+
 // One 256 x 256 tile of expert e's weight gradient at (n0, k0).
+template <int kOut>
 __device__ __forceinline__ void wgrad_tile(const uint8_t* __restrict__ aT,
                                            const float* __restrict__ aTs,
                                            const uint8_t* __restrict__ bT,
                                            const float* __restrict__ bTs,
                                            const int32_t* __restrict__ pad, int N, int Kd, int ld,
                                            int e, int n0, int k0, uint8_t* smem,
-                                           float* __restrict__ dW) {
+                                           void* __restrict__ dW) {
   // opaque per tile: keeps lane-dependent address arithmetic inside the
   // caller's tile loop instead of live (in VGPRs) across it
   int tid = threadIdx.x;
@@ -165,13 +177,20 @@ __device__ __forceinline__ void wgrad_tile(const uint8_t* __restrict__ aT,
     asm volatile("" ::: "memory");
   }
 
+  // An expert without rows adds nothing to an accumulation buffer.
+  if ((kOut == kOutF32Acc || kOut == kOutBF16Acc) && steps == 0) return;
+
   // Epilogue: the fp32 tile leaves through LDS in two 128-row halves (the
   // stage buffers are free after the K loop's last barrier).  Lane (i, j, v)
   // holds dW row n = wn*64 + j*16 + (lane/16)*4 + v, column k = wk*128 +
   // i*16 + lane%16; with a row pitch of 260 floats the 4 lane groups of a
   // write land 16 banks apart, so the writes are conflict-free.  Then each
-  // wave stores whole 1 KB rows, 16 bytes per lane, non-temporally (dW is
-  // written once here and read by a later kernel).
+  // wave writes whole rows, 4 columns per lane: fp32 as 16-byte stores,
+  // non-temporal (dW is written once here and read by a later kernel), bf16
+  // rounded to nearest even as 8-byte stores.  The accumulating modes read
+  // the 4 columns first and add the tile's fp32 values to them (one fp32
+  // addition per value, then the bf16 rounding for a bf16 buffer: the same
+  // result as adding an fp32 gradient to the buffer in a separate pass).
   float* ct = (float*)smem;
   constexpr int kPitch = kWK + 4;
   static_assert(128 * kPitch * 4 <= kWSmem, "epilogue half-tile fits the LDS buffers");
@@ -192,8 +211,30 @@ __device__ __forceinline__ void wgrad_tile(const uint8_t* __restrict__ aT,
     for (int r = wid; r < 128; r += 8) {
       const int nl = half * 128 + r;
       if (nl < nrows && lane * 4 < krows) {
-        const v4f val = *(const v4f*)(ct + r * kPitch + lane * 4);
-        __builtin_nontemporal_store(val, (v4f*)(dW + ((size_t)e * N + n0 + nl) * Kd + k0 + lane * 4));
+        v4f val = *(const v4f*)(ct + r * kPitch + lane * 4);
+        const size_t o = ((size_t)e * N + n0 + nl) * Kd + k0 + lane * 4;
+        if constexpr (kOut == kOutF32) {
+          __builtin_nontemporal_store(val, (v4f*)((float*)dW + o));
+        } else if constexpr (kOut == kOutF32Acc) {
+          v4f* d = (v4f*)((float*)dW + o);
+          const v4f old = *d;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) val[v] = old[v] + val[v];
+          *d = val;
+        } else {
+          uint2* d = (uint2*)((uint16_t*)dW + o);
+          if constexpr (kOut == kOutBF16Acc) {
+            const uint2 old = *d;
+            val[0] += __uint_as_float(old.x << 16);
+            val[1] += __uint_as_float(old.x & 0xffff0000u);
+            val[2] += __uint_as_float(old.y << 16);
+            val[3] += __uint_as_float(old.y & 0xffff0000u);
+          }
+          uint2 b;
+          b.x = bf16_pack2(val[0], val[1]);
+          b.y = bf16_pack2(val[2], val[3]);
+          *d = b;
+        }
       }
     }
     __syncthreads();
@@ -204,10 +245,11 @@ __device__ __forceinline__ void wgrad_tile(const uint8_t* __restrict__ aT,
 // fp32 output and the prologue), so that empty experts' tiles count too.
 constexpr int kTileFixed = 4;
 
+template <int kOut>
 __global__ __launch_bounds__(kWThreads, 1) void grouped_gemm_fp8_wgrad_kernel(
     const uint8_t* __restrict__ aT, const float* __restrict__ aTs, const uint8_t* __restrict__ bT,
     const float* __restrict__ bTs, const int32_t* __restrict__ pad, int E, int N, int Kd, int ld,
-    int per_xcd, float* __restrict__ dW) {
+    int per_xcd, void* __restrict__ dW) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kWSmem];
   // the cost prefix lives in the stage buffers until the tile range is known
   long long* cpre = (long long*)smem;
@@ -283,7 +325,8 @@ __global__ __launch_bounds__(kWThreads, 1) void grouped_gemm_fp8_wgrad_kernel(
   for (int t = t_begin + j; t < t_end; t += per_xcd) {
     const int e = t / TE;
     const int rem = t - e * TE;
-    wgrad_tile(aT, aTs, bT, bTs, pad, N, Kd, ld, e, (rem / KT) * kWN, (rem % KT) * kWK, smem, dW);
+    wgrad_tile<kOut>(aT, aTs, bT, bTs, pad, N, Kd, ld, e, (rem / KT) * kWN, (rem % KT) * kWK, smem,
+                     dW);
     __syncthreads();  // the next tile reuses the LDS
   }
 }
@@ -292,14 +335,15 @@ __global__ __launch_bounds__(kWThreads, 1) void grouped_gemm_fp8_wgrad_kernel(
 
 using namespace smoe;
 
-extern "C" int smoe_grouped_gemm_fp8_wgrad(const uint8_t* aT, const float* aTs,
-                                           const uint8_t* bT, const float* bTs,
-                                           const int32_t* pad, int E, int N, int Kdim, int ld,
-                                           float* dW, void* stream) {
+extern "C" int smoe_grouped_gemm_fp8_wgrad_ex(const uint8_t* aT, const float* aTs,
+                                              const uint8_t* bT, const float* bTs,
+                                              const int32_t* pad, int E, int N, int Kdim, int ld,
+                                              void* dW, int mode, void* stream) {
   if (N <= 0 || Kdim <= 0 || ld <= 0) return SMOE_EINVAL_DIM;
   if (E <= 0 || E > SMOE_MAX_EXPERTS) return SMOE_EINVAL_EXPERTS;
   if (N % kGroup || Kdim % kGroup || ld % kGroup) return SMOE_EINVAL_ALIGN128;
   if ((long long)kWN * ld >= (1LL << 31)) return SMOE_EINVAL_DIM;
+  if (mode < kOutF32 || mode > kOutBF16Acc) return SMOE_EINVAL_MODE;
   SMOE_CHECK_PTR(aT);
   SMOE_CHECK_PTR(bT);
   SMOE_CHECK_PTR(dW);
@@ -310,8 +354,25 @@ extern "C" int smoe_grouped_gemm_fp8_wgrad(const uint8_t* aT, const float* aTs,
   const long long tiles = (long long)E * ((Kdim + kWK - 1) / kWK) * ((N + kWN - 1) / kWN);
   const long long per_xcd = (tiles + 7) / 8;
   if (per_xcd * 8 > 0x7fffffffLL) return SMOE_EINVAL_DIM;
-  grouped_gemm_fp8_wgrad_kernel<<<dim3((unsigned)(per_xcd * 8)), dim3(kWThreads), 0,
-                                  (hipStream_t)stream>>>(aT, aTs, bT, bTs, pad, E, N, Kdim, ld,
-                                                         (int)per_xcd, dW);
+  const dim3 grid((unsigned)(per_xcd * 8)), block(kWThreads);
+  hipStream_t s = (hipStream_t)stream;
+#define SMOE_WG(M)                                                                     \
+  grouped_gemm_fp8_wgrad_kernel<M><<<grid, block, 0, s>>>(aT, aTs, bT, bTs, pad, E, N, Kdim, ld, \
+                                                          (int)per_xcd, dW)
+  switch (mode) {
+    case kOutF32: SMOE_WG(kOutF32); break;
+    case kOutF32Acc: SMOE_WG(kOutF32Acc); break;
+    case kOutBF16: SMOE_WG(kOutBF16); break;
+    default: SMOE_WG(kOutBF16Acc); break;
+  }
+#undef SMOE_WG
   SMOE_RETURN_LAUNCH();
+}
+
+extern "C" int smoe_grouped_gemm_fp8_wgrad(const uint8_t* aT, const float* aTs,
+                                           const uint8_t* bT, const float* bTs,
+                                           const int32_t* pad, int E, int N, int Kdim, int ld,
+                                           float* dW, void* stream) {
+  return smoe_grouped_gemm_fp8_wgrad_ex(aT, aTs, bT, bTs, pad, E, N, Kdim, ld, dW, kOutF32,
+                                        stream);
 }

@@ -33,7 +33,6 @@ SIGNATURES = {
                                     c_size_t, P]),
     "smoe_selftest_quant": (c_int, [P, P]),
     "smoe_selftest_recip": (c_int, [P, P]),
-    "smoe_bw_probe": (c_int, [P, c_int, c_int, c_int, P, c_size_t, P, P]),
     "smoe_quantize_weight_blockwise": (c_int, [P, c_int, c_int, c_int, P, P, P]),
     "smoe_grouped_gemm_fp8_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int]),
     "smoe_grouped_gemm_fp8": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int, P, P,
@@ -54,11 +53,19 @@ SIGNATURES = {
     "smoe_quant_rows_cols": (c_int, [P, c_int, c_int, P, c_int, c_int, P, P, P, P, P, P]),
     "smoe_swiglu_bwd_quant": (c_int, [P, P, c_int, c_int, P, c_int, c_int, P, P, P, P, P, P, P]),
     "smoe_grouped_gemm_fp8_wgrad": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int, P, P]),
+    "smoe_grouped_gemm_fp8_wgrad_ex": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int, P,
+                                               c_int, P]),
     "smoe_swiglu_bwd": (c_int, [P, P, c_int, c_int, P, P]),
     "smoe_unpermute_combine_bwd": (c_int, [P, P, P, P, c_int, c_int, c_int, P, P, P]),
     "smoe_unpermute_combine_bwd_quant": (c_int, [P, P, P, P, P, c_int, c_int, c_int, P, c_int,
                                                  c_int, P, P, P, P, P, P, P]),
 }
+
+
+# libsmoe_probe.so: the benchmark's HBM traffic-mix probe, kept out of the
+# product library (csrc/bench/smoe_bw_probe.hip)
+PROBE_PATH = os.path.join(_HERE, "libsmoe_probe.so")
+PROBE_SIGNATURES = {"smoe_bw_probe": (c_int, [P, c_int, c_int, c_int, P, c_size_t, P, P])}
 
 
 class SmoeLibraryMissing(RuntimeError):
@@ -97,5 +104,26 @@ def lib() -> ctypes.CDLL:
 def call(name: str, *args) -> None:
     """Call a status-returning entry point and raise SmoeError on failure."""
     st = getattr(lib(), name)(*args)
+    if st != 0:
+        raise SmoeError(name, st, lib().smoe_strerror(st).decode())
+
+
+_probe = None
+
+
+def probe_call(name: str, *args) -> None:
+    """Call an entry point of the benchmark's probe library
+    (libsmoe_probe.so, built next to libsmoe.so) and raise on failure."""
+    global _probe
+    with _lock:
+        if _probe is None:
+            if not os.path.exists(PROBE_PATH):
+                raise SmoeLibraryMissing(f"{PROBE_PATH} not found: build it with `python -m smoe.build`")
+            handle = ctypes.CDLL(PROBE_PATH)
+            for n, (res, a) in PROBE_SIGNATURES.items():
+                getattr(handle, n).restype = res
+                getattr(handle, n).argtypes = a
+            _probe = handle
+    st = getattr(_probe, name)(*args)
     if st != 0:
         raise SmoeError(name, st, lib().smoe_strerror(st).decode())

@@ -20,8 +20,10 @@ LIB = os.path.join(PKG, "libsmoe.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 SOURCES = ["smoe_api.cpp", "smoe_route.hip", "smoe_quant.hip", "smoe_gemm.hip",
-           "smoe_gemm_wgrad.hip", "smoe_gemm_packed.hip", "smoe_combine.hip", "smoe_backward.hip",
-           "smoe_probe.hip"]
+           "smoe_gemm_wgrad.hip", "smoe_gemm_packed.hip", "smoe_combine.hip", "smoe_backward.hip"]
+# the benchmark's HBM probe: its own library, not part of libsmoe.so
+PROBE_SOURCES = ["bench/smoe_bw_probe.hip"]
+PROBE_LIB = os.path.join(PKG, "libsmoe_probe.so")
 
 HIP_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
@@ -33,7 +35,7 @@ HIP_FLAGS = [
 
 
 def _compile(src: str) -> str:
-    obj = os.path.join(PKG, "_obj", os.path.splitext(src)[0] + ".o")
+    obj = os.path.join(PKG, "_obj", os.path.splitext(os.path.basename(src))[0] + ".o")
     os.makedirs(os.path.dirname(obj), exist_ok=True)
     path = os.path.join(CSRC, src)
     if src.endswith(".hip"):
@@ -46,17 +48,23 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(verbose: bool = False) -> str:
-    with ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as ex:
-        objs = list(ex.map(_compile, SOURCES))
-    tmp = LIB + ".tmp"
+def _link(objs, lib: str) -> None:
+    tmp = lib + ".tmp"
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib)
+
+
+def build(verbose: bool = False) -> str:
+    srcs = SOURCES + PROBE_SOURCES
+    with ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
+        objs = list(ex.map(_compile, srcs))
+    _link(objs[:len(SOURCES)], LIB)
+    _link(objs[len(SOURCES):], PROBE_LIB)
     if verbose:
-        print("built", LIB)
+        print("built", LIB, "and", PROBE_LIB)
     return LIB
 
 

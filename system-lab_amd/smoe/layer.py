@@ -15,37 +15,65 @@ from torch import nn
 from . import ops
 
 
+# Optimizer steps seen in this process.  Megatron-style optimizers write the
+# stepped weights back through ``param.data.copy_()``, which does not advance
+# a parameter's version counter; every torch optimizer step (Megatron's inner
+# fp32 optimizer included) bumps this count instead, and the fp8 weight cache
+# is keyed on it as well as on the parameters' storage and versions.
+_OPT_STEPS = [0]
+_OPT_HOOK = []
+
+
+def _count_optimizer_step(optimizer, args, kwargs):
+    _OPT_STEPS[0] += 1
+
+
+def _install_optimizer_hook():
+    if not _OPT_HOOK:
+        from torch.optim.optimizer import register_optimizer_step_post_hook
+        _OPT_HOOK.append(register_optimizer_step_post_hook(_count_optimizer_step))
+
+
 class _SimpleMoEFunction(torch.autograd.Function):
     """Autograd node of one SimpleMoE forward.  The forward keeps the
-    intermediates the fp8 backward needs; the backward is
+    intermediates the fp8 backward needs as saved tensors, so autograd frees
+    them after a backward (a second backward needs ``retain_graph=True``, as
+    for any node, and otherwise raises PyTorch's own error) and checks that
+    none was modified in place.  It also keeps the fp8 weights the forward
+    used, so the dgrad runs on their transposes even if the weights are
+    re-quantised before the backward.  The backward is
     ``SimpleMoE.backward_from`` (every stage a HIP kernel) plus the router
     backward into the logits.  The gating linear that produces the logits
     (x @ w_gate) sits outside this node, so autograd carries dlogits on into
-    x and w_gate.  Weight gradients are computed in fp32; a parameter with a
-    ``main_grad`` fp32 buffer (Megatron's gradient-accumulation convention)
-    has them accumulated there, otherwise they are returned in the
-    parameter's dtype."""
+    x and w_gate.  A parameter with a ``main_grad`` fp32 buffer (Megatron's
+    gradient-accumulation convention) has its weight gradient added into it
+    by the wgrad kernel itself (no separate fp32 gradient or add pass);
+    otherwise the gradient is returned in the parameter's dtype."""
 
     @staticmethod
     def forward(ctx, x, logits, w1, w2, module):
         out, inter = module._forward_impl(x, logits, save=True)
         ctx.module = module
-        ctx.inter = inter
+        ctx.keys = [k for k, v in inter.items() if isinstance(v, torch.Tensor)]
+        ctx.extra = {k: v for k, v in inter.items() if not isinstance(v, torch.Tensor)}
+        ctx.save_for_backward(*[inter[k] for k in ctx.keys])
         ctx.dtypes = (x.dtype, w1.dtype, w2.dtype)
         ctx.main_grads = (getattr(w1, "main_grad", None), getattr(w2, "main_grad", None))
         return out
 
     @staticmethod
     def backward(ctx, dout):
-        g = ctx.module.backward_from(ctx.inter, dout.to(torch.bfloat16).contiguous())
-        ctx.inter = None
+        inter = dict(zip(ctx.keys, ctx.saved_tensors))
+        inter.update(ctx.extra)
+        mg1, mg2 = ctx.main_grads
+        # a weight gradient in the parameters' own dtype where that is bf16
+        # (rounded once from the fp32 sums, as .to() would), else fp32
+        wdt = torch.bfloat16 if ctx.dtypes[1] == ctx.dtypes[2] == torch.bfloat16 else torch.float32
+        g = ctx.module.backward_from(inter, dout.to(torch.bfloat16).contiguous(),
+                                     dw1_into=mg1, dw2_into=mg2, wgrad_dtype=wdt)
         grads = []
         for dw, mg, dt in zip((g["dw1"], g["dw2"]), ctx.main_grads, ctx.dtypes[1:]):
-            if mg is not None:
-                mg.add_(dw)
-                grads.append(None)
-            else:
-                grads.append(dw.to(dt))
+            grads.append(None if mg is not None else dw.to(dt))
         return g["dx"].to(ctx.dtypes[0]), g["dlogits"], grads[0], grads[1], None
 
 
@@ -55,13 +83,20 @@ class SimpleMoE(nn.Module):
     Parameters follow the notes' naming: ``w1`` [E, 2I, H] holds the gate
     rows [0, I) and up rows [I, 2I) of fc1 in [N, K] layout; ``w2`` [E, H, I]
     is fc2.  ``w_gate`` [H, E] is the router's gating linear.
-    Weights are quantised to fp8 with 128x128 block scales on first use; the
-    cache is keyed on the parameters' storage and version counters, so an
-    in-place update (an optimizer step) re-quantises on the next call.  Where
-    a GEMM's K is a multiple of 512 its weights are also cached packed in MFMA
+    Weights are quantised to fp8 with 128x128 block scales on first use.
+    The cache is keyed on the parameters' storage and version counters and
+    on the number of torch optimizer steps taken in the process, so an
+    in-place update (``p.copy_``, an optimizer step, or an optimizer that
+    writes back through ``p.data`` after its inner step) re-quantises on the
+    next call.  A write through ``p.data`` outside any optimizer step is
+    invisible to both: call ``refresh_fp8_cache()`` after one.  Where a
+    GEMM's K is a multiple of 512 the weights are cached packed in MFMA
     fragment order for the register-loaded kernel (``ops.pack_weight_fp8``;
-    the same result, see ``ops.grouped_gemm_fp8``), which adds the packed
-    copy's E*N*K bytes.
+    the same result, see ``ops.grouped_gemm_fp8``).  Footprint of the cache:
+    the plain fp8 w1, w2 (E*(2I*H + H*I) bytes, the source of the dgrad
+    transposes), their packed copies where packed, and the dgrad transposes
+    once a backward ran (packed where covered, else plain; never both), plus
+    the fp32 scales.
 
     Under autograd (grad mode on and an input or parameter requiring grad),
     ``forward`` records one graph node whose backward runs the fp8 backward
@@ -82,9 +117,9 @@ class SimpleMoE(nn.Module):
         self.register_buffer("router_bias", torch.zeros(num_experts, device=device) if router_bias else None)
         self._fp8 = None
         self._fp8_key = None
-        self._fp8_t = None
         self._gemm = None
         self._gemm_t = None
+        _install_optimizer_hook()
 
     @torch.no_grad()
     def reset_parameters(self, generator: torch.Generator | None = None, std: float = 0.02):
@@ -93,7 +128,8 @@ class SimpleMoE(nn.Module):
                                 device=generator.device if generator is not None else p.device).to(p) * std)
 
     def _weights_key(self):
-        return tuple((p.data_ptr(), p._version, tuple(p.shape)) for p in (self.w1, self.w2))
+        return (_OPT_STEPS[0],) + tuple((p.data_ptr(), p._version, tuple(p.shape))
+                                        for p in (self.w1, self.w2))
 
     @torch.no_grad()
     def refresh_fp8_cache(self):
@@ -101,7 +137,6 @@ class SimpleMoE(nn.Module):
         w2q, w2s = ops.quantize_weight_blockwise(self.w2.detach().to(torch.bfloat16).contiguous())
         self._fp8 = (w1q, w1s, w2q, w2s)
         self._fp8_key = self._weights_key()
-        self._fp8_t = None
         self._gemm = (self._for_gemm(w1q), w1s, self._for_gemm(w2q), w2s)
         self._gemm_t = None
         return self._fp8
@@ -122,12 +157,15 @@ class SimpleMoE(nn.Module):
         return self._fp8
 
     def fp8_weights_t(self):
-        """The dgrad weights: (w1q^T, w1s^T, w2q^T, w2s^T), cached with the
-        fp8 weights they come from."""
-        w1q, w1s, w2q, w2s = self.fp8_weights()
-        if self._fp8_t is None:
-            self._fp8_t = ops.transpose_blockwise(w1q, w1s) + ops.transpose_blockwise(w2q, w2s)
-        return self._fp8_t
+        """The dgrad weights: (w1q^T, w1s^T, w2q^T, w2s^T) of the current fp8
+        weights, computed on each call (the backward caches them in GEMM form,
+        ``gemm_weights_t``)."""
+        return self._transposed(self.fp8_weights())
+
+    @staticmethod
+    def _transposed(fp8):
+        w1q, w1s, w2q, w2s = fp8
+        return ops.transpose_blockwise(w1q, w1s) + ops.transpose_blockwise(w2q, w2s)
 
     def gemm_weights(self):
         """(w1, w1s, w2, w2s) as the forward GEMMs take them: fp8_weights()
@@ -135,11 +173,17 @@ class SimpleMoE(nn.Module):
         self.fp8_weights()
         return self._gemm
 
-    def gemm_weights_t(self):
-        """The dgrad weights of fp8_weights_t() in the form the GEMM ops take
-        (packed where covered), cached with them."""
-        w1tq, w1ts, w2tq, w2ts = self.fp8_weights_t()
+    def gemm_weights_t(self, fp8=None):
+        """The dgrad weights in the form the GEMM ops take (packed where
+        covered).  Those of the current fp8 weights are cached with them;
+        ``fp8`` names other fp8 weights (a forward's, since re-quantised),
+        whose transposes are computed and not cached."""
+        cur = self.fp8_weights()
+        if fp8 is not None and fp8 is not cur:
+            w1tq, w1ts, w2tq, w2ts = self._transposed(fp8)
+            return (self._for_gemm(w1tq), w1ts, self._for_gemm(w2tq), w2ts)
         if self._gemm_t is None:
+            w1tq, w1ts, w2tq, w2ts = self._transposed(cur)
             self._gemm_t = (self._for_gemm(w1tq), w1ts, self._for_gemm(w2tq), w2ts)
         return self._gemm_t
 
@@ -172,7 +216,8 @@ class SimpleMoE(nn.Module):
         logits = logits.detach().float().contiguous()
         if x.shape[0] == 0:
             return self._empty_forward(x, logits, save)
-        w1q, w1s, w2q, w2s = self.gemm_weights()
+        fp8 = self.fp8_weights()
+        w1q, w1s, w2q, w2s = self._gemm
         # router and expert sort in three launches (the sort's histogram is
         # counted inside the router launch)
         idx, w, row_map, inv_map, counts, offsets = ops.route_topk_sort(logits, self.top_k,
@@ -191,7 +236,7 @@ class SimpleMoE(nn.Module):
         if save:
             return out, dict(x=x, logits=logits, topk_idx=idx, topk_w=w, row_map=row_map,
                              inv_map=inv_map, counts=counts, offsets=offsets, xq=xq, xs=xs,
-                             c1=c1, hq=hq, hs=hs, h=h, y=y)
+                             c1=c1, hq=hq, hs=hs, h=h, y=y, fp8=fp8)
         return out
 
     def _empty_forward(self, x: torch.Tensor, logits: torch.Tensor, save: bool):
@@ -217,14 +262,15 @@ class SimpleMoE(nn.Module):
                      y=torch.empty((0, H), dtype=torch.bfloat16, device=dev))
         return out, inter
 
-    def _empty_backward(self, inter: dict) -> dict:
+    def _empty_backward(self, inter: dict, wgrad_dtype=torch.float32) -> dict:
         """Gradients of an empty batch: empty dx / dlogits / dtopk_w and zero
         weight gradients, with the keys ``backward_from`` returns."""
         dev, H, I = inter["x"].device, self.hidden, self.intermediate
         E, K = self.num_experts, self.top_k
         f32 = dict(dtype=torch.float32, device=dev)
+        wg = dict(dtype=wgrad_dtype, device=dev)
         out = dict(dx=torch.empty((0, H), dtype=torch.bfloat16, device=dev),
-                   dw1=torch.zeros((E, 2 * I, H), **f32), dw2=torch.zeros((E, H, I), **f32),
+                   dw1=torch.zeros((E, 2 * I, H), **wg), dw2=torch.zeros((E, H, I), **wg),
                    dtopk_w=torch.empty((0, K), **f32), dlogits=torch.empty((0, E), **f32),
                    dyq=torch.empty((0, H), dtype=ops.FP8, device=dev),
                    dys=torch.empty((0, H // ops.GROUP), **f32),
@@ -235,7 +281,9 @@ class SimpleMoE(nn.Module):
         return out
 
     @torch.no_grad()
-    def backward_from(self, inter: dict, dout: torch.Tensor) -> dict:
+    def backward_from(self, inter: dict, dout: torch.Tensor, dw1_into: torch.Tensor | None = None,
+                      dw2_into: torch.Tensor | None = None,
+                      wgrad_dtype: torch.dtype = torch.float32) -> dict:
         """Backward of one forward call given its intermediates
         (``forward(..., return_intermediates=True)``) and dout [T,H] bf16.
 
@@ -251,10 +299,27 @@ class SimpleMoE(nn.Module):
         forward computed the logits itself (x @ w_gate), dx also holds the
         gating linear's contribution and dw_gate [H,E] f32 is returned.
         Every expert stage is a HIP kernel; the gating linear's two small
-        fp32 matmuls are library GEMMs.  Nothing synchronises with the host."""
+        fp32 matmuls are library GEMMs.  Nothing synchronises with the host.
+
+        ``dw1_into`` / ``dw2_into`` (fp32 or bf16 [E,2I,H] / [E,H,I]) are
+        gradient-accumulation buffers: the wgrad kernel adds the weight
+        gradient into them in its epilogue and they are returned as dw1 /
+        dw2.  Otherwise dw1 / dw2 are new tensors of ``wgrad_dtype`` (fp32 or
+        bf16, rounded once from the fp32 sums).  The dgrad uses the
+        transposes of the fp8 weights the forward ran with."""
+        E, H, I = self.num_experts, self.hidden, self.intermediate
+        for buf, shape, name in ((dw1_into, (E, 2 * I, H), "dw1_into"), (dw2_into, (E, H, I), "dw2_into")):
+            if buf is not None and (tuple(buf.shape) != shape or buf.dtype not in (torch.float32, torch.bfloat16)
+                                    or not buf.is_contiguous() or buf.device != dout.device):
+                raise ValueError(f"{name} must be a contiguous fp32 or bf16 {list(shape)} tensor on {dout.device}")
         if inter["x"].shape[0] == 0:
-            return self._empty_backward(inter)
-        w1tq, w1ts, w2tq, w2ts = self.gemm_weights_t()
+            out = self._empty_backward(inter, wgrad_dtype)
+            if dw1_into is not None:
+                out["dw1"] = dw1_into
+            if dw2_into is not None:
+                out["dw2"] = dw2_into
+            return out
+        w1tq, w1ts, w2tq, w2ts = self.gemm_weights_t(inter.get("fp8"))
         off, inv = inter["offsets"], inter["inv_map"]
         K = self.top_k
         # The weight gradients are off the dx critical path.  They run on a
@@ -268,9 +333,10 @@ class SimpleMoE(nn.Module):
         # the returned weight gradients are allocated on the caller's stream,
         # so the caching allocator never hands their memory to side-stream
         # work while the caller still uses them
-        E, H, I = self.num_experts, self.hidden, self.intermediate
-        dw1 = torch.empty((E, 2 * I, H), dtype=torch.float32, device=dout.device)
-        dw2 = torch.empty((E, H, I), dtype=torch.float32, device=dout.device)
+        dw1 = dw1_into if dw1_into is not None else torch.empty((E, 2 * I, H), dtype=wgrad_dtype,
+                                                                device=dout.device)
+        dw2 = dw2_into if dw2_into is not None else torch.empty((E, H, I), dtype=wgrad_dtype,
+                                                                device=dout.device)
         side.wait_stream(main)
         with torch.cuda.stream(side):
             # the wgrad activation operands depend on the forward only: h, and
@@ -283,14 +349,16 @@ class SimpleMoE(nn.Module):
             dout.contiguous(), inter["y"], inv, inter["row_map"], inter["topk_w"], off)
         side.wait_stream(main)
         with torch.cuda.stream(side):
-            ops.grouped_gemm_fp8_wgrad(dyTq, dyTs, hTq, hTs, pad, ld, out=dw2)
+            ops.grouped_gemm_fp8_wgrad(dyTq, dyTs, hTq, hTs, pad, ld, out=dw2,
+                                       accumulate=dw2_into is not None)
         dh = ops.grouped_gemm_fp8(dyq, dys, w2tq, w2ts, off)
         # SwiGLU backward fused with both quantisations of dc1 (dc1 itself is
         # never stored)
         dcq, dcs, dcTq, dcTs, _, _ = ops.swiglu_bwd_quant(inter["c1"], dh, off)
         side.wait_stream(main)
         with torch.cuda.stream(side):
-            ops.grouped_gemm_fp8_wgrad(dcTq, dcTs, xTq, xTs, pad, ld, out=dw1)
+            ops.grouped_gemm_fp8_wgrad(dcTq, dcTs, xTq, xTs, pad, ld, out=dw1,
+                                       accumulate=dw1_into is not None)
         dxs = ops.grouped_gemm_fp8(dcq, dcs, w1tq, w1ts, off)
         dx = ops.unpermute_combine(dxs, inv, ones)
         # router: renormalisation + softmax backward into the logits

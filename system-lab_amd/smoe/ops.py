@@ -94,22 +94,35 @@ ROUTE_STATUS_OFFSET = 0
 _route_status: dict = {}
 
 
+def _dev_key(device) -> torch.device:
+    """A GPU device with its index filled in, so that 'cuda', 'cuda:0' and
+    torch.device('cuda', 0) name the same status entry."""
+    dev = torch.device("cuda") if device is None else torch.device(device)
+    if dev.type != "cuda":
+        raise ValueError(f"routing status is kept per GPU, got {dev}")
+    return torch.device("cuda", torch.cuda.current_device() if dev.index is None else dev.index)
+
+
 def _sort_workspace(T: int, K: int, E: int, dev) -> torch.Tensor:
     nbytes = int(_C.lib().smoe_route_sort_workspace_size(T, K, E))
     ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     # the status word of this call; check_route_status() reads it lazily
-    _route_status[dev] = ws[ROUTE_STATUS_OFFSET:ROUTE_STATUS_OFFSET + 4].view(torch.int32)
+    _route_status[_dev_key(dev)] = ws[ROUTE_STATUS_OFFSET:ROUTE_STATUS_OFFSET + 4].view(torch.int32)
     return ws
 
 
 def last_route_status(device=None) -> torch.Tensor:
     """Device int32 [1]: pairs dropped for an out-of-range expert id by the
     most recent sort on ``device`` (0 when every id was valid).  Reading it
-    does not synchronise; converting it to a Python int does."""
-    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    does not synchronise; converting it to a Python int does.  ``device``
+    may omit the index ('cuda' is the current GPU)."""
+    dev = _dev_key(device)
     if dev not in _route_status:
         raise RuntimeError(f"no routing sort has run on {dev}")
-    return _route_status[dev]
+    st = _route_status[dev]
+    # the allocation-free sort keeps its status word in library memory:
+    # its count is recovered as T*K - offsets[E] (dropped pairs get no row)
+    return st() if callable(st) else st
 
 
 def check_route_status(device=None) -> None:
@@ -120,6 +133,28 @@ def check_route_status(device=None) -> None:
     if n:
         raise ValueError(f"routing: {n} (token, slot) pairs had an expert id outside [0, E) "
                          "and were dropped")
+
+
+def route_sort_noalloc(topk_idx: torch.Tensor, row_map: torch.Tensor, inv_map: torch.Tensor,
+                       counts: torch.Tensor, offsets: torch.Tensor) -> None:
+    """``route_sort`` into caller-provided outputs through the allocation-free
+    entry point (smoe_route_sort_noalloc: the sort's workspace is a static
+    array inside the library, so nothing is allocated and the call can be
+    captured in a HIP graph).  The routing status of this call is readable
+    through ``last_route_status`` / ``check_route_status`` like any sort's.
+    Calls that overlap on one GPU share the library's array and race."""
+    _check(topk_idx, "topk_idx", (torch.int32,), 2)
+    T, K = topk_idx.shape
+    R = T * K
+    E = counts.numel()
+    for t, n, name in ((row_map, R, "row_map"), (inv_map, R, "inv_map"), (counts, E, "counts"),
+                       (offsets, E + 1, "offsets")):
+        _check(t, name, (torch.int32,), 1)
+        if t.numel() != n:
+            raise ValueError(f"{name} must have {n} entries")
+    _C.call("smoe_route_sort_noalloc", _ptr(topk_idx), T, K, E, _ptr(row_map), _ptr(inv_map),
+            _ptr(counts), _ptr(offsets), _stream())
+    _route_status[_dev_key(topk_idx.device)] = lambda: (R - offsets[E:]).to(torch.int32)
 
 
 def route_sort(topk_idx: torch.Tensor, num_experts: int):
@@ -243,10 +278,15 @@ class PackedWeight:
         return self.data.device
 
 
+PACKED_MAX_K = 65536  # the packed kernel keeps a tile's weight-scale column in LDS
+
+
 def packed_gemm_ok(N: int, Kd: int) -> bool:
     """Whether the packed GEMM covers a weight of N rows and K = Kd: it needs
-    K a multiple of 512 and N*K < 2^32 (other weights use the plain kernel)."""
-    return Kd % (4 * GROUP) == 0 and N % GROUP == 0 and N * Kd < (1 << 32)
+    K a multiple of 512 and at most 65536, and N*K < 2^32 (the same checks
+    as smoe_grouped_gemm_fp8_packed; other weights use the plain kernel)."""
+    return (Kd % (4 * GROUP) == 0 and 0 < Kd <= PACKED_MAX_K and N % GROUP == 0
+            and N * Kd < (1 << 32))
 
 
 def pack_weight_fp8(wq: torch.Tensor) -> PackedWeight:
@@ -255,8 +295,8 @@ def pack_weight_fp8(wq: torch.Tensor) -> PackedWeight:
     _check(wq, "wq", (FP8, torch.uint8), 3)
     E, N, Kd = wq.shape
     if not packed_gemm_ok(N, Kd):
-        raise ValueError(f"packed weights need K % 512 == 0, N % 128 == 0 and N*K < 2^32 "
-                         f"(N={N}, K={Kd})")
+        raise ValueError(f"packed weights need K % 512 == 0, K <= {PACKED_MAX_K}, N % 128 == 0 "
+                         f"and N*K < 2^32 (N={N}, K={Kd})")
     wp = torch.empty((E, N, Kd), dtype=torch.uint8, device=wq.device)
     _C.call("smoe_pack_weight_fp8", _ptr(_bytes(wq)), E, N, Kd, _ptr(wp), _stream())
     return PackedWeight(wp)
@@ -291,7 +331,8 @@ def grouped_gemm_fp8(xq: torch.Tensor, xs: torch.Tensor, wq: torch.Tensor, ws: t
     if Kw != Kd:
         raise ValueError(f"K mismatch: xq has {Kd}, wq has {Kw}")
     if packed and not packed_gemm_ok(N, Kd):
-        raise ValueError(f"packed weights need K % 512 == 0 and N*K < 2^32 (N={N}, K={Kd})")
+        raise ValueError(f"packed weights need K % 512 == 0, K <= {PACKED_MAX_K} and N*K < 2^32 "
+                         f"(N={N}, K={Kd})")
     if offsets.numel() != E + 1:
         raise ValueError("offsets must have E+1 entries")
     if xs.shape != (R, Kd // GROUP) or ws.shape != (E, N // GROUP, Kd // GROUP):
@@ -328,7 +369,8 @@ def grouped_gemm_fp8_swiglu(xq: torch.Tensor, xs: torch.Tensor, w1q: torch.Tenso
     if Kw != Kd:
         raise ValueError(f"K mismatch: xq has {Kd}, w1q has {Kw}")
     if packed and not packed_gemm_ok(N, Kd):
-        raise ValueError(f"packed weights need K % 512 == 0 and N*K < 2^32 (N={N}, K={Kd})")
+        raise ValueError(f"packed weights need K % 512 == 0, K <= {PACKED_MAX_K} and N*K < 2^32 "
+                         f"(N={N}, K={Kd})")
     if N % (2 * GROUP):
         raise ValueError("w1q rows must be gate | up halves of a multiple of 128 each")
     if offsets.numel() != E + 1:
@@ -493,9 +535,18 @@ def swiglu_bwd_quant(c1: torch.Tensor, dh: torch.Tensor, offsets: torch.Tensor,
     return out + (dc1,) if save_dc1 else out
 
 
-def grouped_gemm_fp8_wgrad(aTq, aTs, bTq, bTs, pad, ld: int, out: torch.Tensor | None = None) -> torch.Tensor:
+WGRAD_MODES = {(torch.float32, False): 0, (torch.float32, True): 1,
+               (torch.bfloat16, False): 2, (torch.bfloat16, True): 3}
+
+
+def grouped_gemm_fp8_wgrad(aTq, aTs, bTq, bTs, pad, ld: int, out: torch.Tensor | None = None,
+                           accumulate: bool = False, dtype=torch.float32) -> torch.Tensor:
     """dW[e] = A_e^T B_e over each expert's rows from quant_cols operands:
-    aT [N, ld], bT [K, ld] -> fp32 [E, N, K] (into ``out`` when given)."""
+    aT [N, ld], bT [K, ld] -> [E, N, K] (into ``out`` when given, else a new
+    tensor of ``dtype``, fp32 or bf16).  With ``accumulate`` the gradient is
+    added into ``out`` (fp32: one fp32 addition per value; bf16: the fp32 sum
+    rounded once), as a gradient-accumulation buffer (``main_grad``) needs;
+    experts without rows leave ``out`` untouched."""
     _check(aTq, "aTq", (FP8, torch.uint8), 2)
     _check(bTq, "bTq", (FP8, torch.uint8), 2)
     _check(aTs, "aTs", (torch.float32,), 2)
@@ -507,14 +558,19 @@ def grouped_gemm_fp8_wgrad(aTq, aTs, bTq, bTs, pad, ld: int, out: torch.Tensor |
     if tuple(aTs.shape) != (N, ld // GROUP) or tuple(bTs.shape) != (K, ld // GROUP):
         raise ValueError(f"scales must be [{N}, {ld // GROUP}] and [{K}, {ld // GROUP}]")
     if out is None:
-        dW = torch.empty((E, N, K), dtype=torch.float32, device=aTq.device)
+        if accumulate:
+            raise ValueError("accumulate needs the buffer to add into (out)")
+        if dtype not in (torch.float32, torch.bfloat16):
+            raise TypeError("the weight gradient is fp32 or bf16")
+        dW = torch.empty((E, N, K), dtype=dtype, device=aTq.device)
     else:
-        _check(out, "out", (torch.float32,), 3)
+        _check(out, "out", (torch.float32, torch.bfloat16), 3)
         if tuple(out.shape) != (E, N, K):
-            raise ValueError(f"out must be [{E}, {N}, {K}] fp32")
+            raise ValueError(f"out must be [{E}, {N}, {K}]")
         dW = out
-    _C.call("smoe_grouped_gemm_fp8_wgrad", _ptr(_bytes(aTq)), _ptr(aTs), _ptr(_bytes(bTq)),
-            _ptr(bTs), _ptr(pad), E, N, K, ld, _ptr(dW), _stream())
+    _C.call("smoe_grouped_gemm_fp8_wgrad_ex", _ptr(_bytes(aTq)), _ptr(aTs), _ptr(_bytes(bTq)),
+            _ptr(bTs), _ptr(pad), E, N, K, ld, _ptr(dW), WGRAD_MODES[(dW.dtype, bool(accumulate))],
+            _stream())
     return dW
 
 

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_strerror_covers_codes():
     lib = _C.lib()
-    for code in range(0, -8, -1):
+    for code in range(0, -9, -1):
         assert lib.smoe_strerror(code)
     assert b"unknown" in lib.smoe_strerror(-99)
 
@@ -174,3 +174,24 @@ def test_remaining_entry_points_reject():
     assert lib.smoe_selftest_quant(MIS, None) == -6
     assert lib.smoe_selftest_recip(None, None) == -1
     assert lib.smoe_selftest_recip(MIS, None) == -6
+
+
+def test_wgrad_ex_and_packed_bounds_reject():
+    """The wgrad output-mode entry rejects a mode outside SMOE_WGRAD_* and the
+    plain wgrad's bad shapes; the packed GEMM's K limit (the weight-scale
+    column of a tile lives in LDS: K <= 65536) is the same in the C check
+    and in ops.packed_gemm_ok, so SimpleMoE never packs a weight the packed
+    entry point would refuse."""
+    from smoe import ops
+    lib = _C.lib()
+    w = lib.smoe_grouped_gemm_fp8_wgrad_ex
+    assert w(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 256, 256, 1024, FAKE, 4, None) == -8
+    assert w(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 256, 256, 1024, FAKE, -1, None) == -8
+    assert w(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 100, 256, 1024, FAKE, 1, None) == -3
+    assert w(FAKE, FAKE, FAKE, FAKE, None, 4, 256, 256, 1024, FAKE, 3, None) == -1
+    p = lib.smoe_grouped_gemm_fp8_packed
+    K = 65536 + 512
+    assert not ops.packed_gemm_ok(128, K)
+    assert p(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 256, 128, K, FAKE, None) == -2
+    assert ops.packed_gemm_ok(128, 65536)
+    assert not ops.packed_gemm_ok(128, 0) and not ops.packed_gemm_ok(128, 1536 + 128)

@@ -132,6 +132,71 @@ def test_packed_config4_full(dev):
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
 
 
+def _np_u16(t):
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def _np_u8(t):
+    return t.detach().cpu().contiguous().view(torch.uint8).numpy()
+
+
+def _oracle_rows(O, aq, as_, wq, ws, rows, offs):
+    """float64 oracle GEMM restricted to the given sorted rows."""
+    aq_np, as_np = _np_u8(aq[rows]), as_[rows].cpu().numpy()
+    wq_np, ws_np = _np_u8(wq), ws.cpu().numpy()
+    rows_np = rows.cpu().numpy()
+    owner = np.searchsorted(offs, rows_np, side="right") - 1
+    ref = np.zeros((len(rows_np), wq.shape[1]), np.float64)
+    for e in np.unique(owner):
+        sel = owner == e
+        ref[sel] = O.dequant_rows(aq_np[sel], as_np[sel]) @ O.dequant_weight(wq_np[e], ws_np[e]).T
+    return ref
+
+
+def test_packed_config4_oracle_samples(dev):
+    """The packed kernel SimpleMoE runs at config 4, held to the float64 oracle
+    directly (not only through the plain kernel): rows of every non-empty
+    expert of fc1 (N=4096, K=7168) and fc2 (N=7168, K=2048), within the GEMM
+    tolerance (max 1e-2, mean 1e-3 of the bf16-rounded oracle); and the fused
+    SwiGLU epilogue's hq / hs on those rows byte-identical to the oracle's
+    swiglu_quant of the kernel's own c1 (the same input), with c1 within the
+    GEMM tolerance."""
+    from oracle import smoe_oracle as O
+
+    def gemm_close(got, ref, what):
+        ref = O.bf16_to_f32(O.f32_to_bf16(np.asarray(ref, np.float32))).astype(np.float64)
+        d = np.abs(got - ref)
+        mx, mn = d.max() / np.abs(ref).max(), d.mean() / np.abs(ref).mean()
+        assert mx <= 1e-2 and mn <= 1e-3, f"{what}: max_rel={mx:.3e} mean_rel={mn:.3e}"
+
+    say("config 4 vs oracle")
+    c = W.CONFIGS["dsv3"]
+    counts = W.zipf_counts()
+    off = W.offsets_from_counts(counts, dev)
+    offs = off.cpu().numpy()
+    R = c.T
+    inv = torch.arange(R, dtype=torch.int32, device=dev)
+    rows = torch.from_numpy(np.concatenate(
+        [np.unique(np.linspace(offs[e], offs[e + 1] - 1, 5).astype(np.int64))
+         for e in range(c.E) if counts[e] > 0])).to(dev)
+    xq, xs = ops.permute_quant_rows(W.tokens(R, c.H, device=dev), inv, 1)
+    w1q, w1s = ops.quantize_weight_blockwise(W.weights(c.E, 2 * c.I, c.H, device=dev))
+    w1p = ops.pack_weight_fp8(w1q)
+    c1 = ops.grouped_gemm_fp8(xq, xs, w1p, w1s, off)
+    ref1 = _oracle_rows(O, xq, xs, w1q, w1s, rows, offs)
+    gemm_close(O.bf16_to_f32(_np_u16(c1[rows])).astype(np.float64), ref1, "packed fc1")
+    hq, hs, c1f = ops.grouped_gemm_fp8_swiglu(xq, xs, w1p, w1s, off, save_c1=True)
+    assert torch.equal(c1f[rows].view(torch.int16), c1[rows].view(torch.int16))
+    rq, rs = O.swiglu_quant(_np_u16(c1f[rows]))
+    assert np.array_equal(_np_u8(hq[rows]), rq) and np.array_equal(hs[rows].cpu().numpy(), rs)
+    del xq, xs, w1q, w1p, c1, c1f
+    torch.cuda.empty_cache()
+    w2q, w2s = ops.quantize_weight_blockwise(W.weights(c.E, c.H, c.I, device=dev, seed=13))
+    y = ops.grouped_gemm_fp8(hq, hs, ops.pack_weight_fp8(w2q), w2s, off)
+    ref2 = _oracle_rows(O, hq, hs, w2q, w2s, rows, offs)
+    gemm_close(O.bf16_to_f32(_np_u16(y[rows])).astype(np.float64), ref2, "packed fc2")
+
+
 def test_packed_validation(dev):
     say("validation")
     off, xq, xs, wq, ws = _operands(dev, [100, 50], 256, 640)

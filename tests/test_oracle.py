@@ -388,6 +388,64 @@ def test_swiglu_bwd_matches_float64_derivative():
     assert np.abs(ref[:, :256] - num).max() <= 1e-6 * np.abs(num).max() + 1e-9
 
 
+def test_combine_bwd_against_float64_autograd_and_identities():
+    """combine_bwd pinned on its own: dw and the unrounded dy are the
+    gradients float64 autograd takes through the combine's definition
+    out[t] = sum_k w[t,k] * y[inv_map[t*K+k]] (the forward C7 restates,
+    pinned by test_combine_identity_and_scalar_loop); dy is that gradient
+    rounded once to bf16; dw is linear in dout; and the adjoint identity
+    <combine(y, w), dout> = sum(w * dw) holds in float64."""
+    rng = np.random.default_rng(71)
+    T, K, H = 37, 3, 256
+    R = T * K
+    inv = rng.permutation(R).astype(np.int32)
+    y = O.f32_to_bf16(rng.standard_normal((R, H)).astype(np.float32))
+    d1 = O.f32_to_bf16(rng.standard_normal((T, H)).astype(np.float32))
+    d2 = O.f32_to_bf16(rng.standard_normal((T, H)).astype(np.float32))
+    w = rng.random((T, K)).astype(np.float32)
+    dy, dw = O.combine_bwd(d1, y, inv, w, K)
+    yt = torch.from_numpy(O.bf16_to_f32(y).astype(np.float64)).requires_grad_(True)
+    wt = torch.from_numpy(w.astype(np.float64)).requires_grad_(True)
+    out = (wt[:, :, None] * yt[torch.from_numpy(inv.astype(np.int64)).view(T, K)]).sum(1)
+    dt = torch.from_numpy(O.bf16_to_f32(d1).astype(np.float64))
+    (out * dt).sum().backward()
+    assert np.allclose(dw, wt.grad.numpy(), rtol=1e-12, atol=1e-12)
+    # dy: the autograd gradient (exact in fp32: one product of a bf16 and an
+    # fp32 value) rounded once to bf16
+    g32 = yt.grad.numpy().astype(np.float32)
+    assert np.array_equal(dy, O.f32_to_bf16(g32))
+    # linearity in dout
+    _, dw2 = O.combine_bwd(d2, y, inv, w, K)
+    d12 = O.f32_to_bf16((O.bf16_to_f32(d1) + 2 * O.bf16_to_f32(d2)).astype(np.float32))
+    _, dw12 = O.combine_bwd(d12, y, inv, w, K)
+    ref12 = np.einsum("th,tkh->tk", O.bf16_to_f32(d12).astype(np.float64),
+                      O.bf16_to_f32(y).astype(np.float64)[inv.reshape(T, K)])
+    assert np.allclose(dw12, ref12, rtol=1e-12, atol=1e-10)
+    exact12 = O.bf16_to_f32(d12) == O.bf16_to_f32(d1) + 2 * O.bf16_to_f32(d2)
+    if exact12.all():
+        assert np.allclose(dw12, dw + 2 * dw2, rtol=1e-10, atol=1e-10)
+    # adjoint identity, with out in float64 from the definition
+    lhs = float((out.detach() * dt).sum())
+    assert abs(lhs - float((w.astype(np.float64) * dw).sum())) <= 1e-9 * max(1.0, abs(lhs))
+
+
+def test_combine_bwd_k1_unit_weight_is_inverse_scatter():
+    """K = 1, w = 1: dy is dout scattered through inv_map, byte for byte, and
+    dw[t] = <dout[t], y[inv_map[t]]> exactly in float64 (bf16 products are
+    exact there)."""
+    rng = np.random.default_rng(72)
+    T, H = 301, 384
+    inv = rng.permutation(T).astype(np.int32)
+    y = O.f32_to_bf16(rng.standard_normal((T, H)).astype(np.float32))
+    d = O.f32_to_bf16(rng.standard_normal((T, H)).astype(np.float32))
+    dy, dw = O.combine_bwd(d, y, inv, np.ones((T, 1), np.float32), 1)
+    want = np.zeros_like(dy)
+    want[inv] = d
+    assert np.array_equal(dy, want)
+    prod = O.bf16_to_f32(d).astype(np.float64) * O.bf16_to_f32(y).astype(np.float64)[inv]
+    assert np.array_equal(dw[:, 0], prod.sum(1))
+
+
 def test_moe_backward_against_float64_autograd():
     """The whole backward against torch autograd in float64 on the
     dequantised weights with the same routing: quantisation noise only."""

@@ -71,3 +71,35 @@ def test_noalloc_sort_rejects_oversized(dev):
     FAKE = 0x100000  # never dereferenced: rejected before any launch
     st = lib.smoe_route_sort_noalloc(FAKE, T, K, E, FAKE, FAKE, FAKE, FAKE, None)
     assert st == -5
+
+
+def test_noalloc_sort_status_readable(dev):
+    """Out-of-range ids through the allocation-free sort: the maps equal the
+    workspace sort's, and the routing status (pairs dropped) is readable
+    through ops.last_route_status / check_route_status, also with an
+    index-less device name."""
+    from smoe import ops
+    g = torch.Generator(device="cpu").manual_seed(23)
+    T, K, E = 1000, 4, 16
+    idx = torch.randint(0, E, (T, K), generator=g, dtype=torch.int32)
+    bad = torch.randperm(T * K, generator=g)[:37]
+    idx.view(-1)[bad[:20]] = E + 3
+    idx.view(-1)[bad[20:]] = -1
+    idx = idx.to(dev)
+    say("noalloc sort status", T, K, E)
+    ref = ops.route_sort(idx, E)
+    got = _outs(T, K, E, dev)
+    ops.route_sort_noalloc(idx, *got)
+    # rows past offsets[E] belong to no pair and are left unwritten
+    assert int(ref[3][-1]) == T * K - 37
+    assert torch.equal(ref[0][:T * K - 37], got[0][:T * K - 37])
+    assert bool((got[0][T * K - 37:] == -7).all())
+    for n, r, g_ in zip(("inv_map", "counts", "offsets"), ref[1:], got[1:]):
+        assert torch.equal(r, g_), n
+    assert int(ops.last_route_status("cuda").item()) == 37
+    assert int(ops.last_route_status(torch.device("cuda", torch.cuda.current_device())).item()) == 37
+    with pytest.raises(ValueError, match="37"):
+        ops.check_route_status()
+    # a clean call clears it
+    ops.route_sort_noalloc(idx.clamp(0, E - 1), *got)
+    assert int(ops.last_route_status().item()) == 0
