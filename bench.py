@@ -334,13 +334,48 @@ def bench_fwd_bwd(dev, steps, warmup):
     with torch.cuda.graph(graph):
         step()
     tg = timed_median(graph.replay, steps, warmup)
+    del graph
     R = c.T * c.K
     fwd = 2.0 * R * (2 * c.I) * c.H + 2.0 * R * c.H * c.I
-    del graph, m
+    tf = lambda ms: round(3 * fwd / (ms * 1e-3) / 1e12, 1)
+    out = {"workload": "qwen3 layer fwd+bwd T=16384 H=2048 I=768 E=128 top8",
+           "ms": round(t, 4), "tflops": tf(t), "ms_graph": round(tg, 4), "tflops_graph": tf(tg)}
+    # The training path a framework runs: loss.backward() through the
+    # autograd node (x a leaf that needs its gradient, as a layer input
+    # does), with the parameters' gradients reset each step.  Without
+    # main_grad the bf16 parameters receive bf16 weight gradients written by
+    # the wgrad kernel; with fp32 main_grad buffers (Megatron's gradient
+    # accumulation) the wgrad kernel adds into them.  The last figure is the
+    # same accumulation done the unfused way: fp32 gradients, then add_.
+    xg = x.detach().clone().requires_grad_(True)
+
+    def train_step():
+        m.zero_grad(set_to_none=True)
+        xg.grad = None
+        m(xg, lg).backward(dout)
+
+    ta = timed_median(train_step, steps, warmup)
+    m.w1.main_grad = torch.zeros(m.w1.shape, dtype=torch.float32, device=dev)
+    m.w2.main_grad = torch.zeros(m.w2.shape, dtype=torch.float32, device=dev)
+    tm = timed_median(train_step, steps, warmup)
+
+    def unfused_step():
+        xg.grad = None
+        _, st = m(xg.detach(), lg, return_intermediates=True)
+        g = m.backward_from(st, dout)
+        m.w1.main_grad.add_(g["dw1"])
+        m.w2.main_grad.add_(g["dw2"])
+
+    tu = timed_median(unfused_step, steps, warmup)
+    del m.w1.main_grad, m.w2.main_grad, m
     torch.cuda.empty_cache()
-    return {"workload": "qwen3 layer fwd+bwd T=16384 H=2048 I=768 E=128 top8",
-            "ms": round(t, 4), "tflops": round(3 * fwd / (t * 1e-3) / 1e12, 1),
-            "ms_graph": round(tg, 4), "tflops_graph": round(3 * fwd / (tg * 1e-3) / 1e12, 1)}
+    out.update({"ms_autograd": round(ta, 4), "tflops_autograd": tf(ta),
+                "ms_autograd_main_grad": round(tm, 4), "tflops_autograd_main_grad": tf(tm),
+                "ms_main_grad_unfused_add": round(tu, 4),
+                "autograd_note": "loss.backward() through SimpleMoE, grads reset per step; "
+                                 "main_grad = fp32 buffers accumulated in the wgrad epilogue; "
+                                 "unfused = fp32 dW then main_grad.add_"})
+    return out
 
 
 def bench_ceiling(dev, c, iters=20):

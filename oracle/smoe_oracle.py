@@ -23,6 +23,11 @@ and is binding for the kernels too:
   C6 SwiGLU: h = silu(g)*u in fp32, g = c1[:, :I], u = c1[:, I:]; C3 on h.
   C7 combine: out[t] = bf16(sum_k w[t,k]*y[inv_map[t*K+k]]), fp32, k order,
      each product and sum rounded separately.
+  C9 short groups: a dimension D that is not a multiple of 128 (D % 16 == 0,
+     e.g. GPT-OSS H = I = 2880) is quantised as the operand zero-padded to
+     pad128(D): a short last group's amax is over its valid elements, its
+     padding is byte 0, fp8 operands keep the padded pitch, and a short last
+     weight block (rows or columns) is the zero-padded block.
 
 Floating-point evaluation order is part of the contract where a kernel is
 bit-exact (router softmax reduction tree, exp routine, combine order): the
@@ -38,7 +43,13 @@ Pinning (what checks each function; tests/test_oracle.py):
                    (moe/MoE_detailed_computation_dataflow.md:74-122, counts
                    [5,4,5,4,3,4,4,3]); permutation/stability invariants;
                    brute-force python counting sort.
-  quant_1x128      closed forms (one-hot, constant, amax==0, +-448 saturation).
+  quant_1x128      closed forms (one-hot, constant, amax==0, +-448 saturation);
+                   C9: full groups equal the aligned prefix's bytes, the short
+                   group's scale is its valid amax / 448, padding is 0.
+  quantize_weight  C9: edge blocks equal the full-width restatement on the
+                   aligned part; scales of short blocks from their valid
+                   elements; transpose_blockwise against an explicit
+                   dequantise-and-transpose.
   grouped_gemm     one-hot rows, identity blocks, single non-zero K block,
                    zero-token experts, float64 dense matmul of the dequantised
                    operands computed per expert independently.
@@ -293,11 +304,22 @@ def route_sort(topk_idx: np.ndarray, E: int):
 # ---------------------------------------------------------------------------
 
 
+def pad128(d: int) -> int:
+    """C9: a dimension that is not a multiple of 128 is quantised as if
+    zero-padded to the next multiple of 128 (zeros never raise an amax and
+    quantise to byte 0); fp8 operands keep that padded pitch."""
+    return -(-int(d) // GROUP) * GROUP
+
+
 def quant_1x128(x: np.ndarray):
-    """C3 on rows of x [M, H] float32 (H % 128 == 0) -> q [M,H] u8, s [M,H/128] f32.
+    """C3 on rows of x [M, H] float32 -> q [M,Hp] u8, s [M,Hp/128] f32 with
+    Hp = pad128(H) (C9: a short last group is the zero-padded group).
     1x128 activation tiles: moe/MegatronCore_MoE_reading_notes.md:498-501."""
     x = np.asarray(x, np.float32)
     M, H = x.shape
+    if H % GROUP:
+        x = np.concatenate([x, np.zeros((M, pad128(H) - H), np.float32)], axis=1)
+        H = x.shape[1]
     g = x.reshape(M, H // GROUP, GROUP)
     amax = np.abs(g).max(axis=2)
     s = group_scale(amax)
@@ -312,8 +334,8 @@ def permute_quant(x_bf16: np.ndarray, inv_map: np.ndarray, K: int):
     T, H = x.shape
     q, s = quant_1x128(x)
     R = T * K
-    xq = np.empty((R, H), np.uint8)
-    xs = np.empty((R, H // GROUP), np.float32)
+    xq = np.empty((R, q.shape[1]), np.uint8)
+    xs = np.empty((R, s.shape[1]), np.float32)
     dst = np.asarray(inv_map, np.int64).reshape(T, K)
     for k in range(K):
         xq[dst[:, k]] = q
@@ -323,14 +345,18 @@ def permute_quant(x_bf16: np.ndarray, inv_map: np.ndarray, K: int):
 
 def quantize_weight_blockwise(w_bf16: np.ndarray):
     """C4: 128x128 blocks of W[e] in [N, K] layout (summary/fp8_expert_gemm_optimization.md:137)
-    -> wq [E,N,K] u8, ws [E,N/128,K/128] f32."""
+    -> wq [E,N,Kp] u8, ws [E,Np/128,Kp/128] f32 with Np, Kp = pad128(N, K):
+    per C9 edge blocks are the zero-padded blocks, and wq keeps N rows."""
     w = bf16_to_f32(w_bf16)
     E, N, Kd = w.shape
-    b = w.reshape(E, N // GROUP, GROUP, Kd // GROUP, GROUP)
+    Np, Kp = pad128(N), pad128(Kd)
+    if (Np, Kp) != (N, Kd):
+        w = np.pad(w, ((0, 0), (0, Np - N), (0, Kp - Kd)))
+    b = w.reshape(E, Np // GROUP, GROUP, Kp // GROUP, GROUP)
     amax = np.abs(b).max(axis=(2, 4))
     s = group_scale(amax)
-    q = quant_rule(b, s[:, :, None, :, None]).reshape(E, N, Kd)
-    return q, s
+    q = quant_rule(b, s[:, :, None, :, None]).reshape(E, Np, Kp)[:, :N]
+    return np.ascontiguousarray(q), s
 
 
 # ---------------------------------------------------------------------------
@@ -346,10 +372,15 @@ def dequant_rows(q: np.ndarray, s: np.ndarray) -> np.ndarray:
 
 
 def dequant_weight(q: np.ndarray, s: np.ndarray) -> np.ndarray:
-    """[N,K] fp8 with [N/128,K/128] scales -> float64."""
+    """[N,K] fp8 with [ceil(N/128),K/128] scales -> float64 (K the padded
+    pitch; a short last row block uses its block's scale)."""
     N, Kd = q.shape
-    v = e4m3_decode(q).astype(np.float64).reshape(N // GROUP, GROUP, Kd // GROUP, GROUP)
-    return (v * s.astype(np.float64)[:, None, :, None]).reshape(N, Kd)
+    Np = pad128(N)
+    v = e4m3_decode(q).astype(np.float64)
+    if Np != N:
+        v = np.concatenate([v, np.zeros((Np - N, Kd))], axis=0)
+    v = v.reshape(Np // GROUP, GROUP, Kd // GROUP, GROUP)
+    return (v * s.astype(np.float64)[:, None, :, None]).reshape(Np, Kd)[:N]
 
 
 def grouped_gemm_fp8(a, a_s, b, b_s, offsets) -> np.ndarray:
@@ -441,11 +472,17 @@ def moe_forward(x_bf16, logits, w1q, w1s, w2q, w2s, K, bias=None):
 # ---------------------------------------------------------------------------
 
 
-def transpose_blockwise(wq: np.ndarray, ws: np.ndarray):
-    """[E,N,K] fp8 + [E,N/128,K/128] scales -> [E,K,N] + [E,K/128,N/128].
+def transpose_blockwise(wq: np.ndarray, ws: np.ndarray, k: int | None = None):
+    """[E,N,Kp] fp8 + [E,NB,KB] scales -> [E,K,Np] + [E,KB,NB], with K = k
+    (default Kp) and Np = pad128(N) (C9 padding: zero columns past N).
     128x128 block quantisation commutes with the transpose, so the dgrad
     weights are the forward bytes transposed (no requantisation)."""
-    return np.ascontiguousarray(wq.transpose(0, 2, 1)), np.ascontiguousarray(ws.transpose(0, 2, 1))
+    E, N, Kp = wq.shape
+    Kd = Kp if k is None else int(k)
+    full = np.zeros((E, pad128(N), Kp), np.uint8)
+    full[:, :N] = wq
+    return (np.ascontiguousarray(full.transpose(0, 2, 1)[:, :Kd]),
+            np.ascontiguousarray(ws.transpose(0, 2, 1)))
 
 
 def pad_offsets(offsets: np.ndarray) -> np.ndarray:

@@ -9,19 +9,24 @@ namespace smoe {
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
 // ------------------------------------------------------ weight transpose
-// [E, N, K] fp8 -> [E, K, N].  One 256-thread workgroup per 64x64-byte tile:
-// each thread loads 16 bytes of a source row into LDS (row stride 80 bytes
-// keeps the column reads spread over banks), then assembles 16 bytes of a
-// destination row from 16 LDS bytes of one source column.
+// [E, N, Kp] fp8 (Kp = pad128(Kd), columns past Kd zero) -> [E, Kd, Np]
+// (Np = pad128(N), columns past N zero).  One 256-thread workgroup per
+// 64x64-byte tile: each thread loads 16 bytes of a source row into LDS (row
+// stride 80 bytes keeps the column reads spread over banks; source rows past
+// N read as zeros), then assembles 16 bytes of a destination row from 16 LDS
+// bytes of one source column (destination rows past Kd are not written).
 __global__ __launch_bounds__(256) void transpose_fp8_kernel(const uint8_t* __restrict__ src,
                                                             int N, int Kd,
                                                             uint8_t* __restrict__ dst) {
   __shared__ uint8_t tile[64][80];
+  const int Kp = pad128(Kd), Np = pad128(N);
   const int tk = blockIdx.x, tn = blockIdx.y, e = blockIdx.z;
   const int t = threadIdx.x;
   const int r = t >> 2, c16 = (t & 3) * 16;
-  const uint8_t* s = src + ((size_t)e * N + tn * 64 + r) * Kd + tk * 64 + c16;
-  *(uint4*)&tile[r][c16] = *(const uint4*)s;
+  const int n = tn * 64 + r;
+  uint4 v = make_uint4(0, 0, 0, 0);
+  if (n < N) v = *(const uint4*)(src + ((size_t)e * N + n) * Kp + tk * 64 + c16);
+  *(uint4*)&tile[r][c16] = v;
   __syncthreads();
   // destination row k = tk*64 + r, columns n = tn*64 + c16 .. +16
   uint32_t w[4];
@@ -30,8 +35,9 @@ __global__ __launch_bounds__(256) void transpose_fp8_kernel(const uint8_t* __res
     w[q] = (uint32_t)tile[c16 + 4 * q][r] | ((uint32_t)tile[c16 + 4 * q + 1][r] << 8) |
            ((uint32_t)tile[c16 + 4 * q + 2][r] << 16) | ((uint32_t)tile[c16 + 4 * q + 3][r] << 24);
   }
-  *(uint4*)(dst + ((size_t)e * Kd + tk * 64 + r) * N + tn * 64 + c16) =
-      make_uint4(w[0], w[1], w[2], w[3]);
+  const int k = tk * 64 + r;
+  if (k < Kd)
+    *(uint4*)(dst + ((size_t)e * Kd + k) * Np + tn * 64 + c16) = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
 // [E, NB, KB] f32 -> [E, KB, NB]
@@ -174,7 +180,7 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(
         row_m[r] = qd.m;
         row_r[r] = qd.r;
         row_e[r] = qd.e;
-        if (r < valid) sr[(size_t)(row0 + r) * (C / kGroup) + c0 / kGroup] = sc;
+        if (r < valid) sr[(size_t)(row0 + r) * (pad128(C) / kGroup) + c0 / kGroup] = sc;
       }
     }
     __syncthreads();
@@ -187,7 +193,7 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(
       col_m[t] = qd.m;
       col_r[t] = qd.r;
       col_e[t] = qd.e;
-      s[(size_t)(c0 + t) * (ld / kGroup) + gpos / kGroup] = sc;
+      if (c0 + t < C) s[(size_t)(c0 + t) * (ld / kGroup) + gpos / kGroup] = sc;
     }
     __syncthreads();
     QDiv d[8];
@@ -197,10 +203,12 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(
       d[i].r = col_r[cc + i];
       d[i].e = col_e[cc + i];
     }
-    // column c0+cc+i gets bytes for rows gpos + rg*8 .. +8
+    // column c0+cc+i gets bytes for rows gpos + rg*8 .. +8 (columns past C
+    // have no output row)
     uint8_t* dst = q + (size_t)(c0 + cc) * ld + gpos + rg * 8;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
+      if (c0 + cc >= C) break;
       float qv[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -228,7 +236,7 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(
           qv[2 * i] = quot_bf16(__uint_as_float(wd[i] << 16), rd);
           qv[2 * i + 1] = quot_bf16(__uint_as_float(wd[i] & 0xffff0000u), rd);
         }
-        *(uint2*)(qr + (size_t)(row0 + r) * C + c0 + cc) =
+        *(uint2*)(qr + (size_t)(row0 + r) * pad128(C) + c0 + cc) =
             make_uint2(e4m3_pack4(qv[0], qv[1], qv[2], qv[3]), e4m3_pack4(qv[4], qv[5], qv[6], qv[7]));
       }
     }
@@ -286,6 +294,10 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(
     v4u v[8];
     float wv[8];
     const int c0 = blockIdx.x * kQcCols;
+    // a thread whose 8 columns lie past C (C % 128 != 0) reads column 0 and
+    // is zeroed below, like a row outside the group
+    const bool col_ok = c0 + cc < C;
+    const int ccl = col_ok ? c0 + cc : 0;
     // Loads are unconditional (out-of-group rows re-read the group's last
     // row, or row 0 when the group is empty) and zeroed by selects after, so
     // no control flow separates them and all 8 are in flight at once.
@@ -306,7 +318,7 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(
         src[j] = (unsigned)src[j] < (unsigned)R ? src[j] : 0;
       }
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = *(const v4u*)(x + (size_t)(src[j] / gather_div) * C + c0 + cc);
+      for (int j = 0; j < 8; ++j) v[j] = *(const v4u*)(x + (size_t)(src[j] / gather_div) * C + ccl);
       if (gather_w) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) wv[j] = gather_w[src[j]];
@@ -315,7 +327,7 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         ok[j] = rg * 8 + j < valid;
-        v[j] = __builtin_nontemporal_load((const v4u*)(x + (size_t)src[j] * C + c0 + cc));
+        v[j] = __builtin_nontemporal_load((const v4u*)(x + (size_t)src[j] * C + ccl));
       }
     }
     if (gather && gather_w) {
@@ -328,10 +340,11 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(
           v[j][i] = bf16_pack2(wv[j] * __uint_as_float(v[j][i] << 16),
                                wv[j] * __uint_as_float(v[j][i] & 0xffff0000u));
     }
-    // rows outside the group are +0 (after the weights: w * +0 can be -0)
+    // rows outside the group and columns past C are +0 (after the weights:
+    // w * +0 can be -0)
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      if (!ok[j]) v[j] = v4u{0u, 0u, 0u, 0u};
+      if (!ok[j] || !col_ok) v[j] = v4u{0u, 0u, 0u, 0u};
     quantize(v, c0);
   }
 }
@@ -471,16 +484,17 @@ extern "C" int smoe_transpose_blockwise_fp8(const uint8_t* wq, const float* ws, 
                                             int Kdim, uint8_t* wqT, float* wsT, void* stream) {
   if (N <= 0 || Kdim <= 0) return SMOE_EINVAL_DIM;
   if (E <= 0 || E > SMOE_MAX_EXPERTS) return SMOE_EINVAL_EXPERTS;
-  if (N % kGroup || Kdim % kGroup) return SMOE_EINVAL_ALIGN128;
+  if (N % kLane || Kdim % kLane) return SMOE_EINVAL_ALIGN128;
   SMOE_CHECK_PTR(wq);
   SMOE_CHECK_PTR(wqT);
   if (!ws || !wsT) return SMOE_EINVAL_NULL;
   if (((uintptr_t)ws | (uintptr_t)wsT) & 3u) return SMOE_EINVAL_PTRALIGN;
   hipStream_t s = (hipStream_t)stream;
-  transpose_fp8_kernel<<<dim3(Kdim / 64, N / 64, E), dim3(256), 0, s>>>(wq, N, Kdim, wqT);
-  const long long ns = (long long)E * (N / kGroup) * (Kdim / kGroup);
+  const int NB = pad128(N) / kGroup, KB = pad128(Kdim) / kGroup;
+  transpose_fp8_kernel<<<dim3(KB * 2, NB * 2, E), dim3(256), 0, s>>>(wq, N, Kdim, wqT);
+  const long long ns = (long long)E * NB * KB;
   transpose_scales_kernel<<<dim3((unsigned)((ns + 255) / 256)), dim3(256), 0, s>>>(
-      ws, E, N / kGroup, Kdim / kGroup, wsT);
+      ws, E, NB, KB, wsT);
   SMOE_RETURN_LAUNCH();
 }
 
@@ -497,7 +511,7 @@ extern "C" int smoe_quant_cols_128x1(const uint16_t* x, const int32_t* gather, i
   if (gather && gather_div <= 0) return SMOE_EINVAL_DIM;
   if (gather && ((uintptr_t)gather & 3u)) return SMOE_EINVAL_PTRALIGN;
   if (E <= 0 || E > SMOE_MAX_EXPERTS) return SMOE_EINVAL_EXPERTS;
-  if (C % kGroup) return SMOE_EINVAL_ALIGN128;
+  if (C % kLane) return SMOE_EINVAL_ALIGN128;
   if (ld < smoe_quant_cols_ld(R, E) || ld % kGroup) return SMOE_EINVAL_DIM;
   if (ld / kGroup > 65535) return SMOE_EINVAL_DIM;  // 128-row groups are grid.y
   SMOE_CHECK_PTR(x);
@@ -518,7 +532,7 @@ extern "C" int smoe_quant_rows_cols(const uint16_t* x, int R, int C, const int32
                                     int32_t* pad, void* stream) {
   if (R <= 0 || C <= 0) return SMOE_EINVAL_DIM;
   if (E <= 0 || E > SMOE_MAX_EXPERTS) return SMOE_EINVAL_EXPERTS;
-  if (C % kGroup) return SMOE_EINVAL_ALIGN128;
+  if (C % kLane) return SMOE_EINVAL_ALIGN128;
   if (ld < smoe_quant_cols_ld(R, E) || ld % kGroup) return SMOE_EINVAL_DIM;
   if (ld / kGroup > 65535) return SMOE_EINVAL_DIM;
   SMOE_CHECK_PTR(x);

@@ -16,6 +16,13 @@ namespace smoe {
 
 constexpr int kWave = 64;
 constexpr int kGroup = 128;  // quantisation group / weight block edge
+constexpr int kLane = 16;    // elements per lane in the row quantisers
+
+// A dimension D that is not a multiple of 128 is quantised as if it were
+// zero-padded to pad128(D): the last group's amax is over its valid
+// elements (zeros never raise it), its padding quantises to byte 0, and the
+// fp8 operand keeps a row pitch of pad128(D).  D must be a multiple of 16.
+__host__ __device__ constexpr int pad128(int d) { return (d + kGroup - 1) / kGroup * kGroup; }
 constexpr float kE4M3Max = 448.0f;
 
 // ---------------------------------------------------------------- bf16 ----

@@ -264,12 +264,13 @@ __global__ __launch_bounds__(C::kThreads, 1) void grouped_gemm_fp8_kernel(
   // on): a compiler-visible global load inside the K loop would make the
   // compiler drain vmcnt to zero, i.e. wait for every DMA stage in flight.
   constexpr int kNB128 = kBN / kGroup;
+  const int NB = (N + kGroup - 1) / kGroup;  // weight-scale blocks per expert (last may be short)
   float* sbt = (float*)mstart;
   __syncthreads();
   for (int i = tid; i < kNB128 * ksb; i += kThreads) {
     const int nb = i / ksb, kb = i - nb * ksb;
-    const int blk = kSwiGLU ? (nb == 0 ? nt : I / kGroup + nt) : min(n0 / kGroup + nb, N / kGroup - 1);
-    sbt[i] = bs[((size_t)e * (N / kGroup) + blk) * ksb + kb];
+    const int blk = kSwiGLU ? (nb == 0 ? nt : I / kGroup + nt) : min(n0 / kGroup + nb, NB - 1);
+    sbt[i] = bs[((size_t)e * NB + blk) * ksb + kb];
   }
   __syncthreads();
   const float* sb_row = sbt + ((wn * 64) / kGroup) * ksb;
@@ -403,7 +404,8 @@ extern "C" int smoe_grouped_gemm_fp8(const uint8_t* a, const float* as, const ui
   (void)ws; (void)ws_bytes;
   if (R <= 0 || N <= 0 || Kdim <= 0) return SMOE_EINVAL_DIM;
   if (E <= 0 || E > SMOE_MAX_EXPERTS) return SMOE_EINVAL_EXPERTS;
-  if (N % kGroup || Kdim % kGroup) return SMOE_EINVAL_ALIGN128;
+  // K is the operands' padded pitch; N may end in a partial weight block
+  if (N % kLane || Kdim % kGroup) return SMOE_EINVAL_ALIGN128;
   if (Kdim > 65536) return SMOE_EINVAL_DIM;  // weight-scale table fits the LDS expert table
   SMOE_CHECK_PTR(a);
   SMOE_CHECK_PTR(b);

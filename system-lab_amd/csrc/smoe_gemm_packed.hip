@@ -240,13 +240,14 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_fp8_packed_kernel(
   load_b(min(1, ksb - 1), fB);
   // the tile's weight-block scales go to LDS (the expert table's space)
   constexpr int kNB128 = kBN / kGroup;
+  const int NB = (N + kGroup - 1) / kGroup;  // weight-scale blocks per expert (last may be short)
   float* sbt = (float*)mstart;
   __syncthreads();
   for (int i = tid; i < kNB128 * ksb; i += kThreads) {
     const int nb = i / ksb, kb = i - nb * ksb;
     const int blk = kSwiGLU ? (nb == 0 ? nt : I / kGroup + nt)
-                            : min(n0 / kGroup + nb, N / kGroup - 1);
-    sbt[i] = bs[((size_t)e * (N / kGroup) + blk) * ksb + kb];
+                            : min(n0 / kGroup + nb, NB - 1);
+    sbt[i] = bs[((size_t)e * NB + blk) * ksb + kb];
   }
   __syncthreads();
   const float* sb_row = sbt + ((wid * 32) / kGroup) * ksb;
@@ -396,7 +397,7 @@ extern "C" int smoe_pack_weight_fp8(const uint8_t* wq, int E, int N, int Kdim, u
                                     void* stream) {
   if (N <= 0 || Kdim <= 0) return SMOE_EINVAL_DIM;
   if (E <= 0 || E > SMOE_MAX_EXPERTS) return SMOE_EINVAL_EXPERTS;
-  if (N % kGroup || Kdim % kGroup) return SMOE_EINVAL_ALIGN128;
+  if (N % kLane || Kdim % kGroup) return SMOE_EINVAL_ALIGN128;
   SMOE_CHECK_PTR(wq);
   SMOE_CHECK_PTR(wp);
   const long long slots = (long long)E * N * Kdim / 16;
@@ -410,7 +411,7 @@ int packed_args(const uint8_t* a, const float* as, const uint8_t* wp, const floa
                 const int32_t* offsets, int E, int R, int N, int Kdim) {
   if (R <= 0 || N <= 0 || Kdim <= 0) return SMOE_EINVAL_DIM;
   if (E <= 0 || E > SMOE_MAX_EXPERTS) return SMOE_EINVAL_EXPERTS;
-  if (N % kGroup || Kdim % (4 * kBK)) return SMOE_EINVAL_ALIGN128;  // K: a multiple of 512
+  if (N % kLane || Kdim % (4 * kBK)) return SMOE_EINVAL_ALIGN128;  // K: a multiple of 512
   if (Kdim > 65536) return SMOE_EINVAL_DIM;  // weight-scale table fits the LDS expert table
   if ((long long)N * Kdim >= (1LL << 32)) return SMOE_EINVAL_DIM;  // 32-bit weight offsets
   SMOE_CHECK_PTR(a);

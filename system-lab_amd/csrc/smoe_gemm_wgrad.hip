@@ -341,7 +341,9 @@ extern "C" int smoe_grouped_gemm_fp8_wgrad_ex(const uint8_t* aT, const float* aT
                                               void* dW, int mode, void* stream) {
   if (N <= 0 || Kdim <= 0 || ld <= 0) return SMOE_EINVAL_DIM;
   if (E <= 0 || E > SMOE_MAX_EXPERTS) return SMOE_EINVAL_EXPERTS;
-  if (N % kGroup || Kdim % kGroup || ld % kGroup) return SMOE_EINVAL_ALIGN128;
+  // N and Kdim (the operands' rows, dW's edges) need only whole 16-row MFMA
+  // blocks: tiles past them are clamped on load and masked on store
+  if (N % 16 || Kdim % 16 || ld % kGroup) return SMOE_EINVAL_ALIGN128;
   if ((long long)kWN * ld >= (1LL << 31)) return SMOE_EINVAL_DIM;
   if (mode < kOutF32 || mode > kOutBF16Acc) return SMOE_EINVAL_MODE;
   SMOE_CHECK_PTR(aT);

@@ -9,6 +9,12 @@
 // kUnroll*32 bytes in flight.  Each lane writes its 16 fp8 bytes as one
 // 128-bit store, and the first lane of each group writes the group's scale.
 //
+// A row of H bf16 values whose H is not a multiple of 128 (H % 16 == 0) is
+// quantised as the row zero-padded to Hp = pad128(H): lanes past H load
+// nothing (a clamped address, zeroed), take part in the group amax as zeros
+// and write zero bytes, so the fp8 row has pitch Hp and its last group's
+// scale is set by its valid elements.
+//
 // permute_quant reads a token row once and writes the same bytes to the K
 // sorted rows inv_map[t*K + k]: the algorithmic minimum of one read of x and
 // K writes of the fp8 row.  Rows of up to 8192 elements use the whole-row
@@ -38,7 +44,8 @@ __global__ __launch_bounds__(256) void permute_quant_kernel(
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
-  const int G = H / kGroup;
+  const int Hp = pad128(H);
+  const int G = Hp / kGroup;
   const int R = T * K;
   const int sub = lane & 7, gl = lane >> 3;
   // destination rows: lane k holds inv_map[t*K + k]
@@ -50,8 +57,9 @@ __global__ __launch_bounds__(256) void permute_quant_kernel(
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const int g = (c0 + u) * 8 + gl;
-      if (g < G) {
-        const uint4* src = (const uint4*)(xrow + g * kGroup + sub * 16);
+      const int col = g * kGroup + sub * kLane;
+      if (g < G && col < H) {
+        const uint4* src = (const uint4*)(xrow + col);
         v[u][0] = src[0];
         v[u][1] = src[1];
       } else {
@@ -73,7 +81,7 @@ __global__ __launch_bounds__(256) void permute_quant_kernel(
       for (int u = 0; u < kUnroll; ++u) {
         const int g = (c0 + u) * 8 + gl;
         if (g < G) {
-          store16<kNT>(xq + (size_t)r * H + g * kGroup + sub * 16, q[u].q);
+          store16<kNT>(xq + (size_t)r * Hp + g * kGroup + sub * kLane, q[u].q);
           if (sub == 0) xs[(size_t)r * G + g] = q[u].scale;
         }
       }
@@ -96,7 +104,8 @@ __global__ __launch_bounds__(256) void permute_quant_row_kernel(
   const unsigned wv = blockIdx.x * 4u + (threadIdx.x >> 6);
   const int t = (int)(wv / kW), c0 = (int)(wv % kW) * kC;
   if (t >= T) return;
-  const int G = H / kGroup;
+  const int Hp = pad128(H);
+  const int G = Hp / kGroup;
   const int R = T * K;
   const int sub = lane & 7, gl = lane >> 3;
   const int my_r = lane < K ? inv_map[(size_t)t * K + lane] : 0;
@@ -104,10 +113,18 @@ __global__ __launch_bounds__(256) void permute_quant_row_kernel(
   uint4 v[kC][2];
 #pragma unroll
   for (int c = 0; c < kC; ++c) {
-    const int g = min((c0 + c) * 8 + gl, G - 1);  // unconditional: every load in flight
-    const uint4* src = (const uint4*)(xrow + g * kGroup + sub * 16);
+    // unconditional: every load in flight (a lane past H re-reads column 0
+    // and is zeroed below)
+    const int col = min((c0 + c) * 8 + gl, G - 1) * kGroup + sub * kLane;
+    const uint4* src = (const uint4*)(xrow + (col < H ? col : 0));
     v[c][0] = src[0];
     v[c][1] = src[1];
+  }
+  if (H != Hp) {
+#pragma unroll
+    for (int c = 0; c < kC; ++c)
+      if (((c0 + c) * 8 + gl) * kGroup + sub * kLane >= H)
+        v[c][0] = v[c][1] = make_uint4(0, 0, 0, 0);
   }
   Q16 q[kC];
 #pragma unroll
@@ -124,7 +141,7 @@ __global__ __launch_bounds__(256) void permute_quant_row_kernel(
     for (int c = 0; c < kC; ++c) {
       const int g = (c0 + c) * 8 + gl;
       if (g < G) {
-        store16<kNT>(xq + (size_t)r * H + g * kGroup + sub * 16, q[c].q);
+        store16<kNT>(xq + (size_t)r * Hp + g * kGroup + sub * kLane, q[c].q);
         if (sub == 0) xs[(size_t)r * G + g] = q[c].scale;
       }
     }
@@ -196,25 +213,33 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const uint16_t* __res
 
 // ------------------------------------------------- weight 128x128 blocks
 // One 256-thread workgroup per 128x128 block.  Thread t owns 8 chunks of 8
-// bf16 (chunk j*256+t -> block row chunk/16, column (chunk%16)*8).
+// bf16 (chunk j*256+t -> block row chunk/16, column (chunk%16)*8).  w is
+// [E, N, Kd] bf16; wq is [E, N, Kp] with Kp = pad128(Kd), ws [E, NB, Kp/128]
+// with NB = ceil(N/128).  Rows past N and columns past Kd of an edge block
+// are zeros (not read); padding columns are written as byte 0.
 __global__ __launch_bounds__(256) void quant_weight_kernel(const uint16_t* __restrict__ w,
                                                            int N, int Kd,
                                                            uint8_t* __restrict__ wq,
                                                            float* __restrict__ ws) {
   __shared__ float wmax[4];
-  const int nb = N / kGroup, kb = Kd / kGroup;
+  const int Kp = pad128(Kd);
+  const int nb = (N + kGroup - 1) / kGroup, kb = Kp / kGroup;
   const int blk = blockIdx.x;
   const int e = blk / (nb * kb);
   const int rem = blk - e * nb * kb;
   const int bn = rem / kb, bk = rem - bn * kb;
-  const size_t base = ((size_t)e * N + (size_t)bn * kGroup) * Kd + (size_t)bk * kGroup;
+  const int r0 = bn * kGroup, k0 = bk * kGroup;
   float f[8][8];
   float amax = 0.0f;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int ch = j * 256 + threadIdx.x;
     const int row = ch >> 4, col = (ch & 15) * 8;
-    uint4 v = *(const uint4*)(w + base + (size_t)row * Kd + col);
+    const bool ok = r0 + row < N && k0 + col < Kd;
+    // unconditional load (an edge chunk re-reads the block's first element)
+    const uint16_t* src = w + ((size_t)e * N + r0 + (ok ? row : 0)) * Kd + k0 + (ok ? col : 0);
+    uint4 v = *(const uint4*)src;
+    if (!ok) v = make_uint4(0, 0, 0, 0);
     unpack_bf16x8(v, f[j]);
 #pragma unroll
     for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(f[j][i]));
@@ -233,7 +258,8 @@ __global__ __launch_bounds__(256) void quant_weight_kernel(const uint16_t* __res
                                    quot_bf16(f[j][2], d), quot_bf16(f[j][3], d));
     const uint32_t hi = e4m3_pack4(quot_bf16(f[j][4], d), quot_bf16(f[j][5], d),
                                    quot_bf16(f[j][6], d), quot_bf16(f[j][7], d));
-    *(uint2*)(wq + base + (size_t)row * Kd + col) = make_uint2(lo, hi);
+    if (r0 + row < N)
+      *(uint2*)(wq + ((size_t)e * N + r0 + row) * Kp + k0 + col) = make_uint2(lo, hi);
   }
   if (threadIdx.x == 0) ws[((size_t)e * nb + bn) * kb + bk] = s;
 }
@@ -378,14 +404,14 @@ extern "C" int smoe_selftest_recip(unsigned long long* counts, void* stream) {
 extern "C" int smoe_permute_quant(const uint16_t* x, const int32_t* inv_map, int T, int H, int K,
                                   uint8_t* xq, float* xs, void* stream) {
   if (T <= 0 || H <= 0) return SMOE_EINVAL_DIM;
-  if (H % kGroup) return SMOE_EINVAL_ALIGN128;
+  if (H % kLane) return SMOE_EINVAL_ALIGN128;
   if (K <= 0 || K > 32) return SMOE_EINVAL_TOPK;
   if ((long long)T * K > 0x7fffffffLL) return SMOE_EINVAL_DIM;
   SMOE_CHECK_PTR(x);
   SMOE_CHECK_PTR(inv_map);
   SMOE_CHECK_PTR(xq);
   SMOE_CHECK_PTR(xs);
-  const int chunks = (H / kGroup + 7) / 8;
+  const int chunks = (pad128(H) / kGroup + 7) / 8;
   hipStream_t s = (hipStream_t)stream;
   // Rows of up to 8 chunks (H <= 8192): the whole-row kernel with cached
   // stores, rows of 5..8 chunks split over two waves.  Measured with cold
@@ -418,11 +444,11 @@ extern "C" int smoe_permute_quant(const uint16_t* x, const int32_t* inv_map, int
 extern "C" int smoe_quant_rows_1x128(const uint16_t* x, int M, int C, uint8_t* q, float* s,
                                      void* stream) {
   if (M <= 0 || C <= 0) return SMOE_EINVAL_DIM;
-  if (C % kGroup) return SMOE_EINVAL_ALIGN128;
+  if (C % kLane) return SMOE_EINVAL_ALIGN128;
   SMOE_CHECK_PTR(x);
   SMOE_CHECK_PTR(q);
   SMOE_CHECK_PTR(s);
-  const int chunks = (C / kGroup + 7) / 8;
+  const int chunks = (pad128(C) / kGroup + 7) / 8;
   const dim3 grid((M + 3) / 4), block(256);
   hipStream_t st = (hipStream_t)stream;
 #define SMOE_QR(U) permute_quant_kernel<U, true><<<grid, block, 0, st>>>(x, nullptr, M, C, 1, q, s)
@@ -441,7 +467,7 @@ extern "C" int smoe_dispatch_quant(const uint16_t* x, const int32_t* topk_idx, i
                                    int32_t* counts, int32_t* offsets, uint8_t* xq, float* xs,
                                    void* ws, size_t ws_bytes, void* stream) {
   if (T <= 0 || H <= 0) return SMOE_EINVAL_DIM;
-  if (H % kGroup) return SMOE_EINVAL_ALIGN128;
+  if (H % kLane) return SMOE_EINVAL_ALIGN128;
   SMOE_CHECK_PTR(x);
   SMOE_CHECK_PTR(xq);
   SMOE_CHECK_PTR(xs);
@@ -481,11 +507,11 @@ extern "C" int smoe_quantize_weight_blockwise(const uint16_t* w, int E, int N, i
                                               uint8_t* wq, float* ws, void* stream) {
   if (N <= 0 || Kdim <= 0) return SMOE_EINVAL_DIM;
   if (E <= 0 || E > SMOE_MAX_EXPERTS) return SMOE_EINVAL_EXPERTS;
-  if (N % kGroup || Kdim % kGroup) return SMOE_EINVAL_ALIGN128;
+  if (N % kLane || Kdim % kLane) return SMOE_EINVAL_ALIGN128;
   SMOE_CHECK_PTR(w);
   SMOE_CHECK_PTR(wq);
   SMOE_CHECK_PTR(ws);
-  const long long blocks = (long long)E * (N / kGroup) * (Kdim / kGroup);
+  const long long blocks = (long long)E * ((N + kGroup - 1) / kGroup) * (pad128(Kdim) / kGroup);
   if (blocks > 0x7fffffffLL) return SMOE_EINVAL_DIM;
   quant_weight_kernel<<<dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream>>>(w, N, Kdim,
                                                                                       wq, ws);

@@ -21,6 +21,19 @@ FP8 = torch.float8_e4m3fn
 GROUP = 128
 
 
+def pad128(d: int) -> int:
+    """The fp8 row pitch of a dimension quantised in 128-wide groups.  A
+    dimension that is not a multiple of 128 (it must be a multiple of 16) is
+    quantised as if zero-padded to this size: the last group's scale comes
+    from its valid elements and the padding bytes are 0."""
+    return -(-d // GROUP) * GROUP
+
+
+def nblocks(d: int) -> int:
+    """128-wide groups (or weight blocks) along a dimension of size d."""
+    return -(-d // GROUP)
+
+
 def _ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
@@ -203,15 +216,17 @@ def route_topk_sort(logits: torch.Tensor, top_k: int, bias: torch.Tensor | None 
 # ---------------------------------------------------------------- dispatch
 def permute_quant_rows(x: torch.Tensor, inv_map: torch.Tensor, top_k: int):
     """Quantise each token row of x [T,H] bf16 once (1x128 groups) and write it
-    to the rows inv_map[t*K+k].  -> (xq [T*K,H] fp8, xs [T*K,H/128] f32)."""
+    to the rows inv_map[t*K+k].  -> (xq [T*K,pad128(H)] fp8,
+    xs [T*K,pad128(H)/128] f32).  H need only be a multiple of 16 (see
+    ``pad128``)."""
     _check(x, "x", (torch.bfloat16,), 2)
     _check(inv_map, "inv_map", (torch.int32,))
     T, H = x.shape
     if inv_map.numel() != T * top_k:
         raise ValueError("inv_map must have T*K entries")
     R = T * top_k
-    xq = torch.empty((R, H), dtype=FP8, device=x.device)
-    xs = torch.empty((R, H // GROUP), dtype=torch.float32, device=x.device)
+    xq = torch.empty((R, pad128(H)), dtype=FP8, device=x.device)
+    xs = torch.empty((R, nblocks(H)), dtype=torch.float32, device=x.device)
     _C.call("smoe_permute_quant", _ptr(x), _ptr(inv_map), T, H, top_k, _ptr(xq), _ptr(xs),
             _stream())
     return xq, xs
@@ -233,8 +248,8 @@ def permute_quant(x: torch.Tensor, topk_idx: torch.Tensor, num_experts: int):
     inv_map = torch.empty(R, dtype=torch.int32, device=dev)
     counts = torch.empty(num_experts, dtype=torch.int32, device=dev)
     offsets = torch.empty(num_experts + 1, dtype=torch.int32, device=dev)
-    xq = torch.empty((R, H), dtype=FP8, device=dev)
-    xs = torch.empty((R, H // GROUP), dtype=torch.float32, device=dev)
+    xq = torch.empty((R, pad128(H)), dtype=FP8, device=dev)
+    xs = torch.empty((R, nblocks(H)), dtype=torch.float32, device=dev)
     ws = _sort_workspace(T, K, num_experts, dev)
     _C.call("smoe_dispatch_quant", _ptr(x), _ptr(topk_idx), T, H, K, num_experts,
             _ptr(row_map), _ptr(inv_map), _ptr(counts), _ptr(offsets), _ptr(xq), _ptr(xs),
@@ -245,12 +260,14 @@ def permute_quant(x: torch.Tensor, topk_idx: torch.Tensor, num_experts: int):
 # ----------------------------------------------------------------- weights
 def quantize_weight_blockwise(w: torch.Tensor):
     """128x128 blockwise fp8 weights.  w [E,N,K] bf16 ("NK" layout,
-    summary/fp8_expert_gemm_optimization.md:137) -> (wq [E,N,K] fp8,
-    ws [E,N/128,K/128] f32)."""
+    summary/fp8_expert_gemm_optimization.md:137) -> (wq [E,N,pad128(K)] fp8,
+    ws [E,ceil(N/128),pad128(K)/128] f32).  N and K that are not multiples
+    of 128 (multiples of 16) end in partial blocks, quantised as the
+    zero-padded block; wq's padding columns are 0."""
     _check(w, "w", (torch.bfloat16,), 3)
     E, N, Kd = w.shape
-    wq = torch.empty((E, N, Kd), dtype=FP8, device=w.device)
-    ws = torch.empty((E, N // GROUP, Kd // GROUP), dtype=torch.float32, device=w.device)
+    wq = torch.empty((E, N, pad128(Kd)), dtype=FP8, device=w.device)
+    ws = torch.empty((E, nblocks(N), nblocks(Kd)), dtype=torch.float32, device=w.device)
     _C.call("smoe_quantize_weight_blockwise", _ptr(w), E, N, Kd, _ptr(wq), _ptr(ws), _stream())
     return wq, ws
 
@@ -285,7 +302,7 @@ def packed_gemm_ok(N: int, Kd: int) -> bool:
     """Whether the packed GEMM covers a weight of N rows and K = Kd: it needs
     K a multiple of 512 and at most 65536, and N*K < 2^32 (the same checks
     as smoe_grouped_gemm_fp8_packed; other weights use the plain kernel)."""
-    return (Kd % (4 * GROUP) == 0 and 0 < Kd <= PACKED_MAX_K and N % GROUP == 0
+    return (Kd % (4 * GROUP) == 0 and 0 < Kd <= PACKED_MAX_K and N % 16 == 0
             and N * Kd < (1 << 32))
 
 
@@ -295,7 +312,7 @@ def pack_weight_fp8(wq: torch.Tensor) -> PackedWeight:
     _check(wq, "wq", (FP8, torch.uint8), 3)
     E, N, Kd = wq.shape
     if not packed_gemm_ok(N, Kd):
-        raise ValueError(f"packed weights need K % 512 == 0, K <= {PACKED_MAX_K}, N % 128 == 0 "
+        raise ValueError(f"packed weights need K % 512 == 0, K <= {PACKED_MAX_K}, N % 16 == 0 "
                          f"and N*K < 2^32 (N={N}, K={Kd})")
     wp = torch.empty((E, N, Kd), dtype=torch.uint8, device=wq.device)
     _C.call("smoe_pack_weight_fp8", _ptr(_bytes(wq)), E, N, Kd, _ptr(wp), _stream())
@@ -335,7 +352,9 @@ def grouped_gemm_fp8(xq: torch.Tensor, xs: torch.Tensor, wq: torch.Tensor, ws: t
                          f"(N={N}, K={Kd})")
     if offsets.numel() != E + 1:
         raise ValueError("offsets must have E+1 entries")
-    if xs.shape != (R, Kd // GROUP) or ws.shape != (E, N // GROUP, Kd // GROUP):
+    if Kd % GROUP:
+        raise ValueError(f"xq's K ({Kd}) must be its 128-padded pitch")
+    if xs.shape != (R, Kd // GROUP) or ws.shape != (E, nblocks(N), Kd // GROUP):
         raise ValueError("scale shapes do not match the operands")
     if out is None:
         out = torch.empty((R, N), dtype=torch.bfloat16, device=xq.device)
@@ -430,27 +449,30 @@ def unpermute_combine(y: torch.Tensor, inv_map: torch.Tensor, topk_w: torch.Tens
 # ---------------------------------------------------------------- backward
 def quant_rows(x: torch.Tensor):
     """1x128 row quantisation without permutation: x [M,C] bf16 ->
-    (q [M,C] fp8, s [M,C/128] f32)."""
+    (q [M,pad128(C)] fp8, s [M,pad128(C)/128] f32)."""
     _check(x, "x", (torch.bfloat16,), 2)
     M, C = x.shape
-    q = torch.empty((M, C), dtype=FP8, device=x.device)
-    s = torch.empty((M, C // GROUP), dtype=torch.float32, device=x.device)
+    q = torch.empty((M, pad128(C)), dtype=FP8, device=x.device)
+    s = torch.empty((M, nblocks(C)), dtype=torch.float32, device=x.device)
     _C.call("smoe_quant_rows_1x128", _ptr(x), M, C, _ptr(q), _ptr(s), _stream())
     return q, s
 
 
-def transpose_blockwise(wq: torch.Tensor, ws: torch.Tensor):
-    """[E,N,K] fp8 + [E,N/128,K/128] -> [E,K,N] + [E,K/128,N/128] (dgrad
-    weights; blockwise quantisation commutes with the transpose)."""
+def transpose_blockwise(wq: torch.Tensor, ws: torch.Tensor, k: int | None = None):
+    """[E,N,Kp] fp8 + [E,NB,KB] -> [E,K,pad128(N)] + [E,KB,NB] (dgrad
+    weights; blockwise quantisation commutes with the transpose).  ``k`` is
+    the true K when wq's pitch Kp = pad128(K) holds padding (default Kp);
+    the result's padding columns past N are 0."""
     _check(wq, "wq", (FP8, torch.uint8), 3)
     _check(ws, "ws", (torch.float32,), 3)
-    E, N, Kd = wq.shape
-    if N % GROUP or Kd % GROUP:
-        raise ValueError("wq dims must be multiples of 128")
-    if tuple(ws.shape) != (E, N // GROUP, Kd // GROUP):
-        raise ValueError(f"ws must be [{E}, {N // GROUP}, {Kd // GROUP}] for wq {tuple(wq.shape)}")
-    wqT = torch.empty((E, Kd, N), dtype=FP8, device=wq.device)
-    wsT = torch.empty((E, Kd // GROUP, N // GROUP), dtype=torch.float32, device=wq.device)
+    E, N, Kp = wq.shape
+    Kd = Kp if k is None else int(k)
+    if N % 16 or Kd % 16 or Kp % GROUP or pad128(Kd) != Kp:
+        raise ValueError(f"wq [{E}, {N}, {Kp}] is not the padded form of a K = {Kd} weight")
+    if tuple(ws.shape) != (E, nblocks(N), Kp // GROUP):
+        raise ValueError(f"ws must be [{E}, {nblocks(N)}, {Kp // GROUP}] for wq {tuple(wq.shape)}")
+    wqT = torch.empty((E, Kd, pad128(N)), dtype=FP8, device=wq.device)
+    wsT = torch.empty((E, Kp // GROUP, nblocks(N)), dtype=torch.float32, device=wq.device)
     _C.call("smoe_transpose_blockwise_fp8", _ptr(_bytes(wq)), _ptr(ws), E, N, Kd,
             _ptr(wqT), _ptr(wsT), _stream())
     return wqT, wsT
@@ -490,14 +512,15 @@ def quant_rows_cols(x: torch.Tensor, offsets: torch.Tensor):
     """Both quantisations of x [R,C] bf16 from one read: the 1x128 rows of
     ``quant_rows`` and the transposed 128x1 columns of ``quant_cols`` over
     the expert segments ``offsets`` (which must cover all R rows).
-    -> (xq [R,C] fp8, xs [R,C/128], xTq [C,ld] fp8, xTs [C,ld/128], pad, ld)."""
+    -> (xq [R,pad128(C)] fp8, xs [R,pad128(C)/128], xTq [C,ld] fp8,
+    xTs [C,ld/128], pad, ld)."""
     _check(x, "x", (torch.bfloat16,), 2)
     _check(offsets, "offsets", (torch.int32,), 1)
     R, C = x.shape
     E = offsets.numel() - 1
     ld = int(_C.lib().smoe_quant_cols_ld(R, E))
-    xq = torch.empty((R, C), dtype=FP8, device=x.device)
-    xs = torch.empty((R, C // GROUP), dtype=torch.float32, device=x.device)
+    xq = torch.empty((R, pad128(C)), dtype=FP8, device=x.device)
+    xs = torch.empty((R, nblocks(C)), dtype=torch.float32, device=x.device)
     xTq = torch.empty((C, ld), dtype=FP8, device=x.device)
     xTs = torch.empty((C, ld // GROUP), dtype=torch.float32, device=x.device)
     pad = torch.empty(E + 1, dtype=torch.int32, device=x.device)

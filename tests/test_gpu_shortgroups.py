@@ -1,0 +1,168 @@
+"""Dimensions that are not a multiple of 128 (GPT-OSS: H = I = 2880, 22.5
+groups of 128) through the quantisers and GEMMs, against the oracle's C9
+rule (the operand quantised as if zero-padded to the next multiple of 128;
+fp8 operands keep that padded pitch).
+
+Bars: fp8 bytes, scales, transposes bit-exact; GEMM outputs within the GEMM
+tolerance of the float64 oracle (max 1e-2, mean 1e-3 of the bf16-rounded
+reference); the fp32 weight gradient within the same tolerance."""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import smoe_oracle as O
+from smoe import ops
+from smoe import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print("[short]", *a, flush=True)
+    sys.stdout.flush()
+
+
+def u16(t):
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def u8(t):
+    return t.detach().cpu().contiguous().view(torch.uint8).numpy()
+
+
+def gemm_close(got, ref, what, bf16_ref=True):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    if bf16_ref:
+        ref = O.bf16_to_f32(O.f32_to_bf16(ref.astype(np.float32))).astype(np.float64)
+    d = np.abs(got - ref)
+    mx, mn = d.max() / np.abs(ref).max(), d.mean() / np.abs(ref).mean()
+    assert mx <= 1e-2 and mn <= 1e-3, f"{what}: max_rel={mx:.3e} mean_rel={mn:.3e}"
+
+
+@pytest.mark.parametrize("M,C", [(301, 2880), (64, 16), (1000, 5760 - 16), (7, 144)])
+def test_quant_rows_short_group(dev, M, C):
+    say("quant rows", M, C)
+    x = W.tokens(M, C, seed=C, outliers=True)
+    q, s = ops.quant_rows(x.to(dev))
+    rq, rs = O.quant_1x128(O.bf16_to_f32(u16(x)))
+    assert q.shape == (M, O.pad128(C))
+    assert np.array_equal(u8(q), rq) and np.array_equal(s.cpu().numpy(), rs)
+
+
+@pytest.mark.parametrize("T,H,K", [(777, 2880, 4), (100, 4096 + 16, 2)])
+def test_permute_quant_short_group(dev, T, H, K):
+    say("permute quant", T, H, K)
+    x = W.tokens(T, H, seed=T, outliers=True)
+    idx, _ = ops.router_topk(W.logits(T, 32, device=dev, seed=T), K)
+    xq, xs, row_map, inv_map, counts, offsets = ops.permute_quant(x.to(dev), idx, 32)
+    rq, rs = O.permute_quant(u16(x), inv_map.cpu().numpy(), K)
+    assert np.array_equal(u8(xq), rq) and np.array_equal(xs.cpu().numpy(), rs)
+
+
+def test_weight_quant_and_transpose_short_blocks(dev):
+    say("weight quant 2880")
+    E, N, K = 3, 2880, 2880 - 16 * 3
+    w = W.weights(E, N, K, seed=7)
+    wq, ws = ops.quantize_weight_blockwise(w.to(dev))
+    rq, rs = O.quantize_weight_blockwise(u16(w))
+    assert wq.shape == (E, N, O.pad128(K))
+    assert np.array_equal(u8(wq), rq) and np.array_equal(ws.cpu().numpy(), rs)
+    wt, wts = ops.transpose_blockwise(wq, ws, k=K)
+    rt, rts = O.transpose_blockwise(rq, rs, k=K)
+    assert wt.shape == (E, K, O.pad128(N))
+    assert np.array_equal(u8(wt), rt) and np.array_equal(wts.cpu().numpy(), rts)
+
+
+def _gemm_case(dev, counts, N, K, seed, packed=False):
+    E = len(counts)
+    R = int(sum(counts))
+    off = W.offsets_from_counts(counts, dev)
+    x = W.tokens(R, K, seed=seed)
+    xq, xs = ops.quant_rows(x.to(dev))
+    w = W.weights(E, N, K, seed=seed + 1)
+    wq, ws = ops.quantize_weight_blockwise(w.to(dev))
+    out = ops.grouped_gemm_fp8(xq, xs, ops.pack_weight_fp8(wq) if packed else wq, ws, off)
+    ref = O.grouped_gemm_fp8(u8(xq), xs.cpu().numpy(), u8(wq), ws.cpu().numpy(),
+                             off.cpu().numpy())
+    return out, ref, (xq, xs, wq, ws, off)
+
+
+@pytest.mark.parametrize("counts,N,K", [([300, 0, 517, 64], 2880, 2880), ([129, 1000], 5760, 2880),
+                                        ([256, 255], 2880 - 16, 256 + 48)])
+def test_gemm_short_n_and_padded_k(dev, counts, N, K):
+    """fc1 / fc2 of the GPT-OSS shape (N = 2I = 5760 or N = H = 2880, K =
+    2880 padded to 2944): N ends in a partial 128-row weight block and a
+    partial 256-column tile."""
+    say("gemm", counts, N, K)
+    out, ref, _ = _gemm_case(dev, counts, N, K, seed=N + K)
+    assert out.shape == (sum(counts), N)
+    gemm_close(O.bf16_to_f32(u16(out)), ref, f"N={N} K={K}")
+
+
+def test_packed_gemm_short_n(dev):
+    """The packed kernel with N = 2880 (K = 1024): the same bytes as the plain
+    kernel."""
+    say("packed gemm N=2880")
+    counts = [700, 0, 300]
+    plain, ref, (xq, xs, wq, ws, off) = _gemm_case(dev, counts, 2880, 1024, seed=5)
+    packed = ops.grouped_gemm_fp8(xq, xs, ops.pack_weight_fp8(wq), ws, off)
+    assert torch.equal(packed.view(torch.int16), plain.view(torch.int16))
+    gemm_close(O.bf16_to_f32(u16(packed)), ref, "packed N=2880")
+
+
+@pytest.mark.parametrize("counts,C", [([300, 0, 129, 1000], 2880), ([64, 70], 144)])
+def test_quant_cols_and_rows_cols_short(dev, counts, C):
+    """The 128x1 column quantiser and the one-read row + column quantiser for
+    C not a multiple of 128: columns bit-exact with the oracle (C rows of the
+    transposed output), rows bit-exact with quant_rows (padded pitch)."""
+    say("quant cols", counts, C)
+    R = int(sum(counts))
+    off = W.offsets_from_counts(counts, dev)
+    x = W.tokens(R, C, seed=C + 3, outliers=True)
+    xT, xTs, pad, ld = ops.quant_cols(x.to(dev), off)
+    rT, rTs, rpad = O.quant_cols_128x1(O.bf16_to_f32(u16(x)), off.cpu().numpy())
+    Rp = int(rpad[-1])
+    assert xT.shape == (C, ld)
+    assert np.array_equal(u8(xT)[:, :Rp], rT) and np.array_equal(xTs.cpu().numpy()[:, :Rp // 128], rTs)
+    q, s, qT, sT, pad2, ld2 = ops.quant_rows_cols(x.to(dev), off)
+    q0, s0 = ops.quant_rows(x.to(dev))
+    assert torch.equal(q.view(torch.uint8), q0.view(torch.uint8)) and torch.equal(s, s0)
+    assert np.array_equal(u8(qT)[:, :Rp], rT) and np.array_equal(sT.cpu().numpy()[:, :Rp // 128], rTs)
+
+
+def test_wgrad_short_edges(dev):
+    """dW [E, 2880, 2880] from 128x1 operands of C = 2880 columns: the wgrad
+    masks its partial 256-tiles in both n and k (fp32 and bf16 outputs)."""
+    say("wgrad 2880")
+    counts = [500, 0, 129, 1]
+    R, N, K, E = sum(counts), 2880, 2880, 4
+    off = W.offsets_from_counts(counts, dev)
+    a = W.tokens(R, N, seed=41)
+    b = W.tokens(R, K, seed=42)
+    aT, aTs, pad, ld = ops.quant_cols(a.to(dev), off)
+    bT, bTs, _, _ = ops.quant_cols(b.to(dev), off)
+    dW = ops.grouped_gemm_fp8_wgrad(aT, aTs, bT, bTs, pad, ld)
+    raT, raTs, rpad = O.quant_cols_128x1(O.bf16_to_f32(u16(a)), off.cpu().numpy())
+    rbT, rbTs, _ = O.quant_cols_128x1(O.bf16_to_f32(u16(b)), off.cpu().numpy())
+    ref = O.grouped_gemm_fp8_wgrad(raT, raTs, rbT, rbTs, rpad, E)
+    assert not dW[1].any()
+    gemm_close(dW.cpu().numpy(), ref, "dW 2880", bf16_ref=False)
+    d16 = ops.grouped_gemm_fp8_wgrad(aT, aTs, bT, bTs, pad, ld, dtype=torch.bfloat16)
+    assert torch.equal(d16.view(torch.int16), dW.to(torch.bfloat16).view(torch.int16))
+
+
+def test_short_dims_rejected():
+    """Dimensions that are not a multiple of 16 are refused on the host."""
+    from smoe import _C
+    lib = _C.lib()
+    FAKE = 0x100000
+    assert lib.smoe_quant_rows_1x128(FAKE, 4, 2872 + 4, FAKE, FAKE, None) == -3
+    assert lib.smoe_quantize_weight_blockwise(FAKE, 2, 2880, 2872 + 4, FAKE, FAKE, None) == -3
+    assert lib.smoe_grouped_gemm_fp8(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 8, 2888, 2944, FAKE, None, 0,
+                                     None) == -3
+    # K must be the padded pitch
+    assert lib.smoe_grouped_gemm_fp8(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 8, 2880, 2880, FAKE, None, 0,
+                                     None) == -3

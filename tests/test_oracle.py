@@ -209,6 +209,53 @@ def _rand_fp8(rng, shape):
     return q
 
 
+def test_quant_1x128_short_last_group():
+    """C9 at GPT-OSS's H = 2880 (22.5 groups): the 22 full groups equal the
+    aligned prefix quantised alone; the short group's scale is the amax of
+    its 64 valid values / 448 (float32 division) and its bytes are torch's
+    e4m3 cast of clamp(x / s); the 64 padding bytes are 0."""
+    rng = np.random.default_rng(2880)
+    M, H = 9, 2880
+    x = (rng.standard_normal((M, H)) * np.exp(rng.standard_normal((M, 1)))).astype(np.float32)
+    x[3, 2816:] = 0.0            # an all-zero short group: s = 1
+    x[4, 2870] = 1000.0          # an outlier in the short group
+    q, s = O.quant_1x128(x)
+    assert q.shape == (M, 2944) and s.shape == (M, 23)
+    q0, s0 = O.quant_1x128(x[:, :2816])
+    assert np.array_equal(q[:, :2816], q0) and np.array_equal(s[:, :22], s0)
+    amax = np.abs(x[:, 2816:]).max(axis=1)
+    want_s = np.where(amax == 0, np.float32(1), (amax / np.float32(448)).astype(np.float32))
+    assert np.array_equal(s[:, 22], want_s.astype(np.float32))
+    assert s[3, 22] == 1.0
+    v = np.clip(x[:, 2816:] / s[:, 22:23], -448, 448).astype(np.float32)
+    assert np.array_equal(q[:, 2816:2880], _torch_e4m3(v))
+    assert not q[:, 2880:].any()
+
+
+def test_weight_quant_short_blocks_and_transpose():
+    """C9 for 128x128 weight blocks at N = K = 2880: blocks inside the
+    aligned part equal the aligned restatement, a short block's scale is the
+    amax of its valid elements / 448, padding columns are 0; the transposed
+    weights dequantise to the transpose of the dequantised weights."""
+    rng = np.random.default_rng(2881)
+    E, N, K = 2, 2880, 2880
+    w = O.f32_to_bf16((rng.standard_normal((E, N, K)) * 0.02).astype(np.float32))
+    q, s = O.quantize_weight_blockwise(w)
+    assert q.shape == (E, N, 2944) and s.shape == (E, 23, 23)
+    qa, sa = O.quantize_weight_blockwise(np.ascontiguousarray(w[:, :2816, :2816]))
+    assert np.array_equal(q[:, :2816, :2816], qa) and np.array_equal(s[:, :22, :22], sa)
+    wf = O.bf16_to_f32(w)
+    for (r0, r1, c0, c1) in ((2816, 2880, 0, 128), (0, 128, 2816, 2880), (2816, 2880, 2816, 2880)):
+        amax = np.abs(wf[0, r0:r1, c0:c1]).max()
+        assert s[0, r0 // 128, c0 // 128] == np.float32(amax) / np.float32(448)
+    assert not q[:, :, 2880:].any()
+    qt, st = O.transpose_blockwise(q, s, k=K)
+    assert qt.shape == (E, K, 2944) and st.shape == (E, 23, 23)
+    for e in range(E):
+        assert np.array_equal(O.dequant_weight(qt[e], st[e])[:, :N], O.dequant_weight(q[e], s[e])[:, :K].T)
+    assert not qt[:, :, 2880:].any()
+
+
 def test_grouped_gemm_brute_force_blocks():
     rng = np.random.default_rng(5)
     E, N, Kd = 3, 256, 384
