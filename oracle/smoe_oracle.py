@@ -576,10 +576,11 @@ def moe_backward(fwd: dict, x_bf16, w1q, w1s, w2q, w2s, dout_bf16, K: int):
     T = x_bf16.shape[0]
     dy, dw = combine_bwd(dout_bf16, fwd["y"], inv, fwd["topk_w"], K)
     dyq, dys = quant_1x128(bf16_to_f32(dy))
-    w2tq, w2ts = transpose_blockwise(w2q, w2s)
-    dh = f32_to_bf16(grouped_gemm_fp8(dyq, dys, w2tq, w2ts, off).astype(np.float32))
     h = bf16_to_f32(fwd["c1"])
     I = h.shape[1] // 2
+    H = x_bf16.shape[1]
+    w2tq, w2ts = transpose_blockwise(w2q, w2s, k=I)
+    dh = f32_to_bf16(grouped_gemm_fp8(dyq, dys, w2tq, w2ts, off).astype(np.float32))
     # h as the forward saves it: silu(g)*u in fp32, rounded to bf16
     hh = bf16_to_f32(f32_to_bf16((silu_f32(h[:, :I]) * h[:, I:]).astype(np.float32)))
     dyTq, dyTs, pad = quant_cols_128x1(bf16_to_f32(dy), off)
@@ -587,7 +588,7 @@ def moe_backward(fwd: dict, x_bf16, w1q, w1s, w2q, w2s, dout_bf16, K: int):
     dW2 = grouped_gemm_fp8_wgrad(dyTq, dyTs, hTq, hTs, pad, E)
     dc1 = swiglu_bwd(fwd["c1"], dh)
     dc1q, dc1s = quant_1x128(bf16_to_f32(dc1))
-    w1tq, w1ts = transpose_blockwise(w1q, w1s)
+    w1tq, w1ts = transpose_blockwise(w1q, w1s, k=H)
     dxs = f32_to_bf16(grouped_gemm_fp8(dc1q, dc1s, w1tq, w1ts, off).astype(np.float32))
     xs_sorted = bf16_to_f32(x_bf16)[fwd["row_map"] // K]
     dcTq, dcTs, _ = quant_cols_128x1(bf16_to_f32(dc1), off)

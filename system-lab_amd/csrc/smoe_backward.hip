@@ -417,8 +417,13 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(
       wk[k] = w[(size_t)t * K + k];
     }
   }
-  for (int col = lane * 8; col < H; col += kWave * 8) {
-    const uint4 vd = *(const uint4*)(dout + (size_t)t * H + col);
+  // kQuant walks the 128-padded row (Hp) so that each 16-lane group covers
+  // one whole quantisation group: columns past H read nothing (zeros) and
+  // quantise to byte 0
+  const int Hp = kQuant ? pad128(H) : H;
+  for (int col = lane * 8; col < Hp; col += kWave * 8) {
+    const bool in = col < H;
+    const uint4 vd = in ? *(const uint4*)(dout + (size_t)t * H + col) : make_uint4(0, 0, 0, 0);
     const uint32_t d4[4] = {vd.x, vd.y, vd.z, vd.w};
     float d[8];
 #pragma unroll
@@ -430,7 +435,8 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(
     uint4 vyk[kMaxK];
 #pragma unroll
     for (int k = 0; k < kMaxK; ++k)
-      if (k < K && (unsigned)r[k] < (unsigned)R) vyk[k] = *(const uint4*)(y + (size_t)r[k] * H + col);
+      vyk[k] = (k < K && (unsigned)r[k] < (unsigned)R && in) ? *(const uint4*)(y + (size_t)r[k] * H + col)
+                                                             : make_uint4(0, 0, 0, 0);
 #pragma unroll
     for (int k = 0; k < kMaxK; ++k) {
       if (k >= K || (unsigned)r[k] >= (unsigned)R) continue;
@@ -445,6 +451,7 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(
         part[k] = part[k] + d[2 * i + 1] * y1;
         o[i] = bf16_pack2(wk[k] * d[2 * i], wk[k] * d[2 * i + 1]);
       }
+      if (!in) o[0] = o[1] = o[2] = o[3] = 0u;  // padding is +0 (w * +0 can be -0)
       if constexpr (kQuant) {
         float m = 0.0f;
 #pragma unroll
@@ -460,9 +467,9 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(
           qv[2 * i] = quot_bf16(__uint_as_float(o[i] << 16), qd);
           qv[2 * i + 1] = quot_bf16(__uint_as_float(o[i] & 0xffff0000u), qd);
         }
-        *(uint2*)(dyq + (size_t)r[k] * H + col) =
+        *(uint2*)(dyq + (size_t)r[k] * Hp + col) =
             make_uint2(e4m3_pack4(qv[0], qv[1], qv[2], qv[3]), e4m3_pack4(qv[4], qv[5], qv[6], qv[7]));
-        if ((lane & 15) == 0) dys[(size_t)r[k] * (H / kGroup) + col / kGroup] = sc;
+        if ((lane & 15) == 0) dys[(size_t)r[k] * (Hp / kGroup) + col / kGroup] = sc;
       } else {
         *(uint4*)(dy + (size_t)r[k] * H + col) = make_uint4(o[0], o[1], o[2], o[3]);
       }
@@ -578,7 +585,7 @@ extern "C" int smoe_swiglu_bwd_quant(const uint16_t* c1, const uint16_t* dh, int
 extern "C" int smoe_swiglu_bwd(const uint16_t* c1, const uint16_t* dh, int R, int I,
                                uint16_t* dc1, void* stream) {
   if (R <= 0 || I <= 0) return SMOE_EINVAL_DIM;
-  if (I % kGroup) return SMOE_EINVAL_ALIGN128;
+  if (I % kLane) return SMOE_EINVAL_ALIGN128;
   SMOE_CHECK_PTR(c1);
   SMOE_CHECK_PTR(dh);
   SMOE_CHECK_PTR(dc1);
@@ -590,7 +597,7 @@ extern "C" int smoe_unpermute_combine_bwd(const uint16_t* dout, const uint16_t* 
                                           const int32_t* inv_map, const float* w, int T, int K,
                                           int H, uint16_t* dy, float* dw, void* stream) {
   if (T <= 0 || H <= 0) return SMOE_EINVAL_DIM;
-  if (H % kGroup) return SMOE_EINVAL_ALIGN128;
+  if (H % kLane) return SMOE_EINVAL_ALIGN128;
   if (K <= 0 || K > 32) return SMOE_EINVAL_TOPK;
   if ((long long)T * K > 0x7fffffffLL) return SMOE_EINVAL_DIM;
   SMOE_CHECK_PTR(dout);
@@ -618,7 +625,7 @@ extern "C" int smoe_unpermute_combine_bwd_quant(const uint16_t* dout, const uint
                                                 float* dyTs, int32_t* pad, float* dw,
                                                 void* stream) {
   if (T <= 0 || H <= 0) return SMOE_EINVAL_DIM;
-  if (H % kGroup) return SMOE_EINVAL_ALIGN128;
+  if (H % kLane) return SMOE_EINVAL_ALIGN128;
   if (K <= 0 || K > 32) return SMOE_EINVAL_TOPK;
   if ((long long)T * K > 0x7fffffffLL) return SMOE_EINVAL_DIM;
   if (E <= 0 || E > SMOE_MAX_EXPERTS) return SMOE_EINVAL_EXPERTS;
@@ -647,7 +654,7 @@ extern "C" int smoe_unpermute_combine_bwd_quant(const uint16_t* dout, const uint
   pad_offsets_kernel<<<1, 1024, 0, s>>>(offsets, E, pad);
   // 128x1 columns: row r of dy is rebuilt as bf16(w[p] * dout[p / K]) with
   // p = row_map[r]
-  quant_cols_kernel<false, false><<<dim3(H / kQcCols, ld / kGroup), dim3(256), 0, s>>>(
+  quant_cols_kernel<false, false><<<dim3((H + kQcCols - 1) / kQcCols, ld / kGroup), dim3(256), 0, s>>>(
       dout, row_map, K, w, R, H, offsets, pad, E, ld, dyTq, dyTs, nullptr, nullptr, nullptr,
       nullptr, nullptr);
   SMOE_RETURN_LAUNCH();

@@ -96,7 +96,7 @@ using namespace smoe;
 extern "C" int smoe_unpermute_combine(const uint16_t* y, const int32_t* inv_map, const float* w,
                                       int T, int K, int H, uint16_t* out, void* stream) {
   if (T <= 0 || H <= 0) return SMOE_EINVAL_DIM;
-  if (H % kGroup) return SMOE_EINVAL_ALIGN128;
+  if (H % kLane) return SMOE_EINVAL_ALIGN128;  // whole 16-byte lane pieces
   if (K <= 0 || K > 32) return SMOE_EINVAL_TOPK;
   if ((long long)T * K > 0x7fffffffLL) return SMOE_EINVAL_DIM;
   SMOE_CHECK_PTR(y);

@@ -163,7 +163,8 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const uint16_t* __res
                                                            float* __restrict__ hs,
                                                            uint16_t* __restrict__ hb) {
   const int lane = threadIdx.x & 63;
-  const uint32_t G = (uint32_t)(I / kGroup);
+  const int Ip = pad128(I);  // hq's pitch; columns I .. Ip of h are 0
+  const uint32_t G = (uint32_t)(Ip / kGroup);
   const int sub = lane & 7, gl = lane >> 3;
   const uint32_t base = (blockIdx.x * 4u + (threadIdx.x >> 6)) * (8u * kUnroll);
   uint4 vg[kUnroll][2], vu[kUnroll][2];
@@ -173,7 +174,7 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const uint16_t* __res
     const uint32_t slot = base + u * 8 + gl;
     rr[u] = slot / G;
     gg[u] = slot - rr[u] * G;
-    if (slot < nslots) {
+    if (slot < nslots && (int)gg[u] * kGroup + sub * kLane < I) {
       const uint16_t* gate = c1 + (size_t)rr[u] * 2 * I + gg[u] * kGroup + sub * 16;
       const uint16_t* up = gate + I;
       vg[u][0] = *(const uint4*)gate;
@@ -197,15 +198,16 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const uint16_t* __res
     // never mixes slots (or a valid slot with padding)
     const Q16 q = quant16(h);
     if (base + u * 8 + gl < nslots) {
-      const size_t off = (size_t)rr[u] * I + gg[u] * kGroup + sub * 16;
-      if (kSaveH) {
+      const int col = (int)gg[u] * kGroup + sub * kLane;
+      if (kSaveH && col < I) {
+        const size_t off = (size_t)rr[u] * I + col;
         uint32_t w[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) w[i] = bf16_pack2(h[2 * i], h[2 * i + 1]);
         *(uint4*)(hb + off) = make_uint4(w[0], w[1], w[2], w[3]);
         *(uint4*)(hb + off + 8) = make_uint4(w[4], w[5], w[6], w[7]);
       }
-      store16<true>(hq + off, q.q);
+      store16<true>(hq + (size_t)rr[u] * Ip + col, q.q);
       if (sub == 0) hs[(size_t)rr[u] * G + gg[u]] = q.scale;
     }
   }
@@ -480,13 +482,13 @@ extern "C" int smoe_dispatch_quant(const uint16_t* x, const int32_t* topk_idx, i
 extern "C" int smoe_swiglu_quant_h(const uint16_t* c1, int R, int I, uint8_t* hq, float* hs,
                                    uint16_t* h, void* stream) {
   if (R <= 0 || I <= 0) return SMOE_EINVAL_DIM;
-  if (I % kGroup) return SMOE_EINVAL_ALIGN128;
+  if (I % kLane) return SMOE_EINVAL_ALIGN128;
   SMOE_CHECK_PTR(c1);
   SMOE_CHECK_PTR(hq);
   SMOE_CHECK_PTR(hs);
   if (h && ((uintptr_t)h & 15u)) return SMOE_EINVAL_PTRALIGN;
   // slots (row, group) are 32-bit; the grid covers them 32 * kUnroll per block
-  const long long nslots = (long long)R * (I / kGroup);
+  const long long nslots = (long long)R * (pad128(I) / kGroup);
   constexpr int kU = 2;
   if (nslots + 32LL * kU > 0xffffffffLL) return SMOE_EINVAL_DIM;
   const dim3 grid((unsigned)((nslots + 32 * kU - 1) / (32 * kU))), block(256);

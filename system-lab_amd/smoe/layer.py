@@ -162,10 +162,10 @@ class SimpleMoE(nn.Module):
         ``gemm_weights_t``)."""
         return self._transposed(self.fp8_weights())
 
-    @staticmethod
-    def _transposed(fp8):
+    def _transposed(self, fp8):
         w1q, w1s, w2q, w2s = fp8
-        return ops.transpose_blockwise(w1q, w1s) + ops.transpose_blockwise(w2q, w2s)
+        return (ops.transpose_blockwise(w1q, w1s, k=self.hidden)
+                + ops.transpose_blockwise(w2q, w2s, k=self.intermediate))
 
     def gemm_weights(self):
         """(w1, w1s, w2, w2s) as the forward GEMMs take them: fp8_weights()
@@ -253,11 +253,11 @@ class SimpleMoE(nn.Module):
                      topk_w=torch.empty((0, K), dtype=torch.float32, device=dev),
                      row_map=torch.empty(0, **i32), inv_map=torch.empty(0, **i32),
                      counts=torch.zeros(E, **i32), offsets=torch.zeros(E + 1, **i32),
-                     xq=torch.empty((0, H), dtype=ops.FP8, device=dev),
-                     xs=torch.empty((0, H // ops.GROUP), dtype=torch.float32, device=dev),
+                     xq=torch.empty((0, ops.pad128(H)), dtype=ops.FP8, device=dev),
+                     xs=torch.empty((0, ops.nblocks(H)), dtype=torch.float32, device=dev),
                      c1=torch.empty((0, 2 * I), dtype=torch.bfloat16, device=dev),
-                     hq=torch.empty((0, I), dtype=ops.FP8, device=dev),
-                     hs=torch.empty((0, I // ops.GROUP), dtype=torch.float32, device=dev),
+                     hq=torch.empty((0, ops.pad128(I)), dtype=ops.FP8, device=dev),
+                     hs=torch.empty((0, ops.nblocks(I)), dtype=torch.float32, device=dev),
                      h=torch.empty((0, I), dtype=torch.bfloat16, device=dev),
                      y=torch.empty((0, H), dtype=torch.bfloat16, device=dev))
         return out, inter
@@ -272,8 +272,8 @@ class SimpleMoE(nn.Module):
         out = dict(dx=torch.empty((0, H), dtype=torch.bfloat16, device=dev),
                    dw1=torch.zeros((E, 2 * I, H), **wg), dw2=torch.zeros((E, H, I), **wg),
                    dtopk_w=torch.empty((0, K), **f32), dlogits=torch.empty((0, E), **f32),
-                   dyq=torch.empty((0, H), dtype=ops.FP8, device=dev),
-                   dys=torch.empty((0, H // ops.GROUP), **f32),
+                   dyq=torch.empty((0, ops.pad128(H)), dtype=ops.FP8, device=dev),
+                   dys=torch.empty((0, ops.nblocks(H)), **f32),
                    dh=torch.empty((0, I), dtype=torch.bfloat16, device=dev),
                    dxs=torch.empty((0, H), dtype=torch.bfloat16, device=dev))
         if inter.get("logits_from_gate"):

@@ -390,8 +390,15 @@ def grouped_gemm_fp8_swiglu(xq: torch.Tensor, xs: torch.Tensor, w1q: torch.Tenso
     if packed and not packed_gemm_ok(N, Kd):
         raise ValueError(f"packed weights need K % 512 == 0, K <= {PACKED_MAX_K} and N*K < 2^32 "
                          f"(N={N}, K={Kd})")
+    if N % 2 == 0 and (N // 2) % GROUP and (N // 2) % 16 == 0:
+        # I not a multiple of 128: the fused epilogue pairs 128-column gate
+        # and up blocks, which such an I does not have; the same bytes come
+        # from the GEMM followed by the SwiGLU kernel
+        c1 = grouped_gemm_fp8(xq, xs, w1q, w1s, offsets)
+        hq, hs = swiglu_quant(c1)
+        return (hq, hs, c1) if save_c1 else (hq, hs)
     if N % (2 * GROUP):
-        raise ValueError("w1q rows must be gate | up halves of a multiple of 128 each")
+        raise ValueError("w1q rows must be gate | up halves, each a multiple of 16")
     if offsets.numel() != E + 1:
         raise ValueError("offsets must have E+1 entries")
     if xs.shape != (R, Kd // GROUP) or w1s.shape != (E, N // GROUP, Kd // GROUP):
@@ -409,15 +416,16 @@ def grouped_gemm_fp8_swiglu(xq: torch.Tensor, xs: torch.Tensor, w1q: torch.Tenso
 # ------------------------------------------------------------------ SwiGLU
 def swiglu_quant(c1: torch.Tensor, save_h: bool = False):
     """h = silu(gate)*up (gate = columns [0,I), up = [I,2I)) requantised 1x128.
-    c1 [R,2I] bf16 -> (hq [R,I] fp8, hs [R,I/128] f32), plus h as bf16 [R,I]
-    when ``save_h`` (the fc2 wgrad operand for the backward pass)."""
+    c1 [R,2I] bf16 -> (hq [R,pad128(I)] fp8, hs [R,pad128(I)/128] f32), plus
+    h as bf16 [R,I] when ``save_h`` (the fc2 wgrad operand for the backward
+    pass)."""
     _check(c1, "c1", (torch.bfloat16,), 2)
     R, I2 = c1.shape
     if I2 % 2:
         raise ValueError("c1 must have an even number of columns (gate | up)")
     I = I2 // 2
-    hq = torch.empty((R, I), dtype=FP8, device=c1.device)
-    hs = torch.empty((R, I // GROUP), dtype=torch.float32, device=c1.device)
+    hq = torch.empty((R, pad128(I)), dtype=FP8, device=c1.device)
+    hs = torch.empty((R, nblocks(I)), dtype=torch.float32, device=c1.device)
     h = torch.empty((R, I), dtype=torch.bfloat16, device=c1.device) if save_h else None
     _C.call("smoe_swiglu_quant_h", _ptr(c1), R, I, _ptr(hq), _ptr(hs), _ptr(h), _stream())
     return (hq, hs, h) if save_h else (hq, hs)
@@ -546,6 +554,13 @@ def swiglu_bwd_quant(c1: torch.Tensor, dh: torch.Tensor, offsets: torch.Tensor,
     E = offsets.numel() - 1
     ld = int(_C.lib().smoe_quant_cols_ld(R, E))
     dev = c1.device
+    if I % GROUP:
+        # dc1's 1x128 row groups straddle the dg | du boundary when I is not
+        # a multiple of 128, which the fused kernel's column slabs assume: the
+        # same bytes from the SwiGLU backward kernel and the one-read quantiser
+        dc1 = swiglu_bwd(c1, dh)
+        out = quant_rows_cols(dc1, offsets)
+        return out + (dc1,) if save_dc1 else out
     dcq = torch.empty((R, N), dtype=FP8, device=dev)
     dcs = torch.empty((R, N // GROUP), dtype=torch.float32, device=dev)
     dcTq = torch.empty((N, ld), dtype=FP8, device=dev)
@@ -650,8 +665,8 @@ def unpermute_combine_bwd_quant(dout: torch.Tensor, y: torch.Tensor, inv_map: to
     E = offsets.numel() - 1
     ld = int(_C.lib().smoe_quant_cols_ld(R, E))
     dev = dout.device
-    dyq = torch.empty((R, H), dtype=FP8, device=dev)
-    dys = torch.empty((R, H // GROUP), dtype=torch.float32, device=dev)
+    dyq = torch.empty((R, pad128(H)), dtype=FP8, device=dev)
+    dys = torch.empty((R, nblocks(H)), dtype=torch.float32, device=dev)
     dyTq = torch.empty((H, ld), dtype=FP8, device=dev)
     dyTs = torch.empty((H, ld // GROUP), dtype=torch.float32, device=dev)
     pad = torch.empty(E + 1, dtype=torch.int32, device=dev)

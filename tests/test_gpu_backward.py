@@ -351,7 +351,8 @@ def _layer_case(dev, T, H, I, E, K):
     return m, x, st, dout, fwd, r
 
 
-CASES = [(256, 256, 256, 8, 2), (1024, 2048, 768, 128, 8)]
+# the last case is GPT-OSS-shaped (H = I = 2880: short last 128-groups)
+CASES = [(256, 256, 256, 8, 2), (1024, 2048, 768, 128, 8), (256, 2880, 2880, 8, 4)]
 
 
 @pytest.mark.parametrize("T,H,I,E,K", CASES)
@@ -367,7 +368,7 @@ def test_layer_backward_stagewise(dev, T, H, I, E, K):
     dy, dw = ops.unpermute_combine_bwd(dout.to(dev), st["y"], inv, st["topk_w"])
     assert np.array_equal(u16(dy), r["dy"])
     close(dw.cpu().numpy(), r["dw"], "dtopk_w")
-    w2tq, w2ts = ops.transpose_blockwise(w2q, w2s)
+    w2tq, w2ts = ops.transpose_blockwise(w2q, w2s, k=I)
     dh = ops.grouped_gemm_fp8(*ops.quant_rows(dy), w2tq, w2ts, off)
     close(f(u16(dh)), f(r["dh"]), "dh", bf16_out=True)
     aq, as_, pad, ld = ops.quant_cols(dy, off)
@@ -375,7 +376,7 @@ def test_layer_backward_stagewise(dev, T, H, I, E, K):
     close(ops.grouped_gemm_fp8_wgrad(aq, as_, bq, bs_, pad, ld).cpu().numpy(), r["dW2"], "dW2")
     dc1 = ops.swiglu_bwd(st["c1"], bf(r["dh"], dev))
     assert np.array_equal(u16(dc1), r["dc1"])
-    w1tq, w1ts = ops.transpose_blockwise(w1q, w1s)
+    w1tq, w1ts = ops.transpose_blockwise(w1q, w1s, k=H)
     dxs = ops.grouped_gemm_fp8(*ops.quant_rows(dc1), w1tq, w1ts, off)
     close(f(u16(dxs)), f(r["dxs"]), "dxs", bf16_out=True)
     cq, cs, _, _ = ops.quant_cols(dc1, off)

@@ -119,14 +119,23 @@ def test_fused_swiglu_dsv3_full_shape(dev):
 
 
 def test_fused_swiglu_rejects_bad_shapes(dev):
+    """I = 200 (not a multiple of 16) is refused; I = 192 (a multiple of 16,
+    not of 128) is computed as the GEMM followed by the SwiGLU kernel, the
+    bytes the fused op promises."""
     say("fused swiglu bad shapes")
     xq = torch.zeros((4, 128), dtype=torch.float8_e4m3fn, device=dev)
     xs = torch.ones((4, 1), device=dev)
-    wq = torch.zeros((1, 384, 128), dtype=torch.float8_e4m3fn, device=dev)  # I = 192
-    ws = torch.ones((1, 3, 1), device=dev)
     off = torch.tensor([0, 4], dtype=torch.int32, device=dev)
+    wq = torch.zeros((1, 400, 128), dtype=torch.float8_e4m3fn, device=dev)  # I = 200
+    ws = torch.ones((1, 4, 1), device=dev)
     with pytest.raises(ValueError):
         ops.grouped_gemm_fp8_swiglu(xq, xs, wq, ws, off)
+    aq, as_ = ops.quant_rows(W.tokens(4, 128, device=dev))
+    wq, ws = ops.quantize_weight_blockwise(W.weights(1, 384, 128, device=dev))  # I = 192
+    hq, hs = ops.grouped_gemm_fp8_swiglu(aq, as_, wq, ws, off)
+    rq, rs = ops.swiglu_quant(ops.grouped_gemm_fp8(aq, as_, wq, ws, off))
+    assert hq.shape == (4, 256)
+    assert torch.equal(hq.view(torch.uint8), rq.view(torch.uint8)) and torch.equal(hs, rs)
 
 
 def test_simple_moe_inference_path_equals_training_path(dev):

@@ -166,3 +166,47 @@ def test_short_dims_rejected():
     # K must be the padded pitch
     assert lib.smoe_grouped_gemm_fp8(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 8, 2880, 2880, FAKE, None, 0,
                                      None) == -3
+
+
+@pytest.mark.parametrize("T,H,I,E,K", [(512, 2880, 2880, 8, 4), (300, 400, 272, 4, 2)])
+def test_simple_moe_forward_short_dims(dev, T, H, I, E, K):
+    """SimpleMoE at GPT-OSS's H = I = 2880 (and an odd 400 / 272 case), both
+    the inference path (fc1 + SwiGLU composed from the GEMM and the SwiGLU
+    kernel, since I is not a multiple of 128) and the path that saves
+    intermediates, against the oracle's whole layer on the same fp8
+    weights: ids, maps and fp8 bytes bit-exact, GEMM stages and the output
+    within the GEMM tolerance."""
+    import smoe
+    say("SimpleMoE short dims", T, H, I, E, K)
+    m = smoe.SimpleMoE(H, I, E, K, device=dev)
+    with torch.no_grad():
+        m.w1.copy_(W.weights(E, 2 * I, H, seed=3).to(dev))
+        m.w2.copy_(W.weights(E, H, I, seed=13).to(dev))
+    x, lg = W.tokens(T, H), W.logits(T, E)
+    out, st = m(x.to(dev), lg.to(dev), return_intermediates=True)
+    with torch.no_grad():
+        inf = m(x.to(dev), lg.to(dev))
+    assert torch.equal(inf.view(torch.int16), out.view(torch.int16))
+    w1q, w1s, w2q, w2s = m.fp8_weights()
+    r = O.moe_forward(u16(x), lg.numpy(), u8(w1q), w1s.cpu().numpy(), u8(w2q), w2s.cpu().numpy(), K)
+    for k in ("topk_idx", "topk_w", "row_map", "inv_map", "offsets", "xs"):
+        assert np.array_equal(st[k].cpu().numpy(), r[k]), k
+    assert np.array_equal(u8(st["xq"]), r["xq"])
+    f = lambda a: O.bf16_to_f32(a).astype(np.float64)
+    gemm_close(f(u16(st["c1"])), f(r["c1"]), "fc1", bf16_ref=False)
+    # hq from the kernel's own c1: bit-exact (same input)
+    rq, rs = O.swiglu_quant(u16(st["c1"]))
+    assert np.array_equal(u8(st["hq"]), rq) and np.array_equal(st["hs"].cpu().numpy(), rs)
+    # fc2 on the kernel's own hq, and the combine of the kernel's own y
+    offs = st["offsets"].cpu().numpy()
+    ry = O.grouped_gemm_fp8(u8(st["hq"]), st["hs"].cpu().numpy(), u8(w2q), w2s.cpu().numpy(), offs)
+    gemm_close(f(u16(st["y"])), ry, "fc2")
+    rout = O.unpermute_combine(u16(st["y"]), st["inv_map"].cpu().numpy(), st["topk_w"].cpu().numpy(), K)
+    assert np.array_equal(u16(out), rout)
+    # end to end against the oracle's own chain: an fp8 requantisation flip
+    # where c1 differs in its last bf16 bit moves a whole h group, so the
+    # bounds are 2e-2 (max) and 2e-3 (mean) here, as for the backward end to
+    # end (the stages above hold the contract's bars)
+    d = np.abs(f(u16(out)) - f(r["out"]))
+    ref = np.abs(f(r["out"]))
+    assert d.max() / ref.max() <= 2e-2 and d.mean() / ref.mean() <= 2e-3
