@@ -15,8 +15,15 @@
  *   - the caller owns every buffer; the library allocates no device memory;
  *   - bf16 tensors are passed as uint16_t (raw bf16 bits), fp8 tensors as
  *     uint8_t holding OCP float8_e4m3fn bytes (max 448, 0x7f/0xff = NaN);
- *   - every pointer must be 16-byte aligned; H, I, N and the GEMM K dimension
- *     must be multiples of 128; E <= SMOE_MAX_EXPERTS.
+ *   - every pointer must be 16-byte aligned; E <= SMOE_MAX_EXPERTS;
+ *   - H, I, N and C (the row length of a quantised tensor) must be multiples
+ *     of 16; a GEMM's K argument is the fp8 operands' row pitch, a multiple
+ *     of 128.  A dimension D that is not a multiple of 128 (GPT-OSS:
+ *     H = I = 2880) is quantised as if zero-padded to Dp = ceil(D/128)*128:
+ *     the short last group's amax is over its valid elements, its padding is
+ *     byte 0, and the fp8 tensor keeps the padded pitch Dp (its scales have
+ *     Dp/128 groups per row); a weight's short last row or column block is
+ *     the zero-padded block.  bf16 tensors keep the tight pitch D.
  *
  * Semantics (binding for the kernels and the CPU oracle alike):
  *   pair p = t*K + k; rows are sorted stably by expert id, ties by ascending p;
@@ -42,7 +49,8 @@ enum {
   SMOE_OK = 0,
   SMOE_EINVAL_NULL = -1,      /* a required pointer is NULL                 */
   SMOE_EINVAL_DIM = -2,       /* a dimension is <= 0 or out of range         */
-  SMOE_EINVAL_ALIGN128 = -3,  /* H / I / N / Kdim not a multiple of 128      */
+  SMOE_EINVAL_ALIGN128 = -3,  /* a dimension not a multiple of 16 (128 where
+                                 noted, e.g. a GEMM's padded K)              */
   SMOE_EINVAL_EXPERTS = -4,   /* E <= 0 or E > SMOE_MAX_EXPERTS              */
   SMOE_EINVAL_WORKSPACE = -5, /* workspace NULL or smaller than required     */
   SMOE_EINVAL_PTRALIGN = -6,  /* a pointer is not 16-byte aligned            */
@@ -138,7 +146,8 @@ int smoe_route_topk_sort(const float* logits, const float* bias, int T, int E, i
 /*
  * Fused permute + 1x128 fp8 quantisation.  Each token row of x [T,H] bf16 is
  * read once, quantised once and its fp8 bytes and scales written to the K
- * sorted rows inv_map[t*K+k]: xq [T*K,H] u8, xs [T*K,H/128] f32.
+ * sorted rows inv_map[t*K+k]: xq [T*K,Hp] u8, xs [T*K,Hp/128] f32 (Hp =
+ * H padded to a multiple of 128, see the conventions above).
  * Replaces Dispatcher.permute(x, routing_map) followed by the separate
  * quantize_fp8 launches (notes/2026-04/2026-04-21_gptoss_10_moe_fp8_grouped_gemm_diagnosis.md:38-46)
  * with the blockwise 1x128 activation recipe
@@ -158,7 +167,8 @@ int smoe_dispatch_quant(const uint16_t* x, const int32_t* topk_idx, int T, int H
 
 /*
  * 128x128 blockwise fp8 weight quantisation.  w [E,N,Kdim] bf16 (Kdim
- * contiguous, "NK" layout) -> wq [E,N,Kdim] u8, ws [E,N/128,Kdim/128] f32.
+ * contiguous, "NK" layout) -> wq [E,N,Kp] u8, ws [E,ceil(N/128),Kp/128] f32
+ * with Kp = Kdim padded to a multiple of 128 (padding columns 0).
  * Replaces the weight-cache refresh (summary/fp8_expert_gemm_optimization.md:135-143)
  * under the 128x128 weight-block recipe (moe/MegatronCore_MoE_reading_notes.md:498-501).
  */
@@ -197,8 +207,9 @@ int smoe_selftest_recip(unsigned long long* counts, void* stream);
  * Dropless fp8 grouped GEMM with blockwise scales.  For each expert e and each
  * row r in [offsets[e], offsets[e+1]):
  *   c[r,n] = bf16( sum_kb as[r,kb]*bs[e,n/128,kb] * sum_{k in kb} a[r,k]*b[e,n,k] )
- * a [R,Kdim] u8, as [R,Kdim/128] f32, b [E,N,Kdim] u8, bs [E,N/128,Kdim/128] f32,
- * offsets [E+1] i32 on the device -> c [R,N] bf16.  Zero-token experts
+ * a [R,Kdim] u8, as [R,Kdim/128] f32, b [E,N,Kdim] u8, bs [E,ceil(N/128),Kdim/128]
+ * f32, offsets [E+1] i32 on the device -> c [R,N] bf16; Kdim is the padded
+ * pitch (a multiple of 128), N a multiple of 16.  Zero-token experts
  * produce no tiles.  offsets[] is read on the device only; the kernel clamps
  * every expert's range to rows [0, R), so malformed offsets (decreasing, or
  * past R) never cause an access outside a, as or c.  ws may be NULL
@@ -221,7 +232,8 @@ int smoe_grouped_gemm_fp8(const uint8_t* a, const float* as, const uint8_t* b,
  * f32, byte for byte, without the c1 round trip through HBM.  w1 [E,2I,Kdim]
  * u8 holds gate rows [0,I) and up rows [I,2I); w1s [E,2I/128,Kdim/128].  c1
  * may be NULL; when given it also receives the bf16 fc1 output (the backward
- * pass needs it).  Requires I % 128 == 0 and 2*I*Kdim < 2^31.
+ * pass needs it).  Requires I % 128 == 0 (the epilogue pairs 128-column gate
+ * and up blocks; other I take the two-kernel path) and 2*I*Kdim < 2^31.
  * Replaces the grouped GEMM + activation_func_with_probs pair of the expert
  * FFN (moe/MoE_detailed_computation_dataflow.md:168-174;
  * notes/2026-04/2026-04-21_gptoss_10_moe_fp8_grouped_gemm_diagnosis.md:39-46).
@@ -235,7 +247,7 @@ int smoe_grouped_gemm_fp8_swiglu(const uint8_t* a, const float* as, const uint8_
  * output of smoe_quantize_weight_blockwise) -> wp [E,N,Kdim] bytes in MFMA
  * fragment order: [E][N/16][Kdim/128][2][64][16 B], where half h, lane l holds
  * row 16*nb + l%16 at K offsets 128*kb + 64*h + 16*(l/16) .. +16.  The scales
- * are unchanged.  Requires N % 128 == 0 and Kdim % 128 == 0.
+ * are unchanged.  Requires N % 16 == 0 and Kdim % 128 == 0.
  * Replaces the fp8 weight cache refresh that keeps each layout the kernels
  * need (_refresh_fp8_weight_cache caching KN and NK,
  * summary/fp8_expert_gemm_optimization.md:133-137).
@@ -272,7 +284,8 @@ int smoe_grouped_gemm_fp8_packed_swiglu(const uint8_t* a, const float* as, const
 
 /*
  * SwiGLU + 1x128 requantisation.  c1 [R,2I] bf16 with gate columns [0,I) and
- * up columns [I,2I): h = silu(g)*u in fp32 -> hq [R,I] u8, hs [R,I/128] f32.
+ * up columns [I,2I): h = silu(g)*u in fp32 -> hq [R,Ip] u8, hs [R,Ip/128] f32
+ * (Ip = I padded to a multiple of 128; h's columns past I are 0).
  * silu(g) = g / (1 + exp(-g)) with exp evaluated by the library's own
  * fp32 routine (Cody-Waite reduction + degree-7 Taylor polynomial).
  * Replaces activation_func_with_probs / the SwiGLU elementwise kernel
@@ -313,16 +326,19 @@ int smoe_unpermute_combine(const uint16_t* y, const int32_t* inv_map, const floa
 
 /*
  * Plain 1x128 row quantisation (no permutation): x [M,C] bf16 ->
- * q [M,C] u8, s [M,C/128] f32 with the forward rule.  Used for output grads
+ * q [M,Cp] u8, s [M,Cp/128] f32 with the forward rule (Cp = C padded to a
+ * multiple of 128).  Used for output grads
  * entering the dgrad GEMM (replaces quantize_fp8 of the grad,
  * notes/2026-04/2026-04-21_gptoss_10_moe_fp8_grouped_gemm_diagnosis.md:99).
  */
 int smoe_quant_rows_1x128(const uint16_t* x, int M, int C, uint8_t* q, float* s, void* stream);
 
 /*
- * Blockwise weight transpose for dgrad: wq [E,N,K] u8 + ws [E,N/128,K/128]
- * -> wqT [E,K,N] + wsT [E,K/128,N/128].  128x128 block quantisation commutes
- * with the transpose, so no requantisation is needed.  Replaces the NK/KN
+ * Blockwise weight transpose for dgrad: wq [E,N,Kp] u8 + ws [E,NB,KB]
+ * -> wqT [E,Kdim,Np] + wsT [E,KB,NB], with Kdim the weight's true K (Kp its
+ * padded pitch), Np = N padded to a multiple of 128 (columns past N are 0),
+ * NB = Np/128, KB = Kp/128.  128x128 block quantisation commutes with the
+ * transpose, so no requantisation is needed.  Replaces the NK/KN
  * weight cache (summary/fp8_expert_gemm_optimization.md:135-143).
  */
 int smoe_transpose_blockwise_fp8(const uint8_t* wq, const float* ws, int E, int N, int Kdim,
@@ -335,6 +351,7 @@ int smoe_transpose_blockwise_fp8(const uint8_t* wq, const float* ws, int E, int 
  * tokens of the forward, gathered on the fly).  Each expert's rows are split
  * into 128-row groups from its first row (short last groups zero-padded);
  * group g of expert e is column block pad[e]/128 + g of the output.
+ * C need only be a multiple of 16 (xTq has C rows).
  * -> xTq [C, ld] u8,
  * xTs [C, ld/128] f32, pad [E+1] i32 (pad[e+1] = pad[e] + ceil(count/128)*128).
  * ld must be >= smoe_quant_cols_ld(R, E) (an upper bound known on the host;
@@ -349,7 +366,7 @@ int smoe_quant_cols_128x1(const uint16_t* x, const int32_t* gather, int gather_d
 
 /*
  * Both quantisations of one tensor from a single read: x [R,C] bf16 ->
- * the 1x128 row quantisation xq [R,C] u8 + xs [R,C/128] f32 (the bytes of
+ * the 1x128 row quantisation xq [R,Cp] u8 + xs [R,Cp/128] f32 (the bytes of
  * smoe_quant_rows_1x128) and the transposed 128x1 column quantisation
  * xTq / xTs / pad of smoe_quant_cols_128x1 (no gather).  Rows are those of
  * the expert segments offsets[E+1], which must cover [0, R) for every row
@@ -369,7 +386,8 @@ int smoe_quant_rows_cols(const uint16_t* x, int R, int C, const int32_t* offsets
  * smoe_quant_rows_cols outputs of dc1 (dcq [R,2I] u8, dcs [R,2I/128],
  * dcTq [2I,ld] u8, dcTs [2I,ld/128], pad) without storing dc1 itself,
  * unless dc1 is not NULL.  Same bytes as smoe_swiglu_bwd followed by
- * smoe_quant_rows_cols.  Replaces the "dexpert" activation backward and
+ * smoe_quant_rows_cols.  Requires I % 128 == 0 (a workgroup takes one
+ * 128-column slab of each half; other I take those two calls).  Replaces the "dexpert" activation backward and
  * the requantisation of its gradient
  * (moe/MoE_detailed_computation_dataflow.md:209-226;
  * moe/MegatronCore_MoE_reading_notes.md:498-501).
@@ -383,7 +401,7 @@ int smoe_swiglu_bwd_quant(const uint16_t* c1, const uint16_t* dh, int R, int I,
  *   dW[e][n][k] = sum over expert e's groups g of aTs[n,g]*bTs[k,g]*sum_r aT[n,r]*bT[k,r]
  * aT [N, ld] / bT [Kdim, ld] u8 and scales [*, ld/128] from
  * smoe_quant_cols_128x1, pad [E+1] -> dW [E, N, Kdim] f32 (zeros for experts
- * without rows).  Replaces the grouped variable-K wgrad
+ * without rows).  N and Kdim must be multiples of 16.  Replaces the grouped variable-K wgrad
  * (notes/2026-04/2026-04-25_gptoss_21_turbo_grouped_mlp_trace_evidence.md:95).
  */
 int smoe_grouped_gemm_fp8_wgrad(const uint8_t* aT, const float* aTs, const uint8_t* bT,
@@ -435,7 +453,7 @@ int smoe_unpermute_combine_bwd(const uint16_t* dout, const uint16_t* y, const in
 /*
  * Combine backward fused with both quantisations of dy: writes dw [T,K] f32
  * as smoe_unpermute_combine_bwd does, and, without storing dy [T*K,H], the
- * smoe_quant_rows_cols outputs of dy (dyq [T*K,H] u8, dys [T*K,H/128],
+ * smoe_quant_rows_cols outputs of dy (dyq [T*K,Hp] u8, dys [T*K,Hp/128],
  * dyTq [H,ld] u8, dyTs [H,ld/128], pad) over the expert segments offsets:
  * row r of dy is rebuilt inside the quantiser as bf16(w[p]*dout[p/K]) with
  * p = row_map[r] (row_map and inv_map inverse permutations of [0, T*K),
