@@ -378,6 +378,39 @@ def bench_fwd_bwd(dev, steps, warmup):
     return out
 
 
+def bench_fwd_bwd_one_stream(dev, steps, warmup):
+    """The config-5 step of ``bench_fwd_bwd`` (forward with saved
+    intermediates + ``backward_from``) with the weight-gradient stream
+    replaced by the caller's stream: every kernel runs alone, which gives
+    their isolated durations in a kernel trace, and the step time shows what
+    the second stream's overlap is worth."""
+    import torch
+    import smoe
+    from smoe import workloads as W
+    c = W.CONFIGS["qwen3"]
+    m = smoe.SimpleMoE(c.H, c.I, c.E, c.K, device=dev)
+    with torch.no_grad():
+        m.w1.copy_(W.weights(c.E, 2 * c.I, c.H, device=dev))
+        m.w2.copy_(W.weights(c.E, c.H, c.I, device=dev, seed=13))
+    m.refresh_fp8_cache()
+    x, lg = W.tokens(c.T, c.H, device=dev), W.logits(c.T, c.E, device=dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(4)
+    dout = (torch.randn((c.T, c.H), generator=g, device=dev) * 1e-3).to(torch.bfloat16)
+
+    def step():
+        _, st = m(x, lg, return_intermediates=True)
+        m.backward_from(st, dout)
+
+    t2 = timed_median(step, steps, warmup)
+    m._side_stream = lambda device: torch.cuda.current_stream()
+    t1 = timed_median(step, steps, warmup)
+    del m
+    torch.cuda.empty_cache()
+    return {"workload": "qwen3 layer fwd+bwd T=16384 H=2048 I=768 E=128 top8",
+            "ms_two_streams": round(t2, 4), "ms_one_stream": round(t1, 4)}
+
+
 def bench_ceiling(dev, c, iters=20):
     """The HBM's rate for the dispatch step's traffic mix without the
     quantisation: smoe_bw_probe reads the config-2 input (T rows of H bf16)
@@ -435,7 +468,9 @@ def run_only(args, dev, c):
     ceiling = the HBM traffic-mix probe, blaslt = hipBLASLt's dense fp8 GEMM
     at the config-4 shapes, router = the fused router + sort at config 2,
     wgrad = the config-5 fc1 weight gradient, fwdbwd = the config-5 layer
-    forward + backward, layer = the config-3 (Mixtral) layer forward."""
+    forward + backward, fwdbwd1 = the same with the weight gradients on the
+    caller's stream (every kernel alone), layer = the config-3 (Mixtral)
+    layer forward."""
     import torch
     from smoe import ops, workloads as W
     if args.only == "copy":
@@ -459,6 +494,8 @@ def run_only(args, dev, c):
         print(json.dumps({"only": "router", **bench_router(dev, c, args.steps, args.warmup)}))
     elif args.only == "fwdbwd":
         print(json.dumps({"only": "fwdbwd", **bench_fwd_bwd(dev, args.steps, args.warmup)}))
+    elif args.only == "fwdbwd1":
+        print(json.dumps({"only": "fwdbwd1", **bench_fwd_bwd_one_stream(dev, args.steps, args.warmup)}))
     elif args.only == "layer":
         print(json.dumps({"only": "layer", **bench_layer(dev, args.steps, args.warmup)}))
     elif args.only == "gemm":
@@ -696,7 +733,7 @@ def main():
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--only", choices=["permute", "gemm", "combine", "copy", "fwdbwd", "ceiling",
                                        "blaslt", "router", "wgrad", "layer", "refshapes",
-                                       "bwdparts"],
+                                       "bwdparts", "fwdbwd1"],
                     help="run one kernel family only (for rocprofv3 runs) and print its timing")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
