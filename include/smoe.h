@@ -23,7 +23,8 @@
  *     the short last group's amax is over its valid elements, its padding is
  *     byte 0, and the fp8 tensor keeps the padded pitch Dp (its scales have
  *     Dp/128 groups per row); a weight's short last row or column block is
- *     the zero-padded block.  bf16 tensors keep the tight pitch D.
+ *     the zero-padded block.  bf16 tensors keep the tight pitch D.  (Blockwise
+ *     fp8 GEMMs align dimensions to 16: moe/MegatronCore_MoE_reading_notes.md:541-543.)
  *
  * Semantics (binding for the kernels and the CPU oracle alike):
  *   pair p = t*K + k; rows are sorted stably by expert id, ties by ascending p;

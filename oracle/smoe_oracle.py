@@ -27,7 +27,8 @@ and is binding for the kernels too:
      e.g. GPT-OSS H = I = 2880) is quantised as the operand zero-padded to
      pad128(D): a short last group's amax is over its valid elements, its
      padding is byte 0, fp8 operands keep the padded pitch, and a short last
-     weight block (rows or columns) is the zero-padded block.
+     weight block (rows or columns) is the zero-padded block.  Blockwise fp8
+     GEMMs need dimensions aligned to 16 (moe/MegatronCore_MoE_reading_notes.md:541-543).
 
 Floating-point evaluation order is part of the contract where a kernel is
 bit-exact (router softmax reduction tree, exp routine, combine order): the
