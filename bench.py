@@ -367,11 +367,16 @@ def bench_fwd_bwd(dev, steps, warmup):
         m.w2.main_grad.add_(g["dw2"])
 
     tu = timed_median(unfused_step, steps, warmup)
-    del m.w1.main_grad, m.w2.main_grad, m
+    del m.w1.main_grad, m.w2.main_grad
+    # the opt-in E8M0 weight-gradient recipe on the same step
+    m.wgrad_recipe = "e8m0"
+    te = timed_median(step, steps, warmup)
+    del m
     torch.cuda.empty_cache()
     out.update({"ms_autograd": round(ta, 4), "tflops_autograd": tf(ta),
                 "ms_autograd_main_grad": round(tm, 4), "tflops_autograd_main_grad": tf(tm),
                 "ms_main_grad_unfused_add": round(tu, 4),
+                "ms_e8m0_wgrad": round(te, 4), "tflops_e8m0_wgrad": tf(te),
                 "autograd_note": "loss.backward() through SimpleMoE, grads reset per step; "
                                  "main_grad = fp32 buffers accumulated in the wgrad epilogue; "
                                  "unfused = fp32 dW then main_grad.add_"})
@@ -531,8 +536,15 @@ def bench_wgrad(dev, steps, warmup):
         dW = torch.empty((c.E, N, K), dtype=torch.float32, device=dev)
         ms = timed_median(lambda: ops.grouped_gemm_fp8_wgrad(aq, as_, bq, bs_, pad, ld, out=dW),
                           steps, warmup)
-        out[name] = {"ms": round(ms, 4), "tflops": round(2.0 * R * N * K / (ms * 1e-3) / 1e12, 1),
+        tfl = lambda t: round(2.0 * R * N * K / (t * 1e-3) / 1e12, 1)
+        out[name] = {"ms": round(ms, 4), "tflops": tfl(ms),
                      "max_expert_share": round(max(counts) / R, 3)}
+        # the E8M0 recipe: power-of-two operand scales applied by the MFMA
+        aq, as_, pad, ld = ops.quant_cols(dc1, off, col_scale="pow2")
+        bq, bs_, _, _ = ops.quant_cols(xs, off, col_scale="pow2")
+        me = timed_median(lambda: ops.grouped_gemm_fp8_wgrad(aq, as_, bq, bs_, pad, ld, out=dW,
+                                                             e8m0=True), steps, warmup)
+        out[name].update({"e8m0_ms": round(me, 4), "e8m0_tflops": tfl(me)})
         del aq, bq, dW
     torch.cuda.empty_cache()
     return out
@@ -617,10 +629,13 @@ def bench_reference_shapes(dev, steps, warmup):
     del flush
     torch.cuda.empty_cache()
     out["fp8_blockwise_fwd_bwd_E32_M4096_H2880"] = _grouped_fc_fwd_bwd(dev, 2880, steps, warmup)
+    e = _grouped_fc_fwd_bwd(dev, 2880, steps, warmup, e8m0=True)
+    out["fp8_e8m0_wgrad_fwd_bwd_E32_M4096_H2880"] = {k: e[k] for k in ("fc1_ms", "fc2_ms", "sum_ms",
+                                                                       "tflops")}
     return out
 
 
-def _grouped_fc_fwd_bwd(dev, hid, steps, warmup):
+def _grouped_fc_fwd_bwd(dev, hid, steps, warmup, e8m0=False):
     """fc1 and fc2 of the GPT-OSS expert shape (32 experts x 4096 rows, fc1
     N = 2I K = H, fc2 N = H K = I, H = I = ``hid``) forward and backward with
     1x128 / 128x1 / 128x128 block scales, each as its autograd function runs
@@ -634,12 +649,15 @@ def _grouped_fc_fwd_bwd(dev, hid, steps, warmup):
     is at H = I = 2880, 22.5 groups of 128: the fp8 operands are quantised as
     zero-padded to 2944 (the short last group's scale from its 64 valid
     values), so fc1 runs K = 2944 and fc2 N = 2880 with a partial last tile.
-    The FLOP count is the reference's, at 2880."""
+    The FLOP count is the reference's, at 2880.  ``e8m0``: the weight
+    gradient's 128x1 operands take power-of-two scales and the wgrad GEMM
+    applies them in the MFMA (the opt-in E8M0 recipe)."""
     import torch
     from smoe import ops, workloads as W
     E, M = 32, 4096
     R = E * M
     off = W.offsets_from_counts([M] * E, dev)
+    cs = "pow2" if e8m0 else "fp32"
     res = {}
     for name, N, Kd in (("fc1", 2 * hid, hid), ("fc2", hid, hid)):
         a = W.tokens(R, Kd, device=dev, seed=31)
@@ -655,10 +673,10 @@ def _grouped_fc_fwd_bwd(dev, hid, steps, warmup):
         def fwd_bwd():
             aq, as_ = ops.quant_rows(a)
             ops.grouped_gemm_fp8(aq, as_, wf, ws, off, out=y)
-            dq, ds, dTq, dTs, pad, ld = ops.quant_rows_cols(dyv, off)
+            dq, ds, dTq, dTs, pad, ld = ops.quant_rows_cols(dyv, off, col_scale=cs)
             ops.grouped_gemm_fp8(dq, ds, wtf, wts, off, out=da)
-            aTq, aTs, _, _ = ops.quant_cols(a, off)
-            ops.grouped_gemm_fp8_wgrad(dTq, dTs, aTq, aTs, pad, ld, out=dw)
+            aTq, aTs, _, _ = ops.quant_cols(a, off, col_scale=cs)
+            ops.grouped_gemm_fp8_wgrad(dTq, dTs, aTq, aTs, pad, ld, out=dw, e8m0=e8m0)
 
         res[name + "_ms"] = round(timed_median(fwd_bwd, steps, warmup), 4)
         res[name + "_kernels"] = "packed" if isinstance(wf, ops.PackedWeight) else "plain"

@@ -323,7 +323,22 @@ int smoe_unpermute_combine(const uint16_t* y, const int32_t* inv_map, const floa
  * "variable-K" grouped GEMM of the reference's backends
  * (notes/2026-04/2026-04-21_gptoss_10_moe_fp8_grouped_gemm_diagnosis.md:125,
  * notes/2026-04/2026-04-25_gptoss_21_turbo_grouped_mlp_trace_evidence.md:95).
+ *
+ * The 128x1 column quantisers (the wgrad operands) take col_scale:
+ *   SMOE_COLSCALE_FP32  s = amax/448 (fp32 RN, 1 when amax == 0), the rule
+ *                       of every other quantiser;
+ *   SMOE_COLSCALE_POW2  s = the least power of two >= RN(amax/448), at least
+ *                       2^-127 (1 when amax == 0).  x/s is then exact and s is
+ *                       an E8M0 value, which the wgrad's scaled MFMA applies
+ *                       in hardware (SMOE_WGRAD_E8M0).  This is the
+ *                       power-of-two scale of the MXFP8 recipe
+ *                       (moe/MegatronCore_MoE_reading_notes.md:503-504) at the
+ *                       blockwise recipe's 128-row granularity; it is opt-in.
+ * Any other value returns SMOE_EINVAL_MODE.  The 1x128 row outputs always
+ * use the FP32 rule.
  * ------------------------------------------------------------------------- */
+#define SMOE_COLSCALE_FP32 0
+#define SMOE_COLSCALE_POW2 1
 
 /*
  * Plain 1x128 row quantisation (no permutation): x [M,C] bf16 ->
@@ -363,7 +378,7 @@ int smoe_transpose_blockwise_fp8(const uint8_t* wq, const float* ws, int E, int 
 int smoe_quant_cols_ld(int R, int E);
 int smoe_quant_cols_128x1(const uint16_t* x, const int32_t* gather, int gather_div, int R, int C,
                           const int32_t* offsets, int E, int ld, uint8_t* xTq, float* xTs,
-                          int32_t* pad, void* stream);
+                          int32_t* pad, int col_scale, void* stream);
 
 /*
  * Both quantisations of one tensor from a single read: x [R,C] bf16 ->
@@ -378,7 +393,7 @@ int smoe_quant_cols_128x1(const uint16_t* x, const int32_t* gather, int gather_d
  */
 int smoe_quant_rows_cols(const uint16_t* x, int R, int C, const int32_t* offsets, int E, int ld,
                          uint8_t* xq, float* xs, uint8_t* xTq, float* xTs, int32_t* pad,
-                         void* stream);
+                         int col_scale, void* stream);
 
 /*
  * SwiGLU backward fused into both quantisations of its output: computes
@@ -395,7 +410,8 @@ int smoe_quant_rows_cols(const uint16_t* x, int R, int C, const int32_t* offsets
  */
 int smoe_swiglu_bwd_quant(const uint16_t* c1, const uint16_t* dh, int R, int I,
                           const int32_t* offsets, int E, int ld, uint8_t* dcq, float* dcs,
-                          uint8_t* dcTq, float* dcTs, int32_t* pad, uint16_t* dc1, void* stream);
+                          uint8_t* dcTq, float* dcTs, int32_t* pad, uint16_t* dc1, int col_scale,
+                          void* stream);
 
 /*
  * Variable-K grouped fp8 GEMM for weight gradients:
@@ -423,12 +439,18 @@ int smoe_grouped_gemm_fp8_wgrad(const uint8_t* aT, const float* aTs, const uint8
  * the fp32 main_grad (notes/mlperf-llama/2026-04-29_nemo_vs_primus_config_diff.md:233-235),
  * and the bf16 main_grads_dtype of the reference's GPT-OSS runs
  * (notes/2026-04/2026-04-20_gptoss_05_borrow_from_deepseek_v3_config.md:23,48).
+ * mode may also hold SMOE_WGRAD_E8M0: the operands' scales are powers of two
+ * (SMOE_COLSCALE_POW2), read by their exponent only and applied by the
+ * scaled MFMA (v_mfma_scale_f32_16x16x128_f8f6f4), so the 128-row groups
+ * accumulate in the MFMA with no per-output scale arithmetic.  With scales
+ * that are not powers of two this flag gives wrong results.
  * Any other mode returns SMOE_EINVAL_MODE.
  */
 #define SMOE_WGRAD_F32 0
 #define SMOE_WGRAD_F32_ACC 1
 #define SMOE_WGRAD_BF16 2
 #define SMOE_WGRAD_BF16_ACC 3
+#define SMOE_WGRAD_E8M0 4
 int smoe_grouped_gemm_fp8_wgrad_ex(const uint8_t* aT, const float* aTs, const uint8_t* bT,
                                    const float* bTs, const int32_t* pad, int E, int N, int Kdim,
                                    int ld, void* dW, int mode, void* stream);
@@ -467,7 +489,8 @@ int smoe_unpermute_combine_bwd_quant(const uint16_t* dout, const uint16_t* y,
                                      const int32_t* inv_map, const int32_t* row_map,
                                      const float* w, int T, int K, int H, const int32_t* offsets,
                                      int E, int ld, uint8_t* dyq, float* dys, uint8_t* dyTq,
-                                     float* dyTs, int32_t* pad, float* dw, void* stream);
+                                     float* dyTs, int32_t* pad, float* dw, int col_scale,
+                                     void* stream);
 
 #ifdef __cplusplus
 }

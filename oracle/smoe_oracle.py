@@ -29,6 +29,8 @@ and is binding for the kernels too:
      padding is byte 0, fp8 operands keep the padded pitch, and a short last
      weight block (rows or columns) is the zero-padded block.  Blockwise fp8
      GEMMs need dimensions aligned to 16 (moe/MegatronCore_MoE_reading_notes.md:541-543).
+  C10 E8M0 column scales (opt-in, wgrad operands only): s = the least power of
+     two >= RN(amax/448), at least 2^-127 (1 when amax == 0); x/s is exact.
 
 Floating-point evaluation order is part of the contract where a kernel is
 bit-exact (router softmax reduction tree, exp routine, combine order): the
@@ -138,6 +140,18 @@ def group_scale(amax: np.ndarray) -> np.ndarray:
     amax = np.asarray(amax, np.float32)
     s = amax / E4M3_MAX
     return np.where(amax == 0, F32(1.0), s).astype(np.float32)
+
+
+def group_scale_pow2(amax: np.ndarray) -> np.ndarray:
+    """C10 (the optional E8M0 recipe of the wgrad operands): the least power
+    of two >= RN(amax / 448), at least 2^-127; 1 when amax == 0.  Powers of
+    two are the E8M0 scale format of MXFP8 (moe/MegatronCore_MoE_reading_notes.md:503-504)."""
+    amax = np.asarray(amax, np.float32)
+    t = (amax / E4M3_MAX).astype(np.float32)
+    with np.errstate(divide="ignore"):
+        e = np.ceil(np.log2(t.astype(np.float64)))
+    s = np.maximum(np.exp2(e), 2.0 ** -127)
+    return np.where(amax == 0, 1.0, s).astype(np.float32)
 
 
 # ---------------------------------------------------------------------------
@@ -312,7 +326,7 @@ def pad128(d: int) -> int:
     return -(-int(d) // GROUP) * GROUP
 
 
-def quant_1x128(x: np.ndarray):
+def quant_1x128(x: np.ndarray, pow2: bool = False):
     """C3 on rows of x [M, H] float32 -> q [M,Hp] u8, s [M,Hp/128] f32 with
     Hp = pad128(H) (C9: a short last group is the zero-padded group).
     1x128 activation tiles: moe/MegatronCore_MoE_reading_notes.md:498-501."""
@@ -323,7 +337,7 @@ def quant_1x128(x: np.ndarray):
         H = x.shape[1]
     g = x.reshape(M, H // GROUP, GROUP)
     amax = np.abs(g).max(axis=2)
-    s = group_scale(amax)
+    s = group_scale_pow2(amax) if pow2 else group_scale(amax)
     q = quant_rule(g, s[:, :, None]).reshape(M, H)
     return q, s
 
@@ -496,12 +510,13 @@ def pad_offsets(offsets: np.ndarray) -> np.ndarray:
     return pad.astype(np.int32)
 
 
-def quant_cols_128x1(x: np.ndarray, offsets: np.ndarray):
+def quant_cols_128x1(x: np.ndarray, offsets: np.ndarray, pow2: bool = False):
     """Transposed 128x1 quantisation for the wgrad operands.  x [R, C] float32
     with expert row segments offsets[E+1].  Each expert's rows are split into
     groups of 128 starting at its first row (the last group may be short);
     group g of expert e lands at columns pad[e] + 128*g .. of the transposed
-    output, short groups zero-padded.  C3 applies per (column, group).
+    output, short groups zero-padded.  C3 applies per (column, group), or C10
+    (power-of-two scales) with ``pow2``.
     -> xT_q [C, Rp] u8, xT_s [C, Rp/128] f32, pad offsets [E+1] i32."""
     x = np.asarray(x, np.float32)
     R, C = x.shape
@@ -511,7 +526,7 @@ def quant_cols_128x1(x: np.ndarray, offsets: np.ndarray):
     for e in range(len(offsets) - 1):
         lo, hi = int(offsets[e]), int(offsets[e + 1])
         xt[:, pad[e]:pad[e] + (hi - lo)] = x[lo:hi].T
-    q, s = quant_1x128(xt) if Rp else (np.zeros((C, 0), np.uint8), np.zeros((C, 0), np.float32))
+    q, s = quant_1x128(xt, pow2) if Rp else (np.zeros((C, 0), np.uint8), np.zeros((C, 0), np.float32))
     return q, s, pad
 
 
@@ -565,12 +580,13 @@ def combine_bwd(dout_bf16, y_bf16, inv_map, w, K: int):
     return dy, dw
 
 
-def moe_backward(fwd: dict, x_bf16, w1q, w1s, w2q, w2s, dout_bf16, K: int):
+def moe_backward(fwd: dict, x_bf16, w1q, w1s, w2q, w2s, dout_bf16, K: int, pow2: bool = False):
     """Backward of moe_forward given its intermediates and dout [T,H] bf16.
     Stages: combine bwd -> dy quant (1x128) -> fc2 dgrad (W2^T) -> fc2 wgrad
     (128x1 dy, h) -> SwiGLU bwd -> dc1 quant -> fc1 dgrad (W1^T) -> fc1 wgrad
     (128x1 dc1, x) -> un-permute (sum of the K replicas).  GEMM outputs are
-    rounded to bf16 between stages like the kernels; wgrads stay float64."""
+    rounded to bf16 between stages like the kernels; wgrads stay float64.
+    ``pow2``: the wgrad operands' 128x1 scales follow C10 instead of C3."""
     E = w1q.shape[0]
     off = fwd["offsets"]
     inv = fwd["inv_map"]
@@ -584,16 +600,16 @@ def moe_backward(fwd: dict, x_bf16, w1q, w1s, w2q, w2s, dout_bf16, K: int):
     dh = f32_to_bf16(grouped_gemm_fp8(dyq, dys, w2tq, w2ts, off).astype(np.float32))
     # h as the forward saves it: silu(g)*u in fp32, rounded to bf16
     hh = bf16_to_f32(f32_to_bf16((silu_f32(h[:, :I]) * h[:, I:]).astype(np.float32)))
-    dyTq, dyTs, pad = quant_cols_128x1(bf16_to_f32(dy), off)
-    hTq, hTs, _ = quant_cols_128x1(hh, off)
+    dyTq, dyTs, pad = quant_cols_128x1(bf16_to_f32(dy), off, pow2)
+    hTq, hTs, _ = quant_cols_128x1(hh, off, pow2)
     dW2 = grouped_gemm_fp8_wgrad(dyTq, dyTs, hTq, hTs, pad, E)
     dc1 = swiglu_bwd(fwd["c1"], dh)
     dc1q, dc1s = quant_1x128(bf16_to_f32(dc1))
     w1tq, w1ts = transpose_blockwise(w1q, w1s, k=H)
     dxs = f32_to_bf16(grouped_gemm_fp8(dc1q, dc1s, w1tq, w1ts, off).astype(np.float32))
     xs_sorted = bf16_to_f32(x_bf16)[fwd["row_map"] // K]
-    dcTq, dcTs, _ = quant_cols_128x1(bf16_to_f32(dc1), off)
-    xTq, xTs, _ = quant_cols_128x1(xs_sorted, off)
+    dcTq, dcTs, _ = quant_cols_128x1(bf16_to_f32(dc1), off, pow2)
+    xTq, xTs, _ = quant_cols_128x1(xs_sorted, off, pow2)
     dW1 = grouped_gemm_fp8_wgrad(dcTq, dcTs, xTq, xTs, pad, E)
     dx = unpermute_combine(dxs, inv, np.ones((T, K), np.float32), K)
     return dict(dy=dy, dw=dw, dh=dh, dW2=dW2, dc1=dc1, dxs=dxs, dW1=dW1, dx=dx, pad=pad)

@@ -98,7 +98,10 @@ constexpr int kQcCols = 128;
 // workgroup takes column block b of both halves, so slabs b (dg) and
 // I/128 + b (du) come from one sigmoid evaluation.  dc1 is written only when
 // not null.
-template <bool kRows, bool kSwigluBwd>
+// kPow2: the 128x1 column scales are group_scale_pow2 (the optional E8M0
+// recipe of the wgrad operands) instead of group_scale; the 1x128 row scales
+// (kRows) keep group_scale.
+template <bool kRows, bool kSwigluBwd, bool kPow2>
 __global__ __launch_bounds__(256) void quant_cols_kernel(
     const uint16_t* __restrict__ x, const int32_t* __restrict__ gather, int gather_div,
     const float* __restrict__ gather_w, int R, int C, const int32_t* __restrict__ offsets, const int32_t* __restrict__ pad, int E, int ld,
@@ -188,7 +191,8 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(
     // quotient set-up (two IEEE divisions) and shares them: the 16 threads
     // that hold pieces of a column would otherwise repeat the divisions
     if (t < kQcCols) {
-      const float sc = group_scale(fmaxf(fmaxf(wmax[0][t], wmax[1][t]), fmaxf(wmax[2][t], wmax[3][t])));
+      const float am = fmaxf(fmaxf(wmax[0][t], wmax[1][t]), fmaxf(wmax[2][t], wmax[3][t]));
+      const float sc = kPow2 ? group_scale_pow2(am) : group_scale(am);
       const QDiv qd = qdiv_setup(sc);
       col_m[t] = qd.m;
       col_r[t] = qd.r;
@@ -513,8 +517,10 @@ extern "C" int smoe_quant_cols_ld(int R, int E) {
 
 extern "C" int smoe_quant_cols_128x1(const uint16_t* x, const int32_t* gather, int gather_div,
                                      int R, int C, const int32_t* offsets, int E, int ld,
-                                     uint8_t* xTq, float* xTs, int32_t* pad, void* stream) {
+                                     uint8_t* xTq, float* xTs, int32_t* pad, int col_scale,
+                                     void* stream) {
   if (R <= 0 || C <= 0) return SMOE_EINVAL_DIM;
+  if (col_scale != SMOE_COLSCALE_FP32 && col_scale != SMOE_COLSCALE_POW2) return SMOE_EINVAL_MODE;
   if (gather && gather_div <= 0) return SMOE_EINVAL_DIM;
   if (gather && ((uintptr_t)gather & 3u)) return SMOE_EINVAL_PTRALIGN;
   if (E <= 0 || E > SMOE_MAX_EXPERTS) return SMOE_EINVAL_EXPERTS;
@@ -528,16 +534,21 @@ extern "C" int smoe_quant_cols_128x1(const uint16_t* x, const int32_t* gather, i
   hipStream_t s = (hipStream_t)stream;
   pad_offsets_kernel<<<1, 1024, 0, s>>>(offsets, E, pad);
   // column slabs vary fastest, so the workgroups in flight read whole rows
-  quant_cols_kernel<false, false><<<dim3((C + kQcCols - 1) / kQcCols, ld / kGroup), dim3(256), 0, s>>>(
-      x, gather, gather ? gather_div : 1, nullptr, R, C, offsets, pad, E, ld, xTq, xTs, nullptr, nullptr,
-      nullptr, nullptr, nullptr);
+#define SMOE_QC(P2)                                                                            \
+  quant_cols_kernel<false, false, P2><<<dim3((C + kQcCols - 1) / kQcCols, ld / kGroup), dim3(256), 0, s>>>( \
+      x, gather, gather ? gather_div : 1, nullptr, R, C, offsets, pad, E, ld, xTq, xTs, nullptr, nullptr, \
+      nullptr, nullptr, nullptr)
+  if (col_scale == SMOE_COLSCALE_POW2) SMOE_QC(true);
+  else SMOE_QC(false);
+#undef SMOE_QC
   SMOE_RETURN_LAUNCH();
 }
 
 extern "C" int smoe_quant_rows_cols(const uint16_t* x, int R, int C, const int32_t* offsets, int E,
                                     int ld, uint8_t* xq, float* xs, uint8_t* xTq, float* xTs,
-                                    int32_t* pad, void* stream) {
+                                    int32_t* pad, int col_scale, void* stream) {
   if (R <= 0 || C <= 0) return SMOE_EINVAL_DIM;
+  if (col_scale != SMOE_COLSCALE_FP32 && col_scale != SMOE_COLSCALE_POW2) return SMOE_EINVAL_MODE;
   if (E <= 0 || E > SMOE_MAX_EXPERTS) return SMOE_EINVAL_EXPERTS;
   if (C % kLane) return SMOE_EINVAL_ALIGN128;
   if (ld < smoe_quant_cols_ld(R, E) || ld % kGroup) return SMOE_EINVAL_DIM;
@@ -551,16 +562,21 @@ extern "C" int smoe_quant_rows_cols(const uint16_t* x, int R, int C, const int32
   if ((uintptr_t)xq & 7u) return SMOE_EINVAL_PTRALIGN;
   hipStream_t s = (hipStream_t)stream;
   pad_offsets_kernel<<<1, 1024, 0, s>>>(offsets, E, pad);
-  quant_cols_kernel<true, false><<<dim3((C + kQcCols - 1) / kQcCols, ld / kGroup), dim3(256), 0, s>>>(
-      x, nullptr, 1, nullptr, R, C, offsets, pad, E, ld, xTq, xTs, xq, xs, nullptr, nullptr, nullptr);
+#define SMOE_QRC(P2)                                                                           \
+  quant_cols_kernel<true, false, P2><<<dim3((C + kQcCols - 1) / kQcCols, ld / kGroup), dim3(256), 0, s>>>( \
+      x, nullptr, 1, nullptr, R, C, offsets, pad, E, ld, xTq, xTs, xq, xs, nullptr, nullptr, nullptr)
+  if (col_scale == SMOE_COLSCALE_POW2) SMOE_QRC(true);
+  else SMOE_QRC(false);
+#undef SMOE_QRC
   SMOE_RETURN_LAUNCH();
 }
 
 extern "C" int smoe_swiglu_bwd_quant(const uint16_t* c1, const uint16_t* dh, int R, int I,
                                      const int32_t* offsets, int E, int ld, uint8_t* dcq,
                                      float* dcs, uint8_t* dcTq, float* dcTs, int32_t* pad,
-                                     uint16_t* dc1, void* stream) {
+                                     uint16_t* dc1, int col_scale, void* stream) {
   if (R <= 0 || I <= 0) return SMOE_EINVAL_DIM;
+  if (col_scale != SMOE_COLSCALE_FP32 && col_scale != SMOE_COLSCALE_POW2) return SMOE_EINVAL_MODE;
   if (E <= 0 || E > SMOE_MAX_EXPERTS) return SMOE_EINVAL_EXPERTS;
   if (I % kGroup) return SMOE_EINVAL_ALIGN128;
   if (ld < smoe_quant_cols_ld(R, E) || ld % kGroup) return SMOE_EINVAL_DIM;
@@ -577,8 +593,12 @@ extern "C" int smoe_swiglu_bwd_quant(const uint16_t* c1, const uint16_t* dh, int
   hipStream_t s = (hipStream_t)stream;
   pad_offsets_kernel<<<1, 1024, 0, s>>>(offsets, E, pad);
   // one workgroup per 128-column block of both halves (dg and du)
-  quant_cols_kernel<true, true><<<dim3(I / kQcCols, ld / kGroup), dim3(256), 0, s>>>(
-      nullptr, nullptr, 1, nullptr, R, C, offsets, pad, E, ld, dcTq, dcTs, dcq, dcs, c1, dh, dc1);
+#define SMOE_SBQ(P2)                                                               \
+  quant_cols_kernel<true, true, P2><<<dim3(I / kQcCols, ld / kGroup), dim3(256), 0, s>>>( \
+      nullptr, nullptr, 1, nullptr, R, C, offsets, pad, E, ld, dcTq, dcTs, dcq, dcs, c1, dh, dc1)
+  if (col_scale == SMOE_COLSCALE_POW2) SMOE_SBQ(true);
+  else SMOE_SBQ(false);
+#undef SMOE_SBQ
   SMOE_RETURN_LAUNCH();
 }
 
@@ -623,8 +643,9 @@ extern "C" int smoe_unpermute_combine_bwd_quant(const uint16_t* dout, const uint
                                                 const int32_t* offsets, int E, int ld,
                                                 uint8_t* dyq, float* dys, uint8_t* dyTq,
                                                 float* dyTs, int32_t* pad, float* dw,
-                                                void* stream) {
+                                                int col_scale, void* stream) {
   if (T <= 0 || H <= 0) return SMOE_EINVAL_DIM;
+  if (col_scale != SMOE_COLSCALE_FP32 && col_scale != SMOE_COLSCALE_POW2) return SMOE_EINVAL_MODE;
   if (H % kLane) return SMOE_EINVAL_ALIGN128;
   if (K <= 0 || K > 32) return SMOE_EINVAL_TOPK;
   if ((long long)T * K > 0x7fffffffLL) return SMOE_EINVAL_DIM;
@@ -654,8 +675,12 @@ extern "C" int smoe_unpermute_combine_bwd_quant(const uint16_t* dout, const uint
   pad_offsets_kernel<<<1, 1024, 0, s>>>(offsets, E, pad);
   // 128x1 columns: row r of dy is rebuilt as bf16(w[p] * dout[p / K]) with
   // p = row_map[r]
-  quant_cols_kernel<false, false><<<dim3((H + kQcCols - 1) / kQcCols, ld / kGroup), dim3(256), 0, s>>>(
-      dout, row_map, K, w, R, H, offsets, pad, E, ld, dyTq, dyTs, nullptr, nullptr, nullptr,
-      nullptr, nullptr);
+#define SMOE_CQ(P2)                                                                    \
+  quant_cols_kernel<false, false, P2><<<dim3((H + kQcCols - 1) / kQcCols, ld / kGroup), dim3(256), 0, \
+                                        s>>>(dout, row_map, K, w, R, H, offsets, pad, E, ld, dyTq,   \
+                                             dyTs, nullptr, nullptr, nullptr, nullptr, nullptr)
+  if (col_scale == SMOE_COLSCALE_POW2) SMOE_CQ(true);
+  else SMOE_CQ(false);
+#undef SMOE_CQ
   SMOE_RETURN_LAUNCH();
 }

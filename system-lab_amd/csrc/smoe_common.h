@@ -89,6 +89,20 @@ __device__ __forceinline__ float group_scale(float amax) {
   return amax == 0.0f ? 1.0f : amax / kE4M3Max;
 }
 
+// The power-of-two scale of the optional E8M0 column recipe: the least power
+// of two >= RN(amax / 448), at least 2^-127 (the smallest E8M0 value); 1 when
+// amax == 0.  Dividing by it is exact, so x / s needs no rounding before the
+// e4m3 encoding, and its fp32 exponent field is the E8M0 byte the scaled
+// MFMA takes.
+__device__ __forceinline__ float group_scale_pow2(float amax) {
+  if (amax == 0.0f) return 1.0f;
+  const float t = amax / kE4M3Max;
+  int e;
+  const float m = __builtin_frexpf(t, &e);  // t = m * 2^e, m in [0.5, 1)
+  const float s = m == 0.5f ? t : __builtin_ldexpf(1.0f, e);
+  return fmaxf(s, 0x1p-127f);
+}
+
 // Division-free quotient for bf16 inputs.  With s = m * 2^e (m in [0.5, 1))
 // and r = RN(1/m) computed once per group, each element takes
 //   xs = x * 2^-e (exact), q0 = RN(xs * r), d = fma(-q0, m, xs),

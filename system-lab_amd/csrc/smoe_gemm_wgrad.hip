@@ -47,8 +47,9 @@ enum WgradOut {
   kOutBF16Acc = SMOE_WGRAD_BF16_ACC
 };
 
-// One 256 x 256 tile of expert e's weight gradient at (n0, k0).
-template <int kOut>
+// One 256 x 256 tile of expert e's weight gradient at (n0, k0).  kE8M0: the
+// operands carry power-of-two scales (the optional E8M0 column recipe).
+template <int kOut, bool kE8M0>
 __device__ __forceinline__ void wgrad_tile(const uint8_t* __restrict__ aT,
                                            const float* __restrict__ aTs,
                                            const uint8_t* __restrict__ bT,
@@ -136,41 +137,74 @@ __device__ __forceinline__ void wgrad_tile(const uint8_t* __restrict__ aT,
     const float* sSa = (const float*)(smem + 2 * kWStage + ((st / kWChunk) & 1) * kWSC) +
                        (st & (kWChunk - 1));
     const float* sSb = sSa + kWN * kWChunk;
-    v8i fa[4];
-    v4f sa[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      fa[j] = lds_frag(sA, wn * 64 + j * 16 + frow, fch);
-      const int r = wn * 64 + j * 16 + (lane >> 4) * 4;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) sa[j][v] = sSa[(r + v) * kWChunk];
-    }
-    // the next row block's fragment and scale are read before this block's
-    // MFMAs are issued, so their LDS latency hides behind them
     const int kr0 = wk * 128 + frow;
-    v8i fb = lds_frag(sB, kr0, fch);
-    float sb = sSb[kr0 * kWChunk];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      v8i fbn = fb;
-      float sbn = sb;
-      if (i + 1 < 8) {
-        fbn = lds_frag(sB, kr0 + (i + 1) * 16, fch);
-        sbn = sSb[(kr0 + (i + 1) * 16) * kWChunk];
-      }
-      // the scale products do not depend on the MFMA results: computing them
-      // first leaves one FMA per output after each MFMA
-      v4f sab[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) sab[j] = sa[j] * sb;
+    if constexpr (kE8M0) {
+      // Power-of-two scales (group_scale_pow2): the fp32 exponent field of
+      // each scale is its E8M0 byte, and the scaled MFMA applies a row's
+      // aT scale and a column's bT scale in hardware, so the 128-row groups
+      // accumulate in the MFMA's own fp32 accumulator with no per-output
+      // arithmetic.  The MFMA's A rows (and their scales) are indexed by
+      // lane % 16, as are its B rows.
+      v8i fa[4];
+      int ea[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const v4f p = mfma16(fa[j], fb, v4f{0.0f, 0.0f, 0.0f, 0.0f});
-#pragma unroll
-        for (int v = 0; v < 4; ++v) acc[i][j][v] = __builtin_fmaf(p[v], sab[j][v], acc[i][j][v]);
+        fa[j] = lds_frag(sA, wn * 64 + j * 16 + frow, fch);
+        ea[j] = (int)((__float_as_uint(sSa[(wn * 64 + j * 16 + frow) * kWChunk]) >> 23) & 0xffu);
       }
-      fb = fbn;
-      sb = sbn;
+      v8i fb = lds_frag(sB, kr0, fch);
+      int eb = (int)((__float_as_uint(sSb[kr0 * kWChunk]) >> 23) & 0xffu);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        v8i fbn = fb;
+        int ebn = eb;
+        if (i + 1 < 8) {
+          fbn = lds_frag(sB, kr0 + (i + 1) * 16, fch);
+          ebn = (int)((__float_as_uint(sSb[(kr0 + (i + 1) * 16) * kWChunk]) >> 23) & 0xffu);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(fa[j], fb, acc[i][j], 0, 0,
+                                                                       0, ea[j], 0, eb);
+        fb = fbn;
+        eb = ebn;
+      }
+    } else {
+      v8i fa[4];
+      v4f sa[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        fa[j] = lds_frag(sA, wn * 64 + j * 16 + frow, fch);
+        const int r = wn * 64 + j * 16 + (lane >> 4) * 4;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) sa[j][v] = sSa[(r + v) * kWChunk];
+      }
+      // the next row block's fragment and scale are read before this block's
+      // MFMAs are issued, so their LDS latency hides behind them
+      v8i fb = lds_frag(sB, kr0, fch);
+      float sb = sSb[kr0 * kWChunk];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        v8i fbn = fb;
+        float sbn = sb;
+        if (i + 1 < 8) {
+          fbn = lds_frag(sB, kr0 + (i + 1) * 16, fch);
+          sbn = sSb[(kr0 + (i + 1) * 16) * kWChunk];
+        }
+        // the scale products do not depend on the MFMA results: computing
+        // them first leaves one FMA per output after each MFMA
+        v4f sab[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sab[j] = sa[j] * sb;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const v4f p = mfma16(fa[j], fb, v4f{0.0f, 0.0f, 0.0f, 0.0f});
+#pragma unroll
+          for (int v = 0; v < 4; ++v) acc[i][j][v] = __builtin_fmaf(p[v], sab[j][v], acc[i][j][v]);
+        }
+        fb = fbn;
+        sb = sbn;
+      }
     }
     __builtin_amdgcn_s_waitcnt(0);
     __builtin_amdgcn_s_barrier();
@@ -245,7 +279,7 @@ __device__ __forceinline__ void wgrad_tile(const uint8_t* __restrict__ aT,
 // fp32 output and the prologue), so that empty experts' tiles count too.
 constexpr int kTileFixed = 4;
 
-template <int kOut>
+template <int kOut, bool kE8M0>
 __global__ __launch_bounds__(kWThreads, 1) void grouped_gemm_fp8_wgrad_kernel(
     const uint8_t* __restrict__ aT, const float* __restrict__ aTs, const uint8_t* __restrict__ bT,
     const float* __restrict__ bTs, const int32_t* __restrict__ pad, int E, int N, int Kd, int ld,
@@ -325,7 +359,7 @@ __global__ __launch_bounds__(kWThreads, 1) void grouped_gemm_fp8_wgrad_kernel(
   for (int t = t_begin + j; t < t_end; t += per_xcd) {
     const int e = t / TE;
     const int rem = t - e * TE;
-    wgrad_tile<kOut>(aT, aTs, bT, bTs, pad, N, Kd, ld, e, (rem / KT) * kWN, (rem % KT) * kWK, smem,
+    wgrad_tile<kOut, kE8M0>(aT, aTs, bT, bTs, pad, N, Kd, ld, e, (rem / KT) * kWN, (rem % KT) * kWK, smem,
                      dW);
     __syncthreads();  // the next tile reuses the LDS
   }
@@ -345,6 +379,8 @@ extern "C" int smoe_grouped_gemm_fp8_wgrad_ex(const uint8_t* aT, const float* aT
   // blocks: tiles past them are clamped on load and masked on store
   if (N % 16 || Kdim % 16 || ld % kGroup) return SMOE_EINVAL_ALIGN128;
   if ((long long)kWN * ld >= (1LL << 31)) return SMOE_EINVAL_DIM;
+  const bool e8m0 = (mode & SMOE_WGRAD_E8M0) != 0;
+  mode &= ~SMOE_WGRAD_E8M0;
   if (mode < kOutF32 || mode > kOutBF16Acc) return SMOE_EINVAL_MODE;
   SMOE_CHECK_PTR(aT);
   SMOE_CHECK_PTR(bT);
@@ -358,15 +394,18 @@ extern "C" int smoe_grouped_gemm_fp8_wgrad_ex(const uint8_t* aT, const float* aT
   if (per_xcd * 8 > 0x7fffffffLL) return SMOE_EINVAL_DIM;
   const dim3 grid((unsigned)(per_xcd * 8)), block(kWThreads);
   hipStream_t s = (hipStream_t)stream;
-#define SMOE_WG(M)                                                                     \
-  grouped_gemm_fp8_wgrad_kernel<M><<<grid, block, 0, s>>>(aT, aTs, bT, bTs, pad, E, N, Kdim, ld, \
-                                                          (int)per_xcd, dW)
+#define SMOE_WG(M, P2)                                                                   \
+  grouped_gemm_fp8_wgrad_kernel<M, P2><<<grid, block, 0, s>>>(aT, aTs, bT, bTs, pad, E, N, Kdim, \
+                                                              ld, (int)per_xcd, dW)
+#define SMOE_WG2(M) \
+  if (e8m0) SMOE_WG(M, true); else SMOE_WG(M, false)
   switch (mode) {
-    case kOutF32: SMOE_WG(kOutF32); break;
-    case kOutF32Acc: SMOE_WG(kOutF32Acc); break;
-    case kOutBF16: SMOE_WG(kOutBF16); break;
-    default: SMOE_WG(kOutBF16Acc); break;
+    case kOutF32: SMOE_WG2(kOutF32); break;
+    case kOutF32Acc: SMOE_WG2(kOutF32Acc); break;
+    case kOutBF16: SMOE_WG2(kOutBF16); break;
+    default: SMOE_WG2(kOutBF16Acc); break;
   }
+#undef SMOE_WG2
 #undef SMOE_WG
   SMOE_RETURN_LAUNCH();
 }

@@ -49,16 +49,18 @@ SIGNATURES = {
     "smoe_quant_rows_1x128": (c_int, [P, c_int, c_int, P, P, P]),
     "smoe_transpose_blockwise_fp8": (c_int, [P, P, c_int, c_int, c_int, P, P, P]),
     "smoe_quant_cols_ld": (c_int, [c_int, c_int]),
-    "smoe_quant_cols_128x1": (c_int, [P, P, c_int, c_int, c_int, P, c_int, c_int, P, P, P, P]),
-    "smoe_quant_rows_cols": (c_int, [P, c_int, c_int, P, c_int, c_int, P, P, P, P, P, P]),
-    "smoe_swiglu_bwd_quant": (c_int, [P, P, c_int, c_int, P, c_int, c_int, P, P, P, P, P, P, P]),
+    "smoe_quant_cols_128x1": (c_int, [P, P, c_int, c_int, c_int, P, c_int, c_int, P, P, P, c_int,
+                                      P]),
+    "smoe_quant_rows_cols": (c_int, [P, c_int, c_int, P, c_int, c_int, P, P, P, P, P, c_int, P]),
+    "smoe_swiglu_bwd_quant": (c_int, [P, P, c_int, c_int, P, c_int, c_int, P, P, P, P, P, P, c_int,
+                                      P]),
     "smoe_grouped_gemm_fp8_wgrad": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int, P, P]),
     "smoe_grouped_gemm_fp8_wgrad_ex": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int, P,
                                                c_int, P]),
     "smoe_swiglu_bwd": (c_int, [P, P, c_int, c_int, P, P]),
     "smoe_unpermute_combine_bwd": (c_int, [P, P, P, P, c_int, c_int, c_int, P, P, P]),
     "smoe_unpermute_combine_bwd_quant": (c_int, [P, P, P, P, P, c_int, c_int, c_int, P, c_int,
-                                                 c_int, P, P, P, P, P, P, P]),
+                                                 c_int, P, P, P, P, P, P, c_int, P]),
 }
 
 

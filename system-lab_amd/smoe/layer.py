@@ -98,6 +98,13 @@ class SimpleMoE(nn.Module):
     once a backward ran (packed where covered, else plain; never both), plus
     the fp32 scales.
 
+    ``wgrad_recipe`` chooses the 128x1 quantisation of the weight-gradient
+    operands: "fp32" (the default) uses the activation rule s = amax/448;
+    "e8m0" uses power-of-two scales (the least power of two >= amax/448, the
+    scale format of the MXFP8 recipe) so that gfx950's scaled MFMA applies
+    them in hardware and the wgrad does no per-output scale arithmetic.  The
+    forward and the dgrad are the same in both.
+
     Under autograd (grad mode on and an input or parameter requiring grad),
     ``forward`` records one graph node whose backward runs the fp8 backward
     (``loss.backward()`` fills w1.grad, w2.grad, w_gate.grad and x.grad).
@@ -106,8 +113,13 @@ class SimpleMoE(nn.Module):
     """
 
     def __init__(self, hidden: int, intermediate: int, num_experts: int, top_k: int,
-                 device=None, dtype=torch.bfloat16, router_bias: bool = False):
+                 device=None, dtype=torch.bfloat16, router_bias: bool = False,
+                 wgrad_recipe: str = "fp32"):
         super().__init__()
+        if wgrad_recipe not in ("fp32", "e8m0"):
+            raise ValueError("wgrad_recipe is 'fp32' (128x1 scales amax/448) or 'e8m0' "
+                             "(power-of-two 128x1 scales applied by the scaled MFMA)")
+        self.wgrad_recipe = wgrad_recipe
         self.hidden, self.intermediate = hidden, intermediate
         self.num_experts, self.top_k = num_experts, top_k
         kw = dict(device=device, dtype=dtype)
@@ -329,6 +341,8 @@ class SimpleMoE(nn.Module):
         # the main stream waits for the side stream before returning.
         main = torch.cuda.current_stream()
         side = self._side_stream(main.device)
+        cs = "pow2" if self.wgrad_recipe == "e8m0" else "fp32"
+        e8m0 = self.wgrad_recipe == "e8m0"
         ones = torch.ones_like(inter["topk_w"])
         # the returned weight gradients are allocated on the caller's stream,
         # so the caching allocator never hands their memory to side-stream
@@ -341,24 +355,25 @@ class SimpleMoE(nn.Module):
         with torch.cuda.stream(side):
             # the wgrad activation operands depend on the forward only: h, and
             # the sorted tokens x[row_map // K] gathered inside the quantiser
-            hTq, hTs, _, _ = ops.quant_cols(inter["h"], off)
-            xTq, xTs, _, _ = ops.quant_cols(inter["x"], off, gather=inter["row_map"], gather_div=K)
+            hTq, hTs, _, _ = ops.quant_cols(inter["h"], off, col_scale=cs)
+            xTq, xTs, _, _ = ops.quant_cols(inter["x"], off, gather=inter["row_map"], gather_div=K,
+                                            col_scale=cs)
         # combine backward fused with both quantisations of dy (1x128 rows for
         # dgrad, 128x1 columns for wgrad); dy itself is never stored
         dyq, dys, dyTq, dyTs, pad, ld, dw = ops.unpermute_combine_bwd_quant(
-            dout.contiguous(), inter["y"], inv, inter["row_map"], inter["topk_w"], off)
+            dout.contiguous(), inter["y"], inv, inter["row_map"], inter["topk_w"], off, col_scale=cs)
         side.wait_stream(main)
         with torch.cuda.stream(side):
             ops.grouped_gemm_fp8_wgrad(dyTq, dyTs, hTq, hTs, pad, ld, out=dw2,
-                                       accumulate=dw2_into is not None)
+                                       accumulate=dw2_into is not None, e8m0=e8m0)
         dh = ops.grouped_gemm_fp8(dyq, dys, w2tq, w2ts, off)
         # SwiGLU backward fused with both quantisations of dc1 (dc1 itself is
         # never stored)
-        dcq, dcs, dcTq, dcTs, _, _ = ops.swiglu_bwd_quant(inter["c1"], dh, off)
+        dcq, dcs, dcTq, dcTs, _, _ = ops.swiglu_bwd_quant(inter["c1"], dh, off, col_scale=cs)
         side.wait_stream(main)
         with torch.cuda.stream(side):
             ops.grouped_gemm_fp8_wgrad(dcTq, dcTs, xTq, xTs, pad, ld, out=dw1,
-                                       accumulate=dw1_into is not None)
+                                       accumulate=dw1_into is not None, e8m0=e8m0)
         dxs = ops.grouped_gemm_fp8(dcq, dcs, w1tq, w1ts, off)
         dx = ops.unpermute_combine(dxs, inv, ones)
         # router: renormalisation + softmax backward into the logits

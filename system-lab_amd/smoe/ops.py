@@ -19,6 +19,8 @@ from . import _C
 
 FP8 = torch.float8_e4m3fn
 GROUP = 128
+# column-scale rules of the 128x1 (wgrad operand) quantisers, SMOE_COLSCALE_*
+COL_SCALES = {"fp32": 0, "pow2": 1}
 
 
 def pad128(d: int) -> int:
@@ -486,12 +488,21 @@ def transpose_blockwise(wq: torch.Tensor, ws: torch.Tensor, k: int | None = None
     return wqT, wsT
 
 
+def _col_scale(col_scale: str) -> int:
+    if col_scale not in COL_SCALES:
+        raise ValueError(f"col_scale must be one of {sorted(COL_SCALES)}, got {col_scale!r}")
+    return COL_SCALES[col_scale]
+
+
 def quant_cols(x: torch.Tensor, offsets: torch.Tensor, gather: torch.Tensor | None = None,
-               gather_div: int = 1):
+               gather_div: int = 1, col_scale: str = "fp32"):
     """Transposed 128x1 quantisation over the expert row segments ``offsets``
     (E+1) of x [R,C] bf16, or, with ``gather`` [R] i32, of the rows
     x[gather[r] // gather_div].  -> (xTq [C, ld] fp8, xTs [C, ld/128] f32,
-    pad [E+1] i32, ld) where pad are the 128-aligned segment starts."""
+    pad [E+1] i32, ld) where pad are the 128-aligned segment starts.
+    ``col_scale`` "fp32" is the s = amax/448 rule; "pow2" the least power of
+    two >= amax/448 (the E8M0 recipe the wgrad's ``e8m0`` mode applies in
+    hardware)."""
     _check(x, "x", (torch.bfloat16,), 2)
     _check(offsets, "offsets", (torch.int32,), 1)
     C = x.shape[1]
@@ -512,11 +523,11 @@ def quant_cols(x: torch.Tensor, offsets: torch.Tensor, gather: torch.Tensor | No
     xTs = torch.empty((C, ld // GROUP), dtype=torch.float32, device=x.device)
     pad = torch.empty(E + 1, dtype=torch.int32, device=x.device)
     _C.call("smoe_quant_cols_128x1", _ptr(x), _ptr(gather), gather_div, R, C, _ptr(offsets), E,
-            ld, _ptr(xTq), _ptr(xTs), _ptr(pad), _stream())
+            ld, _ptr(xTq), _ptr(xTs), _ptr(pad), _col_scale(col_scale), _stream())
     return xTq, xTs, pad, ld
 
 
-def quant_rows_cols(x: torch.Tensor, offsets: torch.Tensor):
+def quant_rows_cols(x: torch.Tensor, offsets: torch.Tensor, col_scale: str = "fp32"):
     """Both quantisations of x [R,C] bf16 from one read: the 1x128 rows of
     ``quant_rows`` and the transposed 128x1 columns of ``quant_cols`` over
     the expert segments ``offsets`` (which must cover all R rows).
@@ -533,12 +544,12 @@ def quant_rows_cols(x: torch.Tensor, offsets: torch.Tensor):
     xTs = torch.empty((C, ld // GROUP), dtype=torch.float32, device=x.device)
     pad = torch.empty(E + 1, dtype=torch.int32, device=x.device)
     _C.call("smoe_quant_rows_cols", _ptr(x), R, C, _ptr(offsets), E, ld, _ptr(xq), _ptr(xs),
-            _ptr(xTq), _ptr(xTs), _ptr(pad), _stream())
+            _ptr(xTq), _ptr(xTs), _ptr(pad), _col_scale(col_scale), _stream())
     return xq, xs, xTq, xTs, pad, ld
 
 
 def swiglu_bwd_quant(c1: torch.Tensor, dh: torch.Tensor, offsets: torch.Tensor,
-                     save_dc1: bool = False):
+                     save_dc1: bool = False, col_scale: str = "fp32"):
     """SwiGLU backward fused with both quantisations of its output: the
     bytes of ``quant_rows_cols(swiglu_bwd(c1, dh), offsets)`` without
     storing dc1 (returned as the last element when ``save_dc1``).
@@ -559,7 +570,7 @@ def swiglu_bwd_quant(c1: torch.Tensor, dh: torch.Tensor, offsets: torch.Tensor,
         # a multiple of 128, which the fused kernel's column slabs assume: the
         # same bytes from the SwiGLU backward kernel and the one-read quantiser
         dc1 = swiglu_bwd(c1, dh)
-        out = quant_rows_cols(dc1, offsets)
+        out = quant_rows_cols(dc1, offsets, col_scale=col_scale)
         return out + (dc1,) if save_dc1 else out
     dcq = torch.empty((R, N), dtype=FP8, device=dev)
     dcs = torch.empty((R, N // GROUP), dtype=torch.float32, device=dev)
@@ -568,23 +579,28 @@ def swiglu_bwd_quant(c1: torch.Tensor, dh: torch.Tensor, offsets: torch.Tensor,
     pad = torch.empty(E + 1, dtype=torch.int32, device=dev)
     dc1 = torch.empty((R, N), dtype=torch.bfloat16, device=dev) if save_dc1 else None
     _C.call("smoe_swiglu_bwd_quant", _ptr(c1), _ptr(dh), R, I, _ptr(offsets), E, ld, _ptr(dcq),
-            _ptr(dcs), _ptr(dcTq), _ptr(dcTs), _ptr(pad), _ptr(dc1), _stream())
+            _ptr(dcs), _ptr(dcTq), _ptr(dcTs), _ptr(pad), _ptr(dc1), _col_scale(col_scale), _stream())
     out = (dcq, dcs, dcTq, dcTs, pad, ld)
     return out + (dc1,) if save_dc1 else out
 
 
 WGRAD_MODES = {(torch.float32, False): 0, (torch.float32, True): 1,
                (torch.bfloat16, False): 2, (torch.bfloat16, True): 3}
+WGRAD_E8M0 = 4  # SMOE_WGRAD_E8M0
 
 
 def grouped_gemm_fp8_wgrad(aTq, aTs, bTq, bTs, pad, ld: int, out: torch.Tensor | None = None,
-                           accumulate: bool = False, dtype=torch.float32) -> torch.Tensor:
+                           accumulate: bool = False, dtype=torch.float32,
+                           e8m0: bool = False) -> torch.Tensor:
     """dW[e] = A_e^T B_e over each expert's rows from quant_cols operands:
     aT [N, ld], bT [K, ld] -> [E, N, K] (into ``out`` when given, else a new
     tensor of ``dtype``, fp32 or bf16).  With ``accumulate`` the gradient is
     added into ``out`` (fp32: one fp32 addition per value; bf16: the fp32 sum
     rounded once), as a gradient-accumulation buffer (``main_grad``) needs;
-    experts without rows leave ``out`` untouched."""
+    experts without rows leave ``out`` untouched.  ``e8m0``: the operands
+    come from the ``col_scale="pow2"`` quantisers, whose power-of-two scales
+    the scaled MFMA applies in hardware (scales that are not powers of two
+    would be read by their exponent only)."""
     _check(aTq, "aTq", (FP8, torch.uint8), 2)
     _check(bTq, "bTq", (FP8, torch.uint8), 2)
     _check(aTs, "aTs", (torch.float32,), 2)
@@ -607,8 +623,8 @@ def grouped_gemm_fp8_wgrad(aTq, aTs, bTq, bTs, pad, ld: int, out: torch.Tensor |
             raise ValueError(f"out must be [{E}, {N}, {K}]")
         dW = out
     _C.call("smoe_grouped_gemm_fp8_wgrad_ex", _ptr(_bytes(aTq)), _ptr(aTs), _ptr(_bytes(bTq)),
-            _ptr(bTs), _ptr(pad), E, N, K, ld, _ptr(dW), WGRAD_MODES[(dW.dtype, bool(accumulate))],
-            _stream())
+            _ptr(bTs), _ptr(pad), E, N, K, ld, _ptr(dW),
+            WGRAD_MODES[(dW.dtype, bool(accumulate))] | (WGRAD_E8M0 if e8m0 else 0), _stream())
     return dW
 
 
@@ -644,11 +660,11 @@ def unpermute_combine_bwd(dout: torch.Tensor, y: torch.Tensor, inv_map: torch.Te
 
 def unpermute_combine_bwd_quant(dout: torch.Tensor, y: torch.Tensor, inv_map: torch.Tensor,
                                 row_map: torch.Tensor, topk_w: torch.Tensor,
-                                offsets: torch.Tensor):
+                                offsets: torch.Tensor, col_scale: str = "fp32"):
     """Combine backward fused with both quantisations of dy: the bytes of
-    ``quant_rows_cols(unpermute_combine_bwd(...)[0], offsets)`` and dw,
-    without storing dy.  -> (dyq [T*K,H] fp8, dys, dyTq [H,ld] fp8, dyTs,
-    pad, ld, dw [T,K] f32)."""
+    ``quant_rows_cols(unpermute_combine_bwd(...)[0], offsets, col_scale)`` and
+    dw, without storing dy.  -> (dyq [T*K,pad128(H)] fp8, dys, dyTq [H,ld] fp8,
+    dyTs, pad, ld, dw [T,K] f32)."""
     _check(dout, "dout", (torch.bfloat16,), 2)
     _check(y, "y", (torch.bfloat16,), 2)
     _check(inv_map, "inv_map", (torch.int32,))
@@ -673,5 +689,5 @@ def unpermute_combine_bwd_quant(dout: torch.Tensor, y: torch.Tensor, inv_map: to
     dw = torch.empty((T, K), dtype=torch.float32, device=dev)
     _C.call("smoe_unpermute_combine_bwd_quant", _ptr(dout), _ptr(y), _ptr(inv_map),
             _ptr(row_map), _ptr(topk_w), T, K, H, _ptr(offsets), E, ld, _ptr(dyq), _ptr(dys),
-            _ptr(dyTq), _ptr(dyTs), _ptr(pad), _ptr(dw), _stream())
+            _ptr(dyTq), _ptr(dyTs), _ptr(pad), _ptr(dw), _col_scale(col_scale), _stream())
     return dyq, dys, dyTq, dyTs, pad, ld, dw

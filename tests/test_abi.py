@@ -124,11 +124,11 @@ def test_remaining_entry_points_reject():
     q = lib.smoe_quant_cols_128x1
     ld = lib.smoe_quant_cols_ld(1000, 4)
     assert ld >= 1000 and ld % 128 == 0
-    assert q(FAKE, None, 1, 1000, 100, FAKE, 4, ld, FAKE, FAKE, FAKE, None) == -3
-    assert q(FAKE, None, 1, 1000, 128, FAKE, 0, ld, FAKE, FAKE, FAKE, None) == -4
-    assert q(FAKE, None, 1, 1000, 128, FAKE, 4, ld - 128, FAKE, FAKE, FAKE, None) == -2
-    assert q(FAKE, FAKE, 0, 1000, 128, FAKE, 4, ld, FAKE, FAKE, FAKE, None) == -2
-    assert q(FAKE, None, 1, 1000, 128, None, 4, ld, FAKE, FAKE, FAKE, None) == -1
+    assert q(FAKE, None, 1, 1000, 100, FAKE, 4, ld, FAKE, FAKE, FAKE, 0, None) == -3
+    assert q(FAKE, None, 1, 1000, 128, FAKE, 0, ld, FAKE, FAKE, FAKE, 0, None) == -4
+    assert q(FAKE, None, 1, 1000, 128, FAKE, 4, ld - 128, FAKE, FAKE, FAKE, 0, None) == -2
+    assert q(FAKE, FAKE, 0, 1000, 128, FAKE, 4, ld, FAKE, FAKE, FAKE, 0, None) == -2
+    assert q(FAKE, None, 1, 1000, 128, None, 4, ld, FAKE, FAKE, FAKE, 0, None) == -1
     # wgrad: N % 128, experts, ld <= 0, pad NULL
     w = lib.smoe_grouped_gemm_fp8_wgrad
     assert w(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 100, 256, 1024, FAKE, None) == -3
@@ -150,24 +150,27 @@ def test_remaining_entry_points_reject():
     assert lib.smoe_quant_rows_1x128(FAKE, 0, 128, FAKE, FAKE, None) == -2
     # one-read row + column quantiser: C % 128, experts, ld too small, xs NULL
     rc = lib.smoe_quant_rows_cols
-    assert rc(FAKE, 1000, 100, FAKE, 4, ld, FAKE, FAKE, FAKE, FAKE, FAKE, None) == -3
-    assert rc(FAKE, 1000, 128, FAKE, 0, ld, FAKE, FAKE, FAKE, FAKE, FAKE, None) == -4
-    assert rc(FAKE, 1000, 128, FAKE, 4, ld - 128, FAKE, FAKE, FAKE, FAKE, FAKE, None) == -2
-    assert rc(FAKE, 1000, 128, FAKE, 4, ld, FAKE, None, FAKE, FAKE, FAKE, None) == -1
+    assert rc(FAKE, 1000, 100, FAKE, 4, ld, FAKE, FAKE, FAKE, FAKE, FAKE, 0, None) == -3
+    assert rc(FAKE, 1000, 128, FAKE, 0, ld, FAKE, FAKE, FAKE, FAKE, FAKE, 0, None) == -4
+    assert rc(FAKE, 1000, 128, FAKE, 4, ld - 128, FAKE, FAKE, FAKE, FAKE, FAKE, 0, None) == -2
+    assert rc(FAKE, 1000, 128, FAKE, 4, ld, FAKE, None, FAKE, FAKE, FAKE, 0, None) == -1
     sb = lib.smoe_swiglu_bwd_quant
-    assert sb(FAKE, FAKE, 1000, 100, FAKE, 4, ld, FAKE, FAKE, FAKE, FAKE, FAKE, None, None) == -3
-    assert sb(FAKE, FAKE, 1000, 128, FAKE, 0, ld, FAKE, FAKE, FAKE, FAKE, FAKE, None, None) == -4
-    assert sb(FAKE, FAKE, 1000, 128, FAKE, 4, ld, FAKE, FAKE, FAKE, FAKE, FAKE, MIS, None) == -6
+    assert sb(FAKE, FAKE, 1000, 100, FAKE, 4, ld, FAKE, FAKE, FAKE, FAKE, FAKE, None, 0, None) == -3
+    assert sb(FAKE, FAKE, 1000, 128, FAKE, 0, ld, FAKE, FAKE, FAKE, FAKE, FAKE, None, 0, None) == -4
+    assert sb(FAKE, FAKE, 1000, 128, FAKE, 4, ld, FAKE, FAKE, FAKE, FAKE, FAKE, MIS, 0, None) == -6
     # fused combine backward + quantiser: H % 128, top-k, experts, ld too small, row_map NULL
     cq = lib.smoe_unpermute_combine_bwd_quant
     ld2 = lib.smoe_quant_cols_ld(1000, 4)
     args = lambda T=500, K=2, H=128, E=4, ld=ld2, rm=FAKE: (
-        FAKE, FAKE, FAKE, rm, FAKE, T, K, H, FAKE, E, ld, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None)
+        FAKE, FAKE, FAKE, rm, FAKE, T, K, H, FAKE, E, ld, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 0, None)
     assert cq(*args(H=130)) == -3
     assert cq(*args(K=33)) == -7
     assert cq(*args(E=0)) == -4
     assert cq(*args(ld=ld2 - 128)) == -2
     assert cq(*args(rm=None)) == -1
+    # a column-scale rule other than SMOE_COLSCALE_FP32 / _POW2
+    assert q(FAKE, None, 1, 1000, 128, FAKE, 4, ld, FAKE, FAKE, FAKE, 2, None) == -8
+    assert rc(FAKE, 1000, 128, FAKE, 4, ld, FAKE, FAKE, FAKE, FAKE, FAKE, -1, None) == -8
     # SwiGLU with the bf16 h output: misaligned h; the quantiser self-test
     assert lib.smoe_swiglu_quant_h(FAKE, 10, 128, FAKE, FAKE, MIS, None) == -6
     assert lib.smoe_selftest_quant(None, None) == -1
@@ -177,15 +180,15 @@ def test_remaining_entry_points_reject():
 
 
 def test_wgrad_ex_and_packed_bounds_reject():
-    """The wgrad output-mode entry rejects a mode outside SMOE_WGRAD_* and the
-    plain wgrad's bad shapes; the packed GEMM's K limit (the weight-scale
+    """The wgrad output-mode entry rejects a mode outside SMOE_WGRAD_* (with
+    the optional SMOE_WGRAD_E8M0 bit) and the plain wgrad's bad shapes; the packed GEMM's K limit (the weight-scale
     column of a tile lives in LDS: K <= 65536) is the same in the C check
     and in ops.packed_gemm_ok, so SimpleMoE never packs a weight the packed
     entry point would refuse."""
     from smoe import ops
     lib = _C.lib()
     w = lib.smoe_grouped_gemm_fp8_wgrad_ex
-    assert w(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 256, 256, 1024, FAKE, 4, None) == -8
+    assert w(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 256, 256, 1024, FAKE, 8, None) == -8
     assert w(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 256, 256, 1024, FAKE, -1, None) == -8
     assert w(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 100, 256, 1024, FAKE, 1, None) == -3
     assert w(FAKE, FAKE, FAKE, FAKE, None, 4, 256, 256, 1024, FAKE, 3, None) == -1

@@ -98,7 +98,7 @@ def test_wgrad_output_modes(dev):
     lib = smoe._C.lib()
     st = lib.smoe_grouped_gemm_fp8_wgrad_ex(aTq.data_ptr(), aTs.data_ptr(), bTq.data_ptr(),
                                             bTs.data_ptr(), pad.data_ptr(), E, N, K, ld,
-                                            acc.data_ptr(), 4, None)
+                                            acc.data_ptr(), 8, None)
     assert st == -8  # SMOE_EINVAL_MODE, rejected before any launch
 
 
