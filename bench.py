@@ -228,6 +228,20 @@ def bench_gemm(dev, steps, warmup, skip_cpu=True):
     fl1 = 2.0 * R * (2 * c.I) * c.H
     fl2 = 2.0 * R * c.H * c.I
     tf = (fl1 + fl2) / ((t1 + t2) * 1e-3) / 1e12
+    # the E8M0 recipe: the same shapes with power-of-two scales, on the
+    # kernel that applies them in the MFMA (smoe_grouped_gemm_fp8_packed_e8m0)
+    del w1p, w2p
+    xq, xs = ops.permute_quant_rows(W.tokens(R, c.H, device=dev), inv, 1, scale="pow2")
+    hq, hs = ops.permute_quant_rows(W.tokens(R, c.I, device=dev, seed=17), inv, 1, scale="pow2")
+    w1q, w1s = ops.quantize_weight_blockwise(W.weights(c.E, 2 * c.I, c.H, device=dev), scale="pow2")
+    w2q, w2s = ops.quantize_weight_blockwise(W.weights(c.E, c.H, c.I, device=dev, seed=13),
+                                             scale="pow2")
+    w1p, w2p = ops.pack_weight_fp8(w1q), ops.pack_weight_fp8(w2q)
+    t1e = timed_median(lambda: ops.grouped_gemm_fp8(xq, xs, w1p, w1s, off, out=c1, e8m0=True),
+                       steps, warmup)
+    t2e = timed_median(lambda: ops.grouped_gemm_fp8(hq, hs, w2p, w2s, off, out=y, e8m0=True),
+                       steps, warmup)
+    tfe = (fl1 + fl2) / ((t1e + t2e) * 1e-3) / 1e12
     tfu = (fl1 + fl2) / ((t1u + t2u) * 1e-3) / 1e12
     out = {"workload": "dsv3 local experts R=65536 H=7168 I=2048 E=32 zipf1.2",
            "weights": "packed (smoe_grouped_gemm_fp8_packed)",
@@ -237,6 +251,10 @@ def bench_gemm(dev, steps, warmup, skip_cpu=True):
            "tflops": round(tf, 1), "roofline_frac": round(tf / FP8_PEAK_TFLOPS, 4),
            "plain_fc1_ms": round(t1u, 4), "plain_fc2_ms": round(t2u, 4),
            "plain_tflops": round(tfu, 1), "plain_roofline_frac": round(tfu / FP8_PEAK_TFLOPS, 4),
+           "e8m0_fc1_ms": round(t1e, 4), "e8m0_fc2_ms": round(t2e, 4),
+           "e8m0_tflops": round(tfe, 1), "e8m0_roofline_frac": round(tfe / FP8_PEAK_TFLOPS, 4),
+           "e8m0_note": "power-of-two 1x128 / 128x128 scales (recipe e8m0), "
+                        "smoe_grouped_gemm_fp8_packed_e8m0",
            "peak_tflops": FP8_PEAK_TFLOPS}
     if not skip_cpu:
         out["cpu_baseline"] = cpu_gemm_baseline(xq, xs, w1q, w1s, c)
@@ -286,13 +304,20 @@ def bench_layer(dev, steps, warmup):
     with torch.no_grad():
         t = timed(lambda: m(x, lg), steps, warmup)
     t_train = timed(lambda: m(x, lg), steps, warmup)
+    # the same layer with power-of-two scales everywhere (recipe "e8m0":
+    # its packed GEMMs apply the scales in the MFMA)
+    m.recipe = "e8m0"
+    m.refresh_fp8_cache()
+    with torch.no_grad():
+        te = timed(lambda: m(x, lg), steps, warmup)
     fl = 2.0 * c.T * c.K * (2 * c.I) * c.H + 2.0 * c.T * c.K * c.H * c.I
     del m
     torch.cuda.empty_cache()
     return {"workload": "mixtral layer fwd T=8192 H=4096 I=14336 E=8 top2",
             "ms": round(t, 4), "tflops": round(fl / (t * 1e-3) / 1e12, 1),
             "ms_with_autograd": round(t_train, 4),
-            "tflops_with_autograd": round(fl / (t_train * 1e-3) / 1e12, 1)}
+            "tflops_with_autograd": round(fl / (t_train * 1e-3) / 1e12, 1),
+            "ms_e8m0_recipe": round(te, 4), "tflops_e8m0_recipe": round(fl / (te * 1e-3) / 1e12, 1)}
 
 
 def bench_fwd_bwd(dev, steps, warmup):
@@ -368,15 +393,20 @@ def bench_fwd_bwd(dev, steps, warmup):
 
     tu = timed_median(unfused_step, steps, warmup)
     del m.w1.main_grad, m.w2.main_grad
-    # the opt-in E8M0 weight-gradient recipe on the same step
+    # the opt-in E8M0 weight-gradient recipe on the same step, then the
+    # whole step with power-of-two scales (recipe "e8m0")
     m.wgrad_recipe = "e8m0"
     te = timed_median(step, steps, warmup)
+    m.recipe = "e8m0"
+    m.refresh_fp8_cache()
+    tr = timed_median(step, steps, warmup)
     del m
     torch.cuda.empty_cache()
     out.update({"ms_autograd": round(ta, 4), "tflops_autograd": tf(ta),
                 "ms_autograd_main_grad": round(tm, 4), "tflops_autograd_main_grad": tf(tm),
                 "ms_main_grad_unfused_add": round(tu, 4),
                 "ms_e8m0_wgrad": round(te, 4), "tflops_e8m0_wgrad": tf(te),
+                "ms_e8m0_recipe": round(tr, 4), "tflops_e8m0_recipe": tf(tr),
                 "autograd_note": "loss.backward() through SimpleMoE, grads reset per step; "
                                  "main_grad = fp32 buffers accumulated in the wgrad epilogue; "
                                  "unfused = fp32 dW then main_grad.add_"})
@@ -607,6 +637,18 @@ def bench_reference_shapes(dev, steps, warmup):
         ops.grouped_gemm_fp8(q, s, wp, ws, off, out=c)
 
     t_full = timed_median(full_fwd, steps, warmup)
+    # the same GEMMs with power-of-two scales on the E8M0 kernel
+    xq2, xs2 = ops.quant_rows(x, scale="pow2")
+    wq2, ws2 = ops.quantize_weight_blockwise(W.weights(E, N, K, device=dev), scale="pow2")
+    wp2 = ops.pack_weight_fp8(wq2)
+    wtq2, wts2 = ops.transpose_blockwise(wq2, ws2)
+    wtp2 = ops.pack_weight_fp8(wtq2)
+    dyq2, dys2 = ops.quant_rows(dy, scale="pow2")
+    t_fwd_e = timed_median(lambda: ops.grouped_gemm_fp8(xq2, xs2, wp2, ws2, off, out=c, e8m0=True),
+                           steps, warmup)
+    t_da_e = timed_median(lambda: ops.grouped_gemm_fp8(dyq2, dys2, wtp2, wts2, off, out=dx,
+                                                       e8m0=True), steps, warmup)
+    del xq2, xs2, wq2, ws2, wp2, wtq2, wts2, wtp2, dyq2, dys2
     fl = 2.0 * M * N * K
     out = {"gemm_E32_M8192_K7168_N2048": {
         "fwd_ms": round(t_fwd, 4), "fwd_tflops": round(fl / (t_fwd * 1e-3) / 1e12, 1),
@@ -614,6 +656,8 @@ def bench_reference_shapes(dev, steps, warmup):
         "dA_ms": round(t_da, 4), "dA_tflops": round(fl / (t_da * 1e-3) / 1e12, 1),
         "reference_dA_ms": 0.372,
         "quant_fwd_ms": round(t_full, 4), "reference_quant_fwd_ms": 0.524,
+        "e8m0_fwd_ms": round(t_fwd_e, 4), "e8m0_fwd_tflops": round(fl / (t_fwd_e * 1e-3) / 1e12, 1),
+        "e8m0_dA_ms": round(t_da_e, 4), "e8m0_dA_tflops": round(fl / (t_da_e * 1e-3) / 1e12, 1),
         "scales": "1x128 activations, 128x128 weights (reference: one per-tensor scale each)"}}
     del x, xq, xs, wq, ws, wp, wtq, wts, wtp, dy, dyq, dys, c, dx
     torch.cuda.empty_cache()
@@ -630,8 +674,8 @@ def bench_reference_shapes(dev, steps, warmup):
     torch.cuda.empty_cache()
     out["fp8_blockwise_fwd_bwd_E32_M4096_H2880"] = _grouped_fc_fwd_bwd(dev, 2880, steps, warmup)
     e = _grouped_fc_fwd_bwd(dev, 2880, steps, warmup, e8m0=True)
-    out["fp8_e8m0_wgrad_fwd_bwd_E32_M4096_H2880"] = {k: e[k] for k in ("fc1_ms", "fc2_ms", "sum_ms",
-                                                                       "tflops")}
+    out["fp8_e8m0_fwd_bwd_E32_M4096_H2880"] = {k: e[k] for k in ("fc1_ms", "fc2_ms", "sum_ms",
+                                                                 "tflops")}
     return out
 
 
@@ -649,20 +693,22 @@ def _grouped_fc_fwd_bwd(dev, hid, steps, warmup, e8m0=False):
     is at H = I = 2880, 22.5 groups of 128: the fp8 operands are quantised as
     zero-padded to 2944 (the short last group's scale from its 64 valid
     values), so fc1 runs K = 2944 and fc2 N = 2880 with a partial last tile.
-    The FLOP count is the reference's, at 2880.  ``e8m0``: the weight
-    gradient's 128x1 operands take power-of-two scales and the wgrad GEMM
-    applies them in the MFMA (the opt-in E8M0 recipe)."""
+    The FLOP count is the reference's, at 2880.  ``e8m0``: every
+    quantisation takes power-of-two scales (the opt-in E8M0 recipe); the
+    wgrad GEMM and the packed GEMMs (where K is a multiple of 512, not the
+    case at 2880) then apply them in the MFMA."""
     import torch
     from smoe import ops, workloads as W
     E, M = 32, 4096
     R = E * M
     off = W.offsets_from_counts([M] * E, dev)
     cs = "pow2" if e8m0 else "fp32"
+    rs = "pow2" if e8m0 else "amax"
     res = {}
     for name, N, Kd in (("fc1", 2 * hid, hid), ("fc2", hid, hid)):
         a = W.tokens(R, Kd, device=dev, seed=31)
         dyv = (W.tokens(R, N, device=dev, seed=32).float() * 1e-2).to(torch.bfloat16)
-        wq, ws = ops.quantize_weight_blockwise(W.weights(E, N, Kd, device=dev))
+        wq, ws = ops.quantize_weight_blockwise(W.weights(E, N, Kd, device=dev), scale=rs)
         wtq, wts = ops.transpose_blockwise(wq, ws, k=Kd)
         wf = ops.pack_weight_fp8(wq) if ops.packed_gemm_ok(N, wq.shape[2]) else wq
         wtf = ops.pack_weight_fp8(wtq) if ops.packed_gemm_ok(Kd, wtq.shape[2]) else wtq
@@ -671,10 +717,10 @@ def _grouped_fc_fwd_bwd(dev, hid, steps, warmup, e8m0=False):
         dw = torch.empty((E, N, Kd), dtype=torch.float32, device=dev)
 
         def fwd_bwd():
-            aq, as_ = ops.quant_rows(a)
-            ops.grouped_gemm_fp8(aq, as_, wf, ws, off, out=y)
-            dq, ds, dTq, dTs, pad, ld = ops.quant_rows_cols(dyv, off, col_scale=cs)
-            ops.grouped_gemm_fp8(dq, ds, wtf, wts, off, out=da)
+            aq, as_ = ops.quant_rows(a, scale=rs)
+            ops.grouped_gemm_fp8(aq, as_, wf, ws, off, out=y, e8m0=e8m0)
+            dq, ds, dTq, dTs, pad, ld = ops.quant_rows_cols(dyv, off, col_scale=cs, row_scale=rs)
+            ops.grouped_gemm_fp8(dq, ds, wtf, wts, off, out=da, e8m0=e8m0)
             aTq, aTs, _, _ = ops.quant_cols(a, off, col_scale=cs)
             ops.grouped_gemm_fp8_wgrad(dTq, dTs, aTq, aTs, pad, ld, out=dw, e8m0=e8m0)
 

@@ -158,6 +158,27 @@ int smoe_permute_quant(const uint16_t* x, const int32_t* inv_map, int T, int H, 
                        uint8_t* xq, float* xs, void* stream);
 
 /*
+ * Scale rule of the row and weight quantisers' _ex entry points:
+ *   SMOE_SCALE_AMAX  s = amax/448 (fp32 RN, 1 when amax == 0): the rule of
+ *                    the entry points without _ex;
+ *   SMOE_SCALE_POW2  s = the least power of two >= RN(amax/448), at least
+ *                    2^-127 (1 when amax == 0).  x/s is then exact and s is
+ *                    an E8M0 value: the power-of-two scales of the MXFP8
+ *                    recipe (moe/MegatronCore_MoE_reading_notes.md:503-504)
+ *                    at the blockwise recipe's 1x128 / 128x128 granularity.
+ *                    smoe_grouped_gemm_fp8_packed_e8m0 applies such scales
+ *                    in the MFMA.
+ * Any other value returns SMOE_EINVAL_MODE.  The bytes for SMOE_SCALE_AMAX
+ * equal those of the entry point without _ex.
+ */
+#define SMOE_SCALE_AMAX 0
+#define SMOE_SCALE_POW2 1
+
+/* smoe_permute_quant with a scale rule (SMOE_SCALE_*). */
+int smoe_permute_quant_ex(const uint16_t* x, const int32_t* inv_map, int T, int H, int K,
+                          uint8_t* xq, float* xs, int scale_mode, void* stream);
+
+/*
  * Dispatch convenience: smoe_route_sort followed by smoe_permute_quant on one
  * stream (no host sync).  ws as for smoe_route_sort.
  */
@@ -175,6 +196,10 @@ int smoe_dispatch_quant(const uint16_t* x, const int32_t* topk_idx, int T, int H
  */
 int smoe_quantize_weight_blockwise(const uint16_t* w, int E, int N, int Kdim, uint8_t* wq,
                                    float* ws, void* stream);
+
+/* smoe_quantize_weight_blockwise with a scale rule (SMOE_SCALE_*). */
+int smoe_quantize_weight_blockwise_ex(const uint16_t* w, int E, int N, int Kdim, uint8_t* wq,
+                                      float* ws, int scale_mode, void* stream);
 
 /*
  * Self-test of the fast quantisation path (no counterpart in the reference:
@@ -270,6 +295,24 @@ int smoe_grouped_gemm_fp8_packed(const uint8_t* a, const float* as, const uint8_
                                  int Kdim, uint16_t* c, void* stream);
 
 /*
+ * smoe_grouped_gemm_fp8_packed for power-of-two scales (SMOE_SCALE_POW2 on
+ * both operands): c within rounding of that kernel's (each K block's sum is
+ * added to the accumulator inside the MFMA instead of by an fp32 fma), with
+ * the scales applied by the scaled MFMA
+ * (v_mfma_scale_f32_16x16x128_f8f6f4) from their exponent bytes and the
+ * accumulators kept in the accumulation registers, which lets a workgroup
+ * of 4 waves (256 x 64 each) replace the 8 of the packed kernel.  Scales
+ * that are not powers of two are read by their exponent only (wrong
+ * results).  Same requirements as smoe_grouped_gemm_fp8_packed.  No
+ * counterpart of its own in the reference: the grouped GEMM it replaces is
+ * that of smoe_grouped_gemm_fp8, under the MXFP8-style power-of-two scale
+ * rule (moe/MegatronCore_MoE_reading_notes.md:503-504).
+ */
+int smoe_grouped_gemm_fp8_packed_e8m0(const uint8_t* a, const float* as, const uint8_t* wp,
+                                      const float* ws, const int32_t* offsets, int E, int R,
+                                      int N, int Kdim, uint16_t* c, void* stream);
+
+/*
  * smoe_grouped_gemm_fp8_swiglu on packed W1 (smoe_pack_weight_fp8 of w1
  * [E,2I,Kdim]): the same hq, hs (and c1 when not NULL) under the same
  * condition as smoe_grouped_gemm_fp8_packed.
@@ -304,6 +347,10 @@ int smoe_swiglu_quant(const uint16_t* c1, int R, int I, uint8_t* hq, float* hs,
 int smoe_swiglu_quant_h(const uint16_t* c1, int R, int I, uint8_t* hq, float* hs, uint16_t* h,
                         void* stream);
 
+/* smoe_swiglu_quant_h with a scale rule (SMOE_SCALE_*) for hs; h may be NULL. */
+int smoe_swiglu_quant_ex(const uint16_t* c1, int R, int I, uint8_t* hq, float* hs, uint16_t* h,
+                         int scale_mode, void* stream);
+
 /*
  * Weighted unpermute/combine: out[t] = bf16( sum_k w[t,k] * y[inv_map[t*K+k]] )
  * accumulated in fp32 in k order (each product and sum rounded separately).
@@ -334,11 +381,15 @@ int smoe_unpermute_combine(const uint16_t* y, const int32_t* inv_map, const floa
  *                       power-of-two scale of the MXFP8 recipe
  *                       (moe/MegatronCore_MoE_reading_notes.md:503-504) at the
  *                       blockwise recipe's 128-row granularity; it is opt-in.
- * Any other value returns SMOE_EINVAL_MODE.  The 1x128 row outputs always
- * use the FP32 rule.
+ * The quantisers that also write 1x128 rows (smoe_quant_rows_cols,
+ * smoe_swiglu_bwd_quant, smoe_unpermute_combine_bwd_quant) take in the same
+ * argument the bit SMOE_ROWSCALE_POW2, which gives their row scales the
+ * SMOE_SCALE_POW2 rule (their row scales follow the FP32 rule without it).
+ * Any other value returns SMOE_EINVAL_MODE.
  * ------------------------------------------------------------------------- */
 #define SMOE_COLSCALE_FP32 0
 #define SMOE_COLSCALE_POW2 1
+#define SMOE_ROWSCALE_POW2 2
 
 /*
  * Plain 1x128 row quantisation (no permutation): x [M,C] bf16 ->
@@ -348,6 +399,10 @@ int smoe_unpermute_combine(const uint16_t* y, const int32_t* inv_map, const floa
  * notes/2026-04/2026-04-21_gptoss_10_moe_fp8_grouped_gemm_diagnosis.md:99).
  */
 int smoe_quant_rows_1x128(const uint16_t* x, int M, int C, uint8_t* q, float* s, void* stream);
+
+/* smoe_quant_rows_1x128 with a scale rule (SMOE_SCALE_*). */
+int smoe_quant_rows_1x128_ex(const uint16_t* x, int M, int C, uint8_t* q, float* s,
+                             int scale_mode, void* stream);
 
 /*
  * Blockwise weight transpose for dgrad: wq [E,N,Kp] u8 + ws [E,NB,KB]

@@ -29,8 +29,11 @@ and is binding for the kernels too:
      padding is byte 0, fp8 operands keep the padded pitch, and a short last
      weight block (rows or columns) is the zero-padded block.  Blockwise fp8
      GEMMs need dimensions aligned to 16 (moe/MegatronCore_MoE_reading_notes.md:541-543).
-  C10 E8M0 column scales (opt-in, wgrad operands only): s = the least power of
-     two >= RN(amax/448), at least 2^-127 (1 when amax == 0); x/s is exact.
+  C10 E8M0 scales (opt-in): s = the least power of two >= RN(amax/448), at
+     least 2^-127 (1 when amax == 0); x/s is exact.  Either for the wgrad
+     operands' 128x1 columns only, or for every quantisation (activation
+     rows, weight blocks, gradient rows and columns), the MXFP8 scale format
+     at the blockwise recipe's granularity.
 
 Floating-point evaluation order is part of the contract where a kernel is
 bit-exact (router softmax reduction tree, exp routine, combine order): the
@@ -143,8 +146,8 @@ def group_scale(amax: np.ndarray) -> np.ndarray:
 
 
 def group_scale_pow2(amax: np.ndarray) -> np.ndarray:
-    """C10 (the optional E8M0 recipe of the wgrad operands): the least power
-    of two >= RN(amax / 448), at least 2^-127; 1 when amax == 0.  Powers of
+    """C10 (the optional E8M0 recipe): the least power of two
+    >= RN(amax / 448), at least 2^-127; 1 when amax == 0.  Powers of
     two are the E8M0 scale format of MXFP8 (moe/MegatronCore_MoE_reading_notes.md:503-504)."""
     amax = np.asarray(amax, np.float32)
     t = (amax / E4M3_MAX).astype(np.float32)
@@ -342,12 +345,13 @@ def quant_1x128(x: np.ndarray, pow2: bool = False):
     return q, s
 
 
-def permute_quant(x_bf16: np.ndarray, inv_map: np.ndarray, K: int):
-    """K1: quantise each token row once (C3) and place it at the K sorted rows
-    inv_map[t*K+k].  x_bf16 [T,H] uint16 -> xq [T*K,H] u8, xs [T*K,H/128] f32."""
+def permute_quant(x_bf16: np.ndarray, inv_map: np.ndarray, K: int, pow2: bool = False):
+    """K1: quantise each token row once (C3, or C10 with ``pow2``) and place it
+    at the K sorted rows inv_map[t*K+k].  x_bf16 [T,H] uint16 -> xq [T*K,H]
+    u8, xs [T*K,H/128] f32."""
     x = bf16_to_f32(x_bf16)
     T, H = x.shape
-    q, s = quant_1x128(x)
+    q, s = quant_1x128(x, pow2)
     R = T * K
     xq = np.empty((R, q.shape[1]), np.uint8)
     xs = np.empty((R, s.shape[1]), np.float32)
@@ -358,10 +362,11 @@ def permute_quant(x_bf16: np.ndarray, inv_map: np.ndarray, K: int):
     return xq, xs
 
 
-def quantize_weight_blockwise(w_bf16: np.ndarray):
+def quantize_weight_blockwise(w_bf16: np.ndarray, pow2: bool = False):
     """C4: 128x128 blocks of W[e] in [N, K] layout (summary/fp8_expert_gemm_optimization.md:137)
     -> wq [E,N,Kp] u8, ws [E,Np/128,Kp/128] f32 with Np, Kp = pad128(N, K):
-    per C9 edge blocks are the zero-padded blocks, and wq keeps N rows."""
+    per C9 edge blocks are the zero-padded blocks, and wq keeps N rows.
+    ``pow2``: the block scales follow C10."""
     w = bf16_to_f32(w_bf16)
     E, N, Kd = w.shape
     Np, Kp = pad128(N), pad128(Kd)
@@ -369,7 +374,7 @@ def quantize_weight_blockwise(w_bf16: np.ndarray):
         w = np.pad(w, ((0, 0), (0, Np - N), (0, Kp - Kd)))
     b = w.reshape(E, Np // GROUP, GROUP, Kp // GROUP, GROUP)
     amax = np.abs(b).max(axis=(2, 4))
-    s = group_scale(amax)
+    s = group_scale_pow2(amax) if pow2 else group_scale(amax)
     q = quant_rule(b, s[:, :, None, :, None]).reshape(E, Np, Kp)[:, :N]
     return np.ascontiguousarray(q), s
 
@@ -426,13 +431,14 @@ def silu_f32(g: np.ndarray) -> np.ndarray:
     return (g / (F32(1.0) + expf32(-g)).astype(np.float32)).astype(np.float32)
 
 
-def swiglu_quant(c1_bf16: np.ndarray):
+def swiglu_quant(c1_bf16: np.ndarray, pow2: bool = False):
     """C6: h = silu(g) * u in fp32 (g = columns [0,I), u = [I,2I);
-    moe/MoE_detailed_computation_dataflow.md:172-174), then C3 per 1x128."""
+    moe/MoE_detailed_computation_dataflow.md:172-174), then C3 (C10 with
+    ``pow2``) per 1x128."""
     c1 = bf16_to_f32(c1_bf16)
     I = c1.shape[1] // 2
     h = (silu_f32(c1[:, :I]) * c1[:, I:]).astype(np.float32)
-    return quant_1x128(h)
+    return quant_1x128(h, pow2)
 
 
 # ---------------------------------------------------------------------------
@@ -460,17 +466,18 @@ def unpermute_combine(y_bf16: np.ndarray, inv_map: np.ndarray, w: np.ndarray, K:
 # ---------------------------------------------------------------------------
 
 
-def moe_forward(x_bf16, logits, w1q, w1s, w2q, w2s, K, bias=None):
+def moe_forward(x_bf16, logits, w1q, w1s, w2q, w2s, K, bias=None, pow2: bool = False):
     """R -> K0 -> K1 -> K2(fc1) -> K3 -> K2(fc2) -> K5
     (moe/MoE_detailed_computation_dataflow.md:295-317).  GEMM outputs are
     rounded to bf16 between stages as the kernels do.  Returns a dict of every
-    intermediate so tests can check stage by stage."""
+    intermediate so tests can check stage by stage.  ``pow2``: the activation
+    quantisations follow C10 (the weights' scales are whatever w1s, w2s hold)."""
     E = w1q.shape[0]
     idx, w = router_topk(logits, K, bias)
     row_map, inv_map, counts, offsets = route_sort(idx, E)
-    xq, xs = permute_quant(x_bf16, inv_map, K)
+    xq, xs = permute_quant(x_bf16, inv_map, K, pow2)
     c1 = f32_to_bf16(grouped_gemm_fp8(xq, xs, w1q, w1s, offsets).astype(np.float32))
-    hq, hs = swiglu_quant(c1)
+    hq, hs = swiglu_quant(c1, pow2)
     y = f32_to_bf16(grouped_gemm_fp8(hq, hs, w2q, w2s, offsets).astype(np.float32))
     out = unpermute_combine(y, inv_map, w, K)
     return dict(topk_idx=idx, topk_w=w, row_map=row_map, inv_map=inv_map, counts=counts,
@@ -580,19 +587,21 @@ def combine_bwd(dout_bf16, y_bf16, inv_map, w, K: int):
     return dy, dw
 
 
-def moe_backward(fwd: dict, x_bf16, w1q, w1s, w2q, w2s, dout_bf16, K: int, pow2: bool = False):
+def moe_backward(fwd: dict, x_bf16, w1q, w1s, w2q, w2s, dout_bf16, K: int, pow2: bool = False,
+                 row_pow2: bool = False):
     """Backward of moe_forward given its intermediates and dout [T,H] bf16.
     Stages: combine bwd -> dy quant (1x128) -> fc2 dgrad (W2^T) -> fc2 wgrad
     (128x1 dy, h) -> SwiGLU bwd -> dc1 quant -> fc1 dgrad (W1^T) -> fc1 wgrad
     (128x1 dc1, x) -> un-permute (sum of the K replicas).  GEMM outputs are
     rounded to bf16 between stages like the kernels; wgrads stay float64.
-    ``pow2``: the wgrad operands' 128x1 scales follow C10 instead of C3."""
+    ``pow2``: the wgrad operands' 128x1 scales follow C10 instead of C3;
+    ``row_pow2`` likewise for the dgrad operands' 1x128 scales."""
     E = w1q.shape[0]
     off = fwd["offsets"]
     inv = fwd["inv_map"]
     T = x_bf16.shape[0]
     dy, dw = combine_bwd(dout_bf16, fwd["y"], inv, fwd["topk_w"], K)
-    dyq, dys = quant_1x128(bf16_to_f32(dy))
+    dyq, dys = quant_1x128(bf16_to_f32(dy), row_pow2)
     h = bf16_to_f32(fwd["c1"])
     I = h.shape[1] // 2
     H = x_bf16.shape[1]
@@ -604,7 +613,7 @@ def moe_backward(fwd: dict, x_bf16, w1q, w1s, w2q, w2s, dout_bf16, K: int, pow2:
     hTq, hTs, _ = quant_cols_128x1(hh, off, pow2)
     dW2 = grouped_gemm_fp8_wgrad(dyTq, dyTs, hTq, hTs, pad, E)
     dc1 = swiglu_bwd(fwd["c1"], dh)
-    dc1q, dc1s = quant_1x128(bf16_to_f32(dc1))
+    dc1q, dc1s = quant_1x128(bf16_to_f32(dc1), row_pow2)
     w1tq, w1ts = transpose_blockwise(w1q, w1s, k=H)
     dxs = f32_to_bf16(grouped_gemm_fp8(dc1q, dc1s, w1tq, w1ts, off).astype(np.float32))
     xs_sorted = bf16_to_f32(x_bf16)[fwd["row_map"] // K]

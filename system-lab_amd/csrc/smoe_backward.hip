@@ -99,9 +99,9 @@ constexpr int kQcCols = 128;
 // I/128 + b (du) come from one sigmoid evaluation.  dc1 is written only when
 // not null.
 // kPow2: the 128x1 column scales are group_scale_pow2 (the optional E8M0
-// recipe of the wgrad operands) instead of group_scale; the 1x128 row scales
-// (kRows) keep group_scale.
-template <bool kRows, bool kSwigluBwd, bool kPow2>
+// recipe of the wgrad operands) instead of group_scale; kRowPow2 likewise for
+// the 1x128 row scales (kRows).
+template <bool kRows, bool kSwigluBwd, bool kPow2, bool kRowPow2 = false>
 __global__ __launch_bounds__(256) void quant_cols_kernel(
     const uint16_t* __restrict__ x, const int32_t* __restrict__ gather, int gather_div,
     const float* __restrict__ gather_w, int R, int C, const int32_t* __restrict__ offsets, const int32_t* __restrict__ pad, int E, int ld,
@@ -177,7 +177,7 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(
         float am = rmax[0];
 #pragma unroll
         for (int i = 1; i < 8; ++i) am = (j == i) ? rmax[i] : am;
-        const float sc = group_scale(am);
+        const float sc = scale_of<kRowPow2>(am);
         const QDiv qd = qdiv_setup(sc);
         const int r = rg * 8 + j;
         row_m[r] = qd.m;
@@ -192,7 +192,7 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(
     // that hold pieces of a column would otherwise repeat the divisions
     if (t < kQcCols) {
       const float am = fmaxf(fmaxf(wmax[0][t], wmax[1][t]), fmaxf(wmax[2][t], wmax[3][t]));
-      const float sc = kPow2 ? group_scale_pow2(am) : group_scale(am);
+      const float sc = scale_of<kPow2>(am);
       const QDiv qd = qdiv_setup(sc);
       col_m[t] = qd.m;
       col_r[t] = qd.r;
@@ -401,7 +401,7 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(const uint16_t* __restr
 // kQuant: dy is not stored; its 1x128 row quantisation goes to dyq [T*K, H]
 // / dys [T*K, H/128] instead (the 16 lanes that hold a 128-column group
 // share its amax), the bytes smoe_quant_rows_1x128 would write from dy.
-template <int kMaxK, bool kQuant>
+template <int kMaxK, bool kQuant, bool kRowPow2 = false>
 __global__ __launch_bounds__(256) void combine_bwd_kernel(
     const uint16_t* __restrict__ dout, const uint16_t* __restrict__ y,
     const int32_t* __restrict__ inv_map, const float* __restrict__ w, int T, int K, int H,
@@ -463,7 +463,7 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(
           m = fmaxf(m, fabsf(__uint_as_float(o[i] << 16)));
           m = fmaxf(m, fabsf(__uint_as_float(o[i] & 0xffff0000u)));
         }
-        const float sc = group_scale(row16_max(m));
+        const float sc = scale_of<kRowPow2>(row16_max(m));
         const QDiv qd = qdiv_setup(sc);
         float qv[8];
 #pragma unroll
@@ -548,7 +548,8 @@ extern "C" int smoe_quant_rows_cols(const uint16_t* x, int R, int C, const int32
                                     int ld, uint8_t* xq, float* xs, uint8_t* xTq, float* xTs,
                                     int32_t* pad, int col_scale, void* stream) {
   if (R <= 0 || C <= 0) return SMOE_EINVAL_DIM;
-  if (col_scale != SMOE_COLSCALE_FP32 && col_scale != SMOE_COLSCALE_POW2) return SMOE_EINVAL_MODE;
+  if (col_scale & ~(SMOE_COLSCALE_POW2 | SMOE_ROWSCALE_POW2)) return SMOE_EINVAL_MODE;
+  const bool cp2 = col_scale & SMOE_COLSCALE_POW2, rp2 = col_scale & SMOE_ROWSCALE_POW2;
   if (E <= 0 || E > SMOE_MAX_EXPERTS) return SMOE_EINVAL_EXPERTS;
   if (C % kLane) return SMOE_EINVAL_ALIGN128;
   if (ld < smoe_quant_cols_ld(R, E) || ld % kGroup) return SMOE_EINVAL_DIM;
@@ -562,11 +563,11 @@ extern "C" int smoe_quant_rows_cols(const uint16_t* x, int R, int C, const int32
   if ((uintptr_t)xq & 7u) return SMOE_EINVAL_PTRALIGN;
   hipStream_t s = (hipStream_t)stream;
   pad_offsets_kernel<<<1, 1024, 0, s>>>(offsets, E, pad);
-#define SMOE_QRC(P2)                                                                           \
-  quant_cols_kernel<true, false, P2><<<dim3((C + kQcCols - 1) / kQcCols, ld / kGroup), dim3(256), 0, s>>>( \
+#define SMOE_QRC(P2, RP2)                                                                      \
+  quant_cols_kernel<true, false, P2, RP2><<<dim3((C + kQcCols - 1) / kQcCols, ld / kGroup), dim3(256), 0, s>>>( \
       x, nullptr, 1, nullptr, R, C, offsets, pad, E, ld, xTq, xTs, xq, xs, nullptr, nullptr, nullptr)
-  if (col_scale == SMOE_COLSCALE_POW2) SMOE_QRC(true);
-  else SMOE_QRC(false);
+  if (cp2) { if (rp2) SMOE_QRC(true, true); else SMOE_QRC(true, false); }
+  else { if (rp2) SMOE_QRC(false, true); else SMOE_QRC(false, false); }
 #undef SMOE_QRC
   SMOE_RETURN_LAUNCH();
 }
@@ -576,7 +577,8 @@ extern "C" int smoe_swiglu_bwd_quant(const uint16_t* c1, const uint16_t* dh, int
                                      float* dcs, uint8_t* dcTq, float* dcTs, int32_t* pad,
                                      uint16_t* dc1, int col_scale, void* stream) {
   if (R <= 0 || I <= 0) return SMOE_EINVAL_DIM;
-  if (col_scale != SMOE_COLSCALE_FP32 && col_scale != SMOE_COLSCALE_POW2) return SMOE_EINVAL_MODE;
+  if (col_scale & ~(SMOE_COLSCALE_POW2 | SMOE_ROWSCALE_POW2)) return SMOE_EINVAL_MODE;
+  const bool cp2 = col_scale & SMOE_COLSCALE_POW2, rp2 = col_scale & SMOE_ROWSCALE_POW2;
   if (E <= 0 || E > SMOE_MAX_EXPERTS) return SMOE_EINVAL_EXPERTS;
   if (I % kGroup) return SMOE_EINVAL_ALIGN128;
   if (ld < smoe_quant_cols_ld(R, E) || ld % kGroup) return SMOE_EINVAL_DIM;
@@ -593,11 +595,11 @@ extern "C" int smoe_swiglu_bwd_quant(const uint16_t* c1, const uint16_t* dh, int
   hipStream_t s = (hipStream_t)stream;
   pad_offsets_kernel<<<1, 1024, 0, s>>>(offsets, E, pad);
   // one workgroup per 128-column block of both halves (dg and du)
-#define SMOE_SBQ(P2)                                                               \
-  quant_cols_kernel<true, true, P2><<<dim3(I / kQcCols, ld / kGroup), dim3(256), 0, s>>>( \
+#define SMOE_SBQ(P2, RP2)                                                          \
+  quant_cols_kernel<true, true, P2, RP2><<<dim3(I / kQcCols, ld / kGroup), dim3(256), 0, s>>>( \
       nullptr, nullptr, 1, nullptr, R, C, offsets, pad, E, ld, dcTq, dcTs, dcq, dcs, c1, dh, dc1)
-  if (col_scale == SMOE_COLSCALE_POW2) SMOE_SBQ(true);
-  else SMOE_SBQ(false);
+  if (cp2) { if (rp2) SMOE_SBQ(true, true); else SMOE_SBQ(true, false); }
+  else { if (rp2) SMOE_SBQ(false, true); else SMOE_SBQ(false, false); }
 #undef SMOE_SBQ
   SMOE_RETURN_LAUNCH();
 }
@@ -645,7 +647,8 @@ extern "C" int smoe_unpermute_combine_bwd_quant(const uint16_t* dout, const uint
                                                 float* dyTs, int32_t* pad, float* dw,
                                                 int col_scale, void* stream) {
   if (T <= 0 || H <= 0) return SMOE_EINVAL_DIM;
-  if (col_scale != SMOE_COLSCALE_FP32 && col_scale != SMOE_COLSCALE_POW2) return SMOE_EINVAL_MODE;
+  if (col_scale & ~(SMOE_COLSCALE_POW2 | SMOE_ROWSCALE_POW2)) return SMOE_EINVAL_MODE;
+  const bool cp2 = col_scale & SMOE_COLSCALE_POW2, rp2 = col_scale & SMOE_ROWSCALE_POW2;
   if (H % kLane) return SMOE_EINVAL_ALIGN128;
   if (K <= 0 || K > 32) return SMOE_EINVAL_TOPK;
   if ((long long)T * K > 0x7fffffffLL) return SMOE_EINVAL_DIM;
@@ -665,12 +668,18 @@ extern "C" int smoe_unpermute_combine_bwd_quant(const uint16_t* dout, const uint
   hipStream_t s = (hipStream_t)stream;
   // dw and the 1x128 rows of dy; dy itself is never stored
   const dim3 grid((T + 3) / 4), block(256);
-#define SMOE_CBB(MK) \
-  combine_bwd_kernel<MK, true><<<grid, block, 0, s>>>(dout, y, inv_map, w, T, K, H, nullptr, dw, \
-                                                      dyq, dys)
-  if (K <= 2) SMOE_CBB(2);
-  else if (K <= 8) SMOE_CBB(8);
-  else SMOE_CBB(32);
+#define SMOE_CBB(MK, RP2) \
+  combine_bwd_kernel<MK, true, RP2><<<grid, block, 0, s>>>(dout, y, inv_map, w, T, K, H, nullptr, dw, \
+                                                           dyq, dys)
+  if (rp2) {
+    if (K <= 2) SMOE_CBB(2, true);
+    else if (K <= 8) SMOE_CBB(8, true);
+    else SMOE_CBB(32, true);
+  } else {
+    if (K <= 2) SMOE_CBB(2, false);
+    else if (K <= 8) SMOE_CBB(8, false);
+    else SMOE_CBB(32, false);
+  }
 #undef SMOE_CBB
   pad_offsets_kernel<<<1, 1024, 0, s>>>(offsets, E, pad);
   // 128x1 columns: row r of dy is rebuilt as bf16(w[p] * dout[p / K]) with
@@ -679,7 +688,7 @@ extern "C" int smoe_unpermute_combine_bwd_quant(const uint16_t* dout, const uint
   quant_cols_kernel<false, false, P2><<<dim3((H + kQcCols - 1) / kQcCols, ld / kGroup), dim3(256), 0, \
                                         s>>>(dout, row_map, K, w, R, H, offsets, pad, E, ld, dyTq,   \
                                              dyTs, nullptr, nullptr, nullptr, nullptr, nullptr)
-  if (col_scale == SMOE_COLSCALE_POW2) SMOE_CQ(true);
+  if (cp2) SMOE_CQ(true);
   else SMOE_CQ(false);
 #undef SMOE_CQ
   SMOE_RETURN_LAUNCH();

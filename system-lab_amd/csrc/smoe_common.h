@@ -266,13 +266,22 @@ struct Q16 {
   float scale;  // group scale (identical in the 8 lanes of a group)
 };
 
+// The group scale of a quantiser: amax/448 (group_scale), or with kPow2 the
+// least power of two at or above it (group_scale_pow2).
+template <bool kPow2>
+__device__ __forceinline__ float scale_of(float amax) {
+  if constexpr (kPow2) return group_scale_pow2(amax);
+  else return group_scale(amax);
+}
+
 // Quantise 16 fp32 values owned by this lane whose group spans 8 lanes.
+template <bool kPow2 = false>
 __device__ __forceinline__ Q16 quant16(const float (&f)[16]) {
   float amax = 0.0f;
 #pragma unroll
   for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(f[i]));
   amax = group_max<8>(amax);
-  const float s = group_scale(amax);
+  const float s = scale_of<kPow2>(amax);
   uint32_t w[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
@@ -284,13 +293,15 @@ __device__ __forceinline__ Q16 quant16(const float (&f)[16]) {
   return r;
 }
 
-// As quant16, for bf16 inputs (the division-free quantiser).
+// As quant16, for bf16 inputs (the division-free quantiser; with a
+// power-of-two scale its quotient is exact).
+template <bool kPow2 = false>
 __device__ __forceinline__ Q16 quant16_bf16(const float (&f)[16]) {
   float amax = 0.0f;
 #pragma unroll
   for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(f[i]));
   amax = group_max<8>(amax);
-  const float s = group_scale(amax);
+  const float s = scale_of<kPow2>(amax);
   const QDiv d = qdiv_setup(s);
   uint32_t w[4];
 #pragma unroll

@@ -37,7 +37,7 @@ __device__ __forceinline__ void store16(uint8_t* p, const uint4& q) {
   }
 }
 
-template <int kUnroll, bool kNT>
+template <int kUnroll, bool kNT, bool kPow2 = false>
 __global__ __launch_bounds__(256) void permute_quant_kernel(
     const uint16_t* __restrict__ x, const int32_t* __restrict__ inv_map, int T, int H, int K,
     uint8_t* __restrict__ xq, float* __restrict__ xs) {
@@ -72,7 +72,7 @@ __global__ __launch_bounds__(256) void permute_quant_kernel(
       float f[16];
       unpack_bf16x8(v[u][0], f);
       unpack_bf16x8(v[u][1], f + 8);
-      q[u] = quant16_bf16(f);
+      q[u] = quant16_bf16<kPow2>(f);
     }
     for (int k = 0; k < K; ++k) {
       const int r = __shfl(my_r, k, kWave);
@@ -96,7 +96,7 @@ __global__ __launch_bounds__(256) void permute_quant_kernel(
 // consecutively) before the next.  kW = 2 halves the registers a wave holds
 // (88 VGPRs for 4 chunks against 156 for 7 chunks in one wave), so 5 waves
 // per SIMD instead of 3 keep loads in flight.
-template <int kC, int kW, bool kNT>
+template <int kC, int kW, bool kNT, bool kPow2 = false>
 __global__ __launch_bounds__(256) void permute_quant_row_kernel(
     const uint16_t* __restrict__ x, const int32_t* __restrict__ inv_map, int T, int H, int K,
     uint8_t* __restrict__ xq, float* __restrict__ xs) {
@@ -132,7 +132,7 @@ __global__ __launch_bounds__(256) void permute_quant_row_kernel(
     float f[16];
     unpack_bf16x8(v[c][0], f);
     unpack_bf16x8(v[c][1], f + 8);
-    q[c] = quant16_bf16(f);
+    q[c] = quant16_bf16<kPow2>(f);
   }
   for (int k = 0; k < K; ++k) {
     const int r = __shfl(my_r, k, kWave);
@@ -156,7 +156,7 @@ __global__ __launch_bounds__(256) void permute_quant_row_kernel(
 // kUnroll batches' loads are issued before any arithmetic.  kSaveH: also
 // write h rounded to bf16 (the fc2 wgrad operand of the backward pass),
 // saving a recompute from c1.
-template <int kUnroll, bool kSaveH>
+template <int kUnroll, bool kSaveH, bool kPow2 = false>
 __global__ __launch_bounds__(256) void swiglu_quant_kernel(const uint16_t* __restrict__ c1,
                                                            uint32_t nslots, int I,
                                                            uint8_t* __restrict__ hq,
@@ -196,7 +196,7 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const uint16_t* __res
     for (int i = 0; i < 16; ++i) h[i] = silu32(fg[i]) * fu[i];
     // the 8 lanes of a group share one slot, so the group's amax shuffle
     // never mixes slots (or a valid slot with padding)
-    const Q16 q = quant16(h);
+    const Q16 q = quant16<kPow2>(h);
     if (base + u * 8 + gl < nslots) {
       const int col = (int)gg[u] * kGroup + sub * kLane;
       if (kSaveH && col < I) {
@@ -219,6 +219,7 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const uint16_t* __res
 // [E, N, Kd] bf16; wq is [E, N, Kp] with Kp = pad128(Kd), ws [E, NB, Kp/128]
 // with NB = ceil(N/128).  Rows past N and columns past Kd of an edge block
 // are zeros (not read); padding columns are written as byte 0.
+template <bool kPow2 = false>
 __global__ __launch_bounds__(256) void quant_weight_kernel(const uint16_t* __restrict__ w,
                                                            int N, int Kd,
                                                            uint8_t* __restrict__ wq,
@@ -250,7 +251,7 @@ __global__ __launch_bounds__(256) void quant_weight_kernel(const uint16_t* __res
   if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = amax;
   __syncthreads();
   amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-  const float s = group_scale(amax);
+  const float s = scale_of<kPow2>(amax);
   const QDiv d = qdiv_setup(s);
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
@@ -403,18 +404,11 @@ extern "C" int smoe_selftest_recip(unsigned long long* counts, void* stream) {
   SMOE_RETURN_LAUNCH();
 }
 
-extern "C" int smoe_permute_quant(const uint16_t* x, const int32_t* inv_map, int T, int H, int K,
-                                  uint8_t* xq, float* xs, void* stream) {
-  if (T <= 0 || H <= 0) return SMOE_EINVAL_DIM;
-  if (H % kLane) return SMOE_EINVAL_ALIGN128;
-  if (K <= 0 || K > 32) return SMOE_EINVAL_TOPK;
-  if ((long long)T * K > 0x7fffffffLL) return SMOE_EINVAL_DIM;
-  SMOE_CHECK_PTR(x);
-  SMOE_CHECK_PTR(inv_map);
-  SMOE_CHECK_PTR(xq);
-  SMOE_CHECK_PTR(xs);
+namespace {
+template <bool kPow2>
+int permute_quant_launch(const uint16_t* x, const int32_t* inv_map, int T, int H, int K,
+                         uint8_t* xq, float* xs, hipStream_t s) {
   const int chunks = (pad128(H) / kGroup + 7) / 8;
-  hipStream_t s = (hipStream_t)stream;
   // Rows of up to 8 chunks (H <= 8192): the whole-row kernel with cached
   // stores, rows of 5..8 chunks split over two waves.  Measured with cold
   // caches at config 2 (T=16384, H=7168, top-8) on one box: 0.214 ms for
@@ -423,7 +417,7 @@ extern "C" int smoe_permute_quant(const uint16_t* x, const int32_t* inv_map, int
   // row took 212 us, its non-temporal stores took 229 us and the
   // chunk-interleaved kernel below 232 us.
 #define SMOE_PR(C, W) \
-  permute_quant_row_kernel<C, W, false><<<dim3((unsigned)(((long long)T * W + 3) / 4)), dim3(256), 0, s>>>( \
+  permute_quant_row_kernel<C, W, false, kPow2><<<dim3((unsigned)(((long long)T * W + 3) / 4)), dim3(256), 0, s>>>( \
       x, inv_map, T, H, K, xq, xs)
   if (chunks <= 8) {
     switch (chunks) {
@@ -436,24 +430,16 @@ extern "C" int smoe_permute_quant(const uint16_t* x, const int32_t* inv_map, int
 #undef SMOE_PR
   // longer rows: kUnroll = 4 chunks (128 B per lane) in flight keeps 2+
   // waves per SIMD
-#define SMOE_PQ(U) \
-  permute_quant_kernel<U, true><<<dim3((unsigned)(((long long)T + 3) / 4)), dim3(256), 0, s>>>(x, inv_map, T, H, K, xq, xs)
-  SMOE_PQ(4);
-#undef SMOE_PQ
+  permute_quant_kernel<4, true, kPow2><<<dim3((unsigned)(((long long)T + 3) / 4)), dim3(256), 0, s>>>(
+      x, inv_map, T, H, K, xq, xs);
   SMOE_RETURN_LAUNCH();
 }
 
-extern "C" int smoe_quant_rows_1x128(const uint16_t* x, int M, int C, uint8_t* q, float* s,
-                                     void* stream) {
-  if (M <= 0 || C <= 0) return SMOE_EINVAL_DIM;
-  if (C % kLane) return SMOE_EINVAL_ALIGN128;
-  SMOE_CHECK_PTR(x);
-  SMOE_CHECK_PTR(q);
-  SMOE_CHECK_PTR(s);
+template <bool kPow2>
+int quant_rows_launch(const uint16_t* x, int M, int C, uint8_t* q, float* s, hipStream_t st) {
   const int chunks = (pad128(C) / kGroup + 7) / 8;
   const dim3 grid((M + 3) / 4), block(256);
-  hipStream_t st = (hipStream_t)stream;
-#define SMOE_QR(U) permute_quant_kernel<U, true><<<grid, block, 0, st>>>(x, nullptr, M, C, 1, q, s)
+#define SMOE_QR(U) permute_quant_kernel<U, true, kPow2><<<grid, block, 0, st>>>(x, nullptr, M, C, 1, q, s)
   switch (chunks) {
     case 1: SMOE_QR(1); break;
     case 2: SMOE_QR(2); break;
@@ -462,6 +448,47 @@ extern "C" int smoe_quant_rows_1x128(const uint16_t* x, int M, int C, uint8_t* q
   }
 #undef SMOE_QR
   SMOE_RETURN_LAUNCH();
+}
+}  // namespace
+
+extern "C" int smoe_permute_quant_ex(const uint16_t* x, const int32_t* inv_map, int T, int H,
+                                     int K, uint8_t* xq, float* xs, int scale_mode,
+                                     void* stream) {
+  if (T <= 0 || H <= 0) return SMOE_EINVAL_DIM;
+  if (H % kLane) return SMOE_EINVAL_ALIGN128;
+  if (K <= 0 || K > 32) return SMOE_EINVAL_TOPK;
+  if ((long long)T * K > 0x7fffffffLL) return SMOE_EINVAL_DIM;
+  if (scale_mode != SMOE_SCALE_AMAX && scale_mode != SMOE_SCALE_POW2) return SMOE_EINVAL_MODE;
+  SMOE_CHECK_PTR(x);
+  SMOE_CHECK_PTR(inv_map);
+  SMOE_CHECK_PTR(xq);
+  SMOE_CHECK_PTR(xs);
+  hipStream_t s = (hipStream_t)stream;
+  return scale_mode == SMOE_SCALE_POW2 ? permute_quant_launch<true>(x, inv_map, T, H, K, xq, xs, s)
+                                       : permute_quant_launch<false>(x, inv_map, T, H, K, xq, xs, s);
+}
+
+extern "C" int smoe_permute_quant(const uint16_t* x, const int32_t* inv_map, int T, int H, int K,
+                                  uint8_t* xq, float* xs, void* stream) {
+  return smoe_permute_quant_ex(x, inv_map, T, H, K, xq, xs, SMOE_SCALE_AMAX, stream);
+}
+
+extern "C" int smoe_quant_rows_1x128_ex(const uint16_t* x, int M, int C, uint8_t* q, float* s,
+                                        int scale_mode, void* stream) {
+  if (M <= 0 || C <= 0) return SMOE_EINVAL_DIM;
+  if (C % kLane) return SMOE_EINVAL_ALIGN128;
+  if (scale_mode != SMOE_SCALE_AMAX && scale_mode != SMOE_SCALE_POW2) return SMOE_EINVAL_MODE;
+  SMOE_CHECK_PTR(x);
+  SMOE_CHECK_PTR(q);
+  SMOE_CHECK_PTR(s);
+  hipStream_t st = (hipStream_t)stream;
+  return scale_mode == SMOE_SCALE_POW2 ? quant_rows_launch<true>(x, M, C, q, s, st)
+                                       : quant_rows_launch<false>(x, M, C, q, s, st);
+}
+
+extern "C" int smoe_quant_rows_1x128(const uint16_t* x, int M, int C, uint8_t* q, float* s,
+                                     void* stream) {
+  return smoe_quant_rows_1x128_ex(x, M, C, q, s, SMOE_SCALE_AMAX, stream);
 }
 
 extern "C" int smoe_dispatch_quant(const uint16_t* x, const int32_t* topk_idx, int T, int H,
@@ -479,10 +506,11 @@ extern "C" int smoe_dispatch_quant(const uint16_t* x, const int32_t* topk_idx, i
   return smoe_permute_quant(x, inv_map, T, H, K, xq, xs, stream);
 }
 
-extern "C" int smoe_swiglu_quant_h(const uint16_t* c1, int R, int I, uint8_t* hq, float* hs,
-                                   uint16_t* h, void* stream) {
+extern "C" int smoe_swiglu_quant_ex(const uint16_t* c1, int R, int I, uint8_t* hq, float* hs,
+                                    uint16_t* h, int scale_mode, void* stream) {
   if (R <= 0 || I <= 0) return SMOE_EINVAL_DIM;
   if (I % kLane) return SMOE_EINVAL_ALIGN128;
+  if (scale_mode != SMOE_SCALE_AMAX && scale_mode != SMOE_SCALE_POW2) return SMOE_EINVAL_MODE;
   SMOE_CHECK_PTR(c1);
   SMOE_CHECK_PTR(hq);
   SMOE_CHECK_PTR(hs);
@@ -493,29 +521,47 @@ extern "C" int smoe_swiglu_quant_h(const uint16_t* c1, int R, int I, uint8_t* hq
   if (nslots + 32LL * kU > 0xffffffffLL) return SMOE_EINVAL_DIM;
   const dim3 grid((unsigned)((nslots + 32 * kU - 1) / (32 * kU))), block(256);
   hipStream_t s = (hipStream_t)stream;
-  if (h)
-    swiglu_quant_kernel<kU, true><<<grid, block, 0, s>>>(c1, (uint32_t)nslots, I, hq, hs, h);
-  else
-    swiglu_quant_kernel<kU, false><<<grid, block, 0, s>>>(c1, (uint32_t)nslots, I, hq, hs, nullptr);
+#define SMOE_SQ(H, P) \
+  swiglu_quant_kernel<kU, H, P><<<grid, block, 0, s>>>(c1, (uint32_t)nslots, I, hq, hs, H ? h : nullptr)
+  const bool p2 = scale_mode == SMOE_SCALE_POW2;
+  if (h) { if (p2) SMOE_SQ(true, true); else SMOE_SQ(true, false); }
+  else { if (p2) SMOE_SQ(false, true); else SMOE_SQ(false, false); }
+#undef SMOE_SQ
   SMOE_RETURN_LAUNCH();
+}
+
+extern "C" int smoe_swiglu_quant_h(const uint16_t* c1, int R, int I, uint8_t* hq, float* hs,
+                                   uint16_t* h, void* stream) {
+  return smoe_swiglu_quant_ex(c1, R, I, hq, hs, h, SMOE_SCALE_AMAX, stream);
 }
 
 extern "C" int smoe_swiglu_quant(const uint16_t* c1, int R, int I, uint8_t* hq, float* hs,
                                  void* stream) {
-  return smoe_swiglu_quant_h(c1, R, I, hq, hs, nullptr, stream);
+  return smoe_swiglu_quant_ex(c1, R, I, hq, hs, nullptr, SMOE_SCALE_AMAX, stream);
 }
 
-extern "C" int smoe_quantize_weight_blockwise(const uint16_t* w, int E, int N, int Kdim,
-                                              uint8_t* wq, float* ws, void* stream) {
+extern "C" int smoe_quantize_weight_blockwise_ex(const uint16_t* w, int E, int N, int Kdim,
+                                                 uint8_t* wq, float* ws, int scale_mode,
+                                                 void* stream) {
   if (N <= 0 || Kdim <= 0) return SMOE_EINVAL_DIM;
   if (E <= 0 || E > SMOE_MAX_EXPERTS) return SMOE_EINVAL_EXPERTS;
   if (N % kLane || Kdim % kLane) return SMOE_EINVAL_ALIGN128;
+  if (scale_mode != SMOE_SCALE_AMAX && scale_mode != SMOE_SCALE_POW2) return SMOE_EINVAL_MODE;
   SMOE_CHECK_PTR(w);
   SMOE_CHECK_PTR(wq);
   SMOE_CHECK_PTR(ws);
   const long long blocks = (long long)E * ((N + kGroup - 1) / kGroup) * (pad128(Kdim) / kGroup);
   if (blocks > 0x7fffffffLL) return SMOE_EINVAL_DIM;
-  quant_weight_kernel<<<dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream>>>(w, N, Kdim,
-                                                                                      wq, ws);
+  const dim3 grid((unsigned)blocks), block(256);
+  hipStream_t s = (hipStream_t)stream;
+  if (scale_mode == SMOE_SCALE_POW2)
+    quant_weight_kernel<true><<<grid, block, 0, s>>>(w, N, Kdim, wq, ws);
+  else
+    quant_weight_kernel<false><<<grid, block, 0, s>>>(w, N, Kdim, wq, ws);
   SMOE_RETURN_LAUNCH();
+}
+
+extern "C" int smoe_quantize_weight_blockwise(const uint16_t* w, int E, int N, int Kdim,
+                                              uint8_t* wq, float* ws, void* stream) {
+  return smoe_quantize_weight_blockwise_ex(w, E, N, Kdim, wq, ws, SMOE_SCALE_AMAX, stream);
 }

@@ -29,11 +29,13 @@ SIGNATURES = {
     "smoe_route_topk_sort": (c_int, [P, P, c_int, c_int, c_int, P, P, P, P, P, P, P, c_size_t,
                                      P]),
     "smoe_permute_quant": (c_int, [P, P, c_int, c_int, c_int, P, P, P]),
+    "smoe_permute_quant_ex": (c_int, [P, P, c_int, c_int, c_int, P, P, c_int, P]),
     "smoe_dispatch_quant": (c_int, [P, P, c_int, c_int, c_int, c_int, P, P, P, P, P, P, P,
                                     c_size_t, P]),
     "smoe_selftest_quant": (c_int, [P, P]),
     "smoe_selftest_recip": (c_int, [P, P]),
     "smoe_quantize_weight_blockwise": (c_int, [P, c_int, c_int, c_int, P, P, P]),
+    "smoe_quantize_weight_blockwise_ex": (c_int, [P, c_int, c_int, c_int, P, P, c_int, P]),
     "smoe_grouped_gemm_fp8_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int]),
     "smoe_grouped_gemm_fp8": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int, P, P,
                                       c_size_t, P]),
@@ -41,12 +43,15 @@ SIGNATURES = {
                                              P, P]),
     "smoe_pack_weight_fp8": (c_int, [P, c_int, c_int, c_int, P, P]),
     "smoe_grouped_gemm_fp8_packed": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int, P, P]),
+    "smoe_grouped_gemm_fp8_packed_e8m0": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int, P, P]),
     "smoe_grouped_gemm_fp8_packed_swiglu": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int,
                                                     P, P, P, P]),
     "smoe_swiglu_quant": (c_int, [P, c_int, c_int, P, P, P]),
     "smoe_swiglu_quant_h": (c_int, [P, c_int, c_int, P, P, P, P]),
+    "smoe_swiglu_quant_ex": (c_int, [P, c_int, c_int, P, P, P, c_int, P]),
     "smoe_unpermute_combine": (c_int, [P, P, P, c_int, c_int, c_int, P, P]),
     "smoe_quant_rows_1x128": (c_int, [P, c_int, c_int, P, P, P]),
+    "smoe_quant_rows_1x128_ex": (c_int, [P, c_int, c_int, P, P, c_int, P]),
     "smoe_transpose_blockwise_fp8": (c_int, [P, P, c_int, c_int, c_int, P, P, P]),
     "smoe_quant_cols_ld": (c_int, [c_int, c_int]),
     "smoe_quant_cols_128x1": (c_int, [P, P, c_int, c_int, c_int, P, c_int, c_int, P, P, P, c_int,

@@ -20,7 +20,7 @@ LIB = os.path.join(PKG, "libsmoe.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 SOURCES = ["smoe_api.cpp", "smoe_route.hip", "smoe_quant.hip", "smoe_gemm.hip",
-           "smoe_gemm_wgrad.hip", "smoe_gemm_packed.hip", "smoe_combine.hip", "smoe_backward.hip"]
+           "smoe_gemm_wgrad.hip", "smoe_gemm_packed.hip", "smoe_gemm_e8m0.hip", "smoe_combine.hip", "smoe_backward.hip"]
 # the benchmark's HBM probe: its own library, not part of libsmoe.so
 PROBE_SOURCES = ["bench/smoe_bw_probe.hip"]
 PROBE_LIB = os.path.join(PKG, "libsmoe_probe.so")

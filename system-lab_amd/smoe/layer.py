@@ -105,6 +105,14 @@ class SimpleMoE(nn.Module):
     them in hardware and the wgrad does no per-output scale arithmetic.  The
     forward and the dgrad are the same in both.
 
+    ``recipe`` chooses the scale rule of every quantisation: "blockwise" (the
+    default: amax/448 for 1x128 activation and gradient rows and 128x128
+    weight blocks) or "e8m0", which gives all of them, and the wgrad
+    operands' 128x1 columns, power-of-two scales (E8M0 values, the MXFP8
+    scale format at the blockwise granularity).  Its GEMMs then apply the
+    scales in the scaled MFMA: the packed-weight GEMMs run
+    ``smoe_grouped_gemm_fp8_packed_e8m0`` and the wgrad its E8M0 mode.
+
     Under autograd (grad mode on and an input or parameter requiring grad),
     ``forward`` records one graph node whose backward runs the fp8 backward
     (``loss.backward()`` fills w1.grad, w2.grad, w_gate.grad and x.grad).
@@ -114,12 +122,16 @@ class SimpleMoE(nn.Module):
 
     def __init__(self, hidden: int, intermediate: int, num_experts: int, top_k: int,
                  device=None, dtype=torch.bfloat16, router_bias: bool = False,
-                 wgrad_recipe: str = "fp32"):
+                 wgrad_recipe: str = "fp32", recipe: str = "blockwise"):
         super().__init__()
         if wgrad_recipe not in ("fp32", "e8m0"):
             raise ValueError("wgrad_recipe is 'fp32' (128x1 scales amax/448) or 'e8m0' "
                              "(power-of-two 128x1 scales applied by the scaled MFMA)")
+        if recipe not in ("blockwise", "e8m0"):
+            raise ValueError("recipe is 'blockwise' (scales amax/448) or 'e8m0' "
+                             "(power-of-two scales for every quantisation)")
         self.wgrad_recipe = wgrad_recipe
+        self.recipe = recipe
         self.hidden, self.intermediate = hidden, intermediate
         self.num_experts, self.top_k = num_experts, top_k
         kw = dict(device=device, dtype=dtype)
@@ -139,14 +151,24 @@ class SimpleMoE(nn.Module):
             p.copy_(torch.randn(p.shape, generator=generator, dtype=torch.float32,
                                 device=generator.device if generator is not None else p.device).to(p) * std)
 
+    @property
+    def _pow2(self) -> bool:
+        """Every quantisation takes power-of-two scales (recipe "e8m0")."""
+        return self.recipe == "e8m0"
+
+    @property
+    def _row_scale(self) -> str:
+        return "pow2" if self._pow2 else "amax"
+
     def _weights_key(self):
-        return (_OPT_STEPS[0],) + tuple((p.data_ptr(), p._version, tuple(p.shape))
+        return (_OPT_STEPS[0], self.recipe) + tuple((p.data_ptr(), p._version, tuple(p.shape))
                                         for p in (self.w1, self.w2))
 
     @torch.no_grad()
     def refresh_fp8_cache(self):
-        w1q, w1s = ops.quantize_weight_blockwise(self.w1.detach().to(torch.bfloat16).contiguous())
-        w2q, w2s = ops.quantize_weight_blockwise(self.w2.detach().to(torch.bfloat16).contiguous())
+        rs = self._row_scale
+        w1q, w1s = ops.quantize_weight_blockwise(self.w1.detach().to(torch.bfloat16).contiguous(), rs)
+        w2q, w2s = ops.quantize_weight_blockwise(self.w2.detach().to(torch.bfloat16).contiguous(), rs)
         self._fp8 = (w1q, w1s, w2q, w2s)
         self._fp8_key = self._weights_key()
         self._gemm = (self._for_gemm(w1q), w1s, self._for_gemm(w2q), w2s)
@@ -234,16 +256,18 @@ class SimpleMoE(nn.Module):
         # counted inside the router launch)
         idx, w, row_map, inv_map, counts, offsets = ops.route_topk_sort(logits, self.top_k,
                                                                         self.router_bias)
-        xq, xs = ops.permute_quant_rows(x, inv_map, self.top_k)
+        rs, e8 = self._row_scale, self._pow2
+        xq, xs = ops.permute_quant_rows(x, inv_map, self.top_k, scale=rs)
         if save:
             # the backward pass needs c1 and bf16 h, so fc1 and SwiGLU run
             # as two kernels here
-            c1 = ops.grouped_gemm_fp8(xq, xs, w1q, w1s, offsets)
-            hq, hs, h = ops.swiglu_quant(c1, save_h=True)
+            c1 = ops.grouped_gemm_fp8(xq, xs, w1q, w1s, offsets, e8m0=e8)
+            hq, hs, h = ops.swiglu_quant(c1, save_h=True, scale=rs)
         else:
             # inference: SwiGLU + requantisation run in the fc1 epilogue
-            hq, hs = ops.grouped_gemm_fp8_swiglu(xq, xs, w1q, w1s, offsets)
-        y = ops.grouped_gemm_fp8(hq, hs, w2q, w2s, offsets)
+            # (the e8m0 recipe runs its GEMM, then the SwiGLU kernel)
+            hq, hs = ops.grouped_gemm_fp8_swiglu(xq, xs, w1q, w1s, offsets, scale=rs)
+        y = ops.grouped_gemm_fp8(hq, hs, w2q, w2s, offsets, e8m0=e8)
         out = ops.unpermute_combine(y, inv_map, w)
         if save:
             return out, dict(x=x, logits=logits, topk_idx=idx, topk_w=w, row_map=row_map,
@@ -341,8 +365,9 @@ class SimpleMoE(nn.Module):
         # the main stream waits for the side stream before returning.
         main = torch.cuda.current_stream()
         side = self._side_stream(main.device)
-        cs = "pow2" if self.wgrad_recipe == "e8m0" else "fp32"
-        e8m0 = self.wgrad_recipe == "e8m0"
+        e8m0 = self.wgrad_recipe == "e8m0" or self._pow2
+        cs = "pow2" if e8m0 else "fp32"
+        rs, e8 = self._row_scale, self._pow2
         ones = torch.ones_like(inter["topk_w"])
         # the returned weight gradients are allocated on the caller's stream,
         # so the caching allocator never hands their memory to side-stream
@@ -361,20 +386,22 @@ class SimpleMoE(nn.Module):
         # combine backward fused with both quantisations of dy (1x128 rows for
         # dgrad, 128x1 columns for wgrad); dy itself is never stored
         dyq, dys, dyTq, dyTs, pad, ld, dw = ops.unpermute_combine_bwd_quant(
-            dout.contiguous(), inter["y"], inv, inter["row_map"], inter["topk_w"], off, col_scale=cs)
+            dout.contiguous(), inter["y"], inv, inter["row_map"], inter["topk_w"], off, col_scale=cs,
+            row_scale=rs)
         side.wait_stream(main)
         with torch.cuda.stream(side):
             ops.grouped_gemm_fp8_wgrad(dyTq, dyTs, hTq, hTs, pad, ld, out=dw2,
                                        accumulate=dw2_into is not None, e8m0=e8m0)
-        dh = ops.grouped_gemm_fp8(dyq, dys, w2tq, w2ts, off)
+        dh = ops.grouped_gemm_fp8(dyq, dys, w2tq, w2ts, off, e8m0=e8)
         # SwiGLU backward fused with both quantisations of dc1 (dc1 itself is
         # never stored)
-        dcq, dcs, dcTq, dcTs, _, _ = ops.swiglu_bwd_quant(inter["c1"], dh, off, col_scale=cs)
+        dcq, dcs, dcTq, dcTs, _, _ = ops.swiglu_bwd_quant(inter["c1"], dh, off, col_scale=cs,
+                                                          row_scale=rs)
         side.wait_stream(main)
         with torch.cuda.stream(side):
             ops.grouped_gemm_fp8_wgrad(dcTq, dcTs, xTq, xTs, pad, ld, out=dw1,
                                        accumulate=dw1_into is not None, e8m0=e8m0)
-        dxs = ops.grouped_gemm_fp8(dcq, dcs, w1tq, w1ts, off)
+        dxs = ops.grouped_gemm_fp8(dcq, dcs, w1tq, w1ts, off, e8m0=e8)
         dx = ops.unpermute_combine(dxs, inv, ones)
         # router: renormalisation + softmax backward into the logits
         dlogits = ops.router_topk_bwd(inter["logits"], inter["topk_idx"], dw)

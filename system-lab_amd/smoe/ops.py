@@ -21,6 +21,10 @@ FP8 = torch.float8_e4m3fn
 GROUP = 128
 # column-scale rules of the 128x1 (wgrad operand) quantisers, SMOE_COLSCALE_*
 COL_SCALES = {"fp32": 0, "pow2": 1}
+# scale rule of the row and weight quantisers (SMOE_SCALE_*): "amax" is
+# s = amax/448, "pow2" the least power of two >= amax/448 (E8M0 values)
+SCALES = {"amax": 0, "pow2": 1}
+ROWSCALE_POW2 = 2  # SMOE_ROWSCALE_POW2: the row-scale bit of the fused quantisers
 
 
 def pad128(d: int) -> int:
@@ -59,6 +63,12 @@ def _check(t: torch.Tensor, name: str, dtypes, ndim: int | None = None) -> None:
         raise ValueError(f"{name} must be {ndim}-D, got shape {tuple(t.shape)}")
     if not t.is_contiguous():
         raise ValueError(f"{name} must be contiguous")
+
+
+def _scale(scale: str) -> int:
+    if scale not in SCALES:
+        raise ValueError(f"scale must be one of {sorted(SCALES)}, got {scale!r}")
+    return SCALES[scale]
 
 
 def _bytes(t: torch.Tensor) -> torch.Tensor:
@@ -216,11 +226,13 @@ def route_topk_sort(logits: torch.Tensor, top_k: int, bias: torch.Tensor | None 
 
 
 # ---------------------------------------------------------------- dispatch
-def permute_quant_rows(x: torch.Tensor, inv_map: torch.Tensor, top_k: int):
+def permute_quant_rows(x: torch.Tensor, inv_map: torch.Tensor, top_k: int, scale: str = "amax"):
     """Quantise each token row of x [T,H] bf16 once (1x128 groups) and write it
     to the rows inv_map[t*K+k].  -> (xq [T*K,pad128(H)] fp8,
     xs [T*K,pad128(H)/128] f32).  H need only be a multiple of 16 (see
-    ``pad128``)."""
+    ``pad128``).  ``scale``: "amax" (s = amax/448) or "pow2" (power-of-two
+    scales, the E8M0 recipe)."""
+    mode = _scale(scale)
     _check(x, "x", (torch.bfloat16,), 2)
     _check(inv_map, "inv_map", (torch.int32,))
     T, H = x.shape
@@ -229,15 +241,21 @@ def permute_quant_rows(x: torch.Tensor, inv_map: torch.Tensor, top_k: int):
     R = T * top_k
     xq = torch.empty((R, pad128(H)), dtype=FP8, device=x.device)
     xs = torch.empty((R, nblocks(H)), dtype=torch.float32, device=x.device)
-    _C.call("smoe_permute_quant", _ptr(x), _ptr(inv_map), T, H, top_k, _ptr(xq), _ptr(xs),
-            _stream())
+    _C.call("smoe_permute_quant_ex", _ptr(x), _ptr(inv_map), T, H, top_k, _ptr(xq), _ptr(xs),
+            mode, _stream())
     return xq, xs
 
 
-def permute_quant(x: torch.Tensor, topk_idx: torch.Tensor, num_experts: int):
+def permute_quant(x: torch.Tensor, topk_idx: torch.Tensor, num_experts: int,
+                  scale: str = "amax"):
     """Dispatcher.permute fused with 1x128 fp8 quantisation
     (moe/MegatronCore_MoE_reading_notes.md:94-99, 498-501).
-    -> (xq, xs, row_map, inv_map, counts, offsets)."""
+    -> (xq, xs, row_map, inv_map, counts, offsets).  ``scale`` as for
+    ``permute_quant_rows``."""
+    if _scale(scale) != SCALES["amax"]:
+        row_map, inv_map, counts, offsets = route_sort(topk_idx, num_experts)
+        xq, xs = permute_quant_rows(x, inv_map, topk_idx.shape[1], scale)
+        return xq, xs, row_map, inv_map, counts, offsets
     _check(x, "x", (torch.bfloat16,), 2)
     _check(topk_idx, "topk_idx", (torch.int32,), 2)
     T, H = x.shape
@@ -260,17 +278,20 @@ def permute_quant(x: torch.Tensor, topk_idx: torch.Tensor, num_experts: int):
 
 
 # ----------------------------------------------------------------- weights
-def quantize_weight_blockwise(w: torch.Tensor):
+def quantize_weight_blockwise(w: torch.Tensor, scale: str = "amax"):
     """128x128 blockwise fp8 weights.  w [E,N,K] bf16 ("NK" layout,
     summary/fp8_expert_gemm_optimization.md:137) -> (wq [E,N,pad128(K)] fp8,
     ws [E,ceil(N/128),pad128(K)/128] f32).  N and K that are not multiples
     of 128 (multiples of 16) end in partial blocks, quantised as the
-    zero-padded block; wq's padding columns are 0."""
+    zero-padded block; wq's padding columns are 0.  ``scale`` as for
+    ``permute_quant_rows``."""
+    mode = _scale(scale)
     _check(w, "w", (torch.bfloat16,), 3)
     E, N, Kd = w.shape
     wq = torch.empty((E, N, pad128(Kd)), dtype=FP8, device=w.device)
     ws = torch.empty((E, nblocks(N), nblocks(Kd)), dtype=torch.float32, device=w.device)
-    _C.call("smoe_quantize_weight_blockwise", _ptr(w), E, N, Kd, _ptr(wq), _ptr(ws), _stream())
+    _C.call("smoe_quantize_weight_blockwise_ex", _ptr(w), E, N, Kd, _ptr(wq), _ptr(ws), mode,
+            _stream())
     return wq, ws
 
 
@@ -331,7 +352,8 @@ def _weight(wq, name):
 
 
 def grouped_gemm_fp8(xq: torch.Tensor, xs: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor,
-                     offsets: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+                     offsets: torch.Tensor, out: torch.Tensor | None = None,
+                     e8m0: bool = False) -> torch.Tensor:
     """Dropless fp8 grouped GEMM: rows [offsets[e], offsets[e+1]) of xq times
     W[e]^T with 1x128 / 128x128 scales -> bf16 [R, N].  Rows outside
     [offsets[0], offsets[E]) are not written.  ``wq`` is [E, N, K] fp8, or a
@@ -339,7 +361,12 @@ def grouped_gemm_fp8(xq: torch.Tensor, xs: torch.Tensor, wq: torch.Tensor, ws: t
     kernel orders each 128-wide K block's products differently inside the
     MFMA: the bytes are the same whenever those products sum exactly in fp32
     (every benchmark and layer workload), else they can differ in the last
-    bf16 bit, within the GEMM tolerance."""
+    bf16 bit, within the GEMM tolerance.  ``e8m0``: every scale is a power
+    of two (the "pow2" quantisers); a PackedWeight then runs the kernel that
+    applies the scales in the MFMA (smoe_grouped_gemm_fp8_packed_e8m0),
+    whose sums can differ from the packed kernel's in the last bf16 bit.
+    Plain weights run the plain kernel either way (its arithmetic is exact
+    for any scale)."""
     _check(xq, "xq", (FP8, torch.uint8))
     wt, packed = _weight(wq, "wq")
     _check(xs, "xs", (torch.float32,), 2)
@@ -365,8 +392,9 @@ def grouped_gemm_fp8(xq: torch.Tensor, xs: torch.Tensor, wq: torch.Tensor, ws: t
         if out.shape != (R, N):
             raise ValueError("out must be [R, N]")
     if packed:
-        _C.call("smoe_grouped_gemm_fp8_packed", _ptr(_bytes(xq)), _ptr(xs), _ptr(wt), _ptr(ws),
-                _ptr(offsets), E, R, N, Kd, _ptr(out), _stream())
+        fn = "smoe_grouped_gemm_fp8_packed_e8m0" if e8m0 else "smoe_grouped_gemm_fp8_packed"
+        _C.call(fn, _ptr(_bytes(xq)), _ptr(xs), _ptr(wt), _ptr(ws), _ptr(offsets), E, R, N, Kd,
+                _ptr(out), _stream())
     else:
         _C.call("smoe_grouped_gemm_fp8", _ptr(_bytes(xq)), _ptr(xs), _ptr(_bytes(wt)), _ptr(ws),
                 _ptr(offsets), E, R, N, Kd, _ptr(out), None, 0, _stream())
@@ -374,12 +402,19 @@ def grouped_gemm_fp8(xq: torch.Tensor, xs: torch.Tensor, wq: torch.Tensor, ws: t
 
 
 def grouped_gemm_fp8_swiglu(xq: torch.Tensor, xs: torch.Tensor, w1q: torch.Tensor,
-                            w1s: torch.Tensor, offsets: torch.Tensor, save_c1: bool = False):
+                            w1s: torch.Tensor, offsets: torch.Tensor, save_c1: bool = False,
+                            scale: str = "amax"):
     """fc1 GEMM with SwiGLU + 1x128 requantisation fused into the epilogue.
     Same bytes as ``swiglu_quant(grouped_gemm_fp8(xq, xs, w1q, w1s, offsets))``;
     returns (hq [R,I] fp8, hs [R,I/128] f32), plus c1 [R,2I] bf16 when
     ``save_c1``.  Rows outside [offsets[0], offsets[E]) are not written.
-    ``w1q`` may be a PackedWeight (see grouped_gemm_fp8)."""
+    ``w1q`` may be a PackedWeight (see grouped_gemm_fp8).  ``scale="pow2"``
+    (the E8M0 recipe: power-of-two operand scales in, power-of-two hs out)
+    runs ``grouped_gemm_fp8(..., e8m0=True)`` and then ``swiglu_quant``."""
+    if _scale(scale) != SCALES["amax"]:
+        c1 = grouped_gemm_fp8(xq, xs, w1q, w1s, offsets, e8m0=True)
+        hq, hs = swiglu_quant(c1, scale=scale)
+        return (hq, hs, c1) if save_c1 else (hq, hs)
     _check(xq, "xq", (FP8, torch.uint8))
     wt, packed = _weight(w1q, "w1q")
     _check(xs, "xs", (torch.float32,), 2)
@@ -416,11 +451,12 @@ def grouped_gemm_fp8_swiglu(xq: torch.Tensor, xs: torch.Tensor, w1q: torch.Tenso
 
 
 # ------------------------------------------------------------------ SwiGLU
-def swiglu_quant(c1: torch.Tensor, save_h: bool = False):
+def swiglu_quant(c1: torch.Tensor, save_h: bool = False, scale: str = "amax"):
     """h = silu(gate)*up (gate = columns [0,I), up = [I,2I)) requantised 1x128.
     c1 [R,2I] bf16 -> (hq [R,pad128(I)] fp8, hs [R,pad128(I)/128] f32), plus
     h as bf16 [R,I] when ``save_h`` (the fc2 wgrad operand for the backward
-    pass)."""
+    pass).  ``scale`` as for ``permute_quant_rows``."""
+    mode = _scale(scale)
     _check(c1, "c1", (torch.bfloat16,), 2)
     R, I2 = c1.shape
     if I2 % 2:
@@ -429,7 +465,7 @@ def swiglu_quant(c1: torch.Tensor, save_h: bool = False):
     hq = torch.empty((R, pad128(I)), dtype=FP8, device=c1.device)
     hs = torch.empty((R, nblocks(I)), dtype=torch.float32, device=c1.device)
     h = torch.empty((R, I), dtype=torch.bfloat16, device=c1.device) if save_h else None
-    _C.call("smoe_swiglu_quant_h", _ptr(c1), R, I, _ptr(hq), _ptr(hs), _ptr(h), _stream())
+    _C.call("smoe_swiglu_quant_ex", _ptr(c1), R, I, _ptr(hq), _ptr(hs), _ptr(h), mode, _stream())
     return (hq, hs, h) if save_h else (hq, hs)
 
 
@@ -457,14 +493,16 @@ def unpermute_combine(y: torch.Tensor, inv_map: torch.Tensor, topk_w: torch.Tens
 
 
 # ---------------------------------------------------------------- backward
-def quant_rows(x: torch.Tensor):
+def quant_rows(x: torch.Tensor, scale: str = "amax"):
     """1x128 row quantisation without permutation: x [M,C] bf16 ->
-    (q [M,pad128(C)] fp8, s [M,pad128(C)/128] f32)."""
+    (q [M,pad128(C)] fp8, s [M,pad128(C)/128] f32).  ``scale`` as for
+    ``permute_quant_rows``."""
+    mode = _scale(scale)
     _check(x, "x", (torch.bfloat16,), 2)
     M, C = x.shape
     q = torch.empty((M, pad128(C)), dtype=FP8, device=x.device)
     s = torch.empty((M, nblocks(C)), dtype=torch.float32, device=x.device)
-    _C.call("smoe_quant_rows_1x128", _ptr(x), M, C, _ptr(q), _ptr(s), _stream())
+    _C.call("smoe_quant_rows_1x128_ex", _ptr(x), M, C, _ptr(q), _ptr(s), mode, _stream())
     return q, s
 
 
@@ -527,12 +565,19 @@ def quant_cols(x: torch.Tensor, offsets: torch.Tensor, gather: torch.Tensor | No
     return xTq, xTs, pad, ld
 
 
-def quant_rows_cols(x: torch.Tensor, offsets: torch.Tensor, col_scale: str = "fp32"):
+def _fused_scale(col_scale: str, row_scale: str) -> int:
+    return _col_scale(col_scale) | (ROWSCALE_POW2 if _scale(row_scale) else 0)
+
+
+def quant_rows_cols(x: torch.Tensor, offsets: torch.Tensor, col_scale: str = "fp32",
+                    row_scale: str = "amax"):
     """Both quantisations of x [R,C] bf16 from one read: the 1x128 rows of
     ``quant_rows`` and the transposed 128x1 columns of ``quant_cols`` over
     the expert segments ``offsets`` (which must cover all R rows).
     -> (xq [R,pad128(C)] fp8, xs [R,pad128(C)/128], xTq [C,ld] fp8,
-    xTs [C,ld/128], pad, ld)."""
+    xTs [C,ld/128], pad, ld).  ``col_scale`` ("fp32" | "pow2") rules the
+    column scales, ``row_scale`` ("amax" | "pow2") the row scales."""
+    mode = _fused_scale(col_scale, row_scale)
     _check(x, "x", (torch.bfloat16,), 2)
     _check(offsets, "offsets", (torch.int32,), 1)
     R, C = x.shape
@@ -544,17 +589,18 @@ def quant_rows_cols(x: torch.Tensor, offsets: torch.Tensor, col_scale: str = "fp
     xTs = torch.empty((C, ld // GROUP), dtype=torch.float32, device=x.device)
     pad = torch.empty(E + 1, dtype=torch.int32, device=x.device)
     _C.call("smoe_quant_rows_cols", _ptr(x), R, C, _ptr(offsets), E, ld, _ptr(xq), _ptr(xs),
-            _ptr(xTq), _ptr(xTs), _ptr(pad), _col_scale(col_scale), _stream())
+            _ptr(xTq), _ptr(xTs), _ptr(pad), mode, _stream())
     return xq, xs, xTq, xTs, pad, ld
 
 
 def swiglu_bwd_quant(c1: torch.Tensor, dh: torch.Tensor, offsets: torch.Tensor,
-                     save_dc1: bool = False, col_scale: str = "fp32"):
+                     save_dc1: bool = False, col_scale: str = "fp32", row_scale: str = "amax"):
     """SwiGLU backward fused with both quantisations of its output: the
     bytes of ``quant_rows_cols(swiglu_bwd(c1, dh), offsets)`` without
     storing dc1 (returned as the last element when ``save_dc1``).
     c1 [R,2I], dh [R,I] bf16 -> (dcq [R,2I] fp8, dcs, dcTq [2I,ld] fp8, dcTs,
-    pad, ld[, dc1])."""
+    pad, ld[, dc1]).  Scale rules as for ``quant_rows_cols``."""
+    mode = _fused_scale(col_scale, row_scale)
     _check(c1, "c1", (torch.bfloat16,), 2)
     _check(dh, "dh", (torch.bfloat16,), 2)
     _check(offsets, "offsets", (torch.int32,), 1)
@@ -570,7 +616,7 @@ def swiglu_bwd_quant(c1: torch.Tensor, dh: torch.Tensor, offsets: torch.Tensor,
         # a multiple of 128, which the fused kernel's column slabs assume: the
         # same bytes from the SwiGLU backward kernel and the one-read quantiser
         dc1 = swiglu_bwd(c1, dh)
-        out = quant_rows_cols(dc1, offsets, col_scale=col_scale)
+        out = quant_rows_cols(dc1, offsets, col_scale=col_scale, row_scale=row_scale)
         return out + (dc1,) if save_dc1 else out
     dcq = torch.empty((R, N), dtype=FP8, device=dev)
     dcs = torch.empty((R, N // GROUP), dtype=torch.float32, device=dev)
@@ -579,7 +625,7 @@ def swiglu_bwd_quant(c1: torch.Tensor, dh: torch.Tensor, offsets: torch.Tensor,
     pad = torch.empty(E + 1, dtype=torch.int32, device=dev)
     dc1 = torch.empty((R, N), dtype=torch.bfloat16, device=dev) if save_dc1 else None
     _C.call("smoe_swiglu_bwd_quant", _ptr(c1), _ptr(dh), R, I, _ptr(offsets), E, ld, _ptr(dcq),
-            _ptr(dcs), _ptr(dcTq), _ptr(dcTs), _ptr(pad), _ptr(dc1), _col_scale(col_scale), _stream())
+            _ptr(dcs), _ptr(dcTq), _ptr(dcTs), _ptr(pad), _ptr(dc1), mode, _stream())
     out = (dcq, dcs, dcTq, dcTs, pad, ld)
     return out + (dc1,) if save_dc1 else out
 
@@ -660,11 +706,13 @@ def unpermute_combine_bwd(dout: torch.Tensor, y: torch.Tensor, inv_map: torch.Te
 
 def unpermute_combine_bwd_quant(dout: torch.Tensor, y: torch.Tensor, inv_map: torch.Tensor,
                                 row_map: torch.Tensor, topk_w: torch.Tensor,
-                                offsets: torch.Tensor, col_scale: str = "fp32"):
+                                offsets: torch.Tensor, col_scale: str = "fp32",
+                                row_scale: str = "amax"):
     """Combine backward fused with both quantisations of dy: the bytes of
-    ``quant_rows_cols(unpermute_combine_bwd(...)[0], offsets, col_scale)`` and
-    dw, without storing dy.  -> (dyq [T*K,pad128(H)] fp8, dys, dyTq [H,ld] fp8,
-    dyTs, pad, ld, dw [T,K] f32)."""
+    ``quant_rows_cols(unpermute_combine_bwd(...)[0], offsets, col_scale,
+    row_scale)`` and dw, without storing dy.  -> (dyq [T*K,pad128(H)] fp8,
+    dys, dyTq [H,ld] fp8, dyTs, pad, ld, dw [T,K] f32)."""
+    mode = _fused_scale(col_scale, row_scale)
     _check(dout, "dout", (torch.bfloat16,), 2)
     _check(y, "y", (torch.bfloat16,), 2)
     _check(inv_map, "inv_map", (torch.int32,))
@@ -689,5 +737,5 @@ def unpermute_combine_bwd_quant(dout: torch.Tensor, y: torch.Tensor, inv_map: to
     dw = torch.empty((T, K), dtype=torch.float32, device=dev)
     _C.call("smoe_unpermute_combine_bwd_quant", _ptr(dout), _ptr(y), _ptr(inv_map),
             _ptr(row_map), _ptr(topk_w), T, K, H, _ptr(offsets), E, ld, _ptr(dyq), _ptr(dys),
-            _ptr(dyTq), _ptr(dyTs), _ptr(pad), _ptr(dw), _col_scale(col_scale), _stream())
+            _ptr(dyTq), _ptr(dyTs), _ptr(pad), _ptr(dw), mode, _stream())
     return dyq, dys, dyTq, dyTs, pad, ld, dw

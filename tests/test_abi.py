@@ -198,3 +198,40 @@ def test_wgrad_ex_and_packed_bounds_reject():
     assert p(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 256, 128, K, FAKE, None) == -2
     assert ops.packed_gemm_ok(128, 65536)
     assert not ops.packed_gemm_ok(128, 0) and not ops.packed_gemm_ok(128, 1536 + 128)
+
+
+def test_scale_mode_entries_reject():
+    """The _ex quantisers take SMOE_SCALE_AMAX (0) or SMOE_SCALE_POW2 (1) and
+    nothing else; the column quantiser takes only the column bit, the fused
+    row-and-column quantisers also the row bit (2); the E8M0 GEMM has the
+    packed GEMM's shape checks.  All rejected before any launch."""
+    lib = _C.lib()
+    for mode in (2, -1):
+        assert lib.smoe_permute_quant_ex(FAKE, FAKE, 4, 256, 2, FAKE, FAKE, mode, None) == -8
+        assert lib.smoe_quant_rows_1x128_ex(FAKE, 4, 256, FAKE, FAKE, mode, None) == -8
+        assert lib.smoe_swiglu_quant_ex(FAKE, 4, 256, FAKE, FAKE, None, mode, None) == -8
+        assert lib.smoe_quantize_weight_blockwise_ex(FAKE, 2, 256, 256, FAKE, FAKE, mode, None) == -8
+    # the other checks still come first for a valid mode
+    assert lib.smoe_permute_quant_ex(None, FAKE, 4, 256, 2, FAKE, FAKE, 1, None) == -1
+    assert lib.smoe_quant_rows_1x128_ex(FAKE, 4, 200, FAKE, FAKE, 1, None) == -3
+    assert lib.smoe_swiglu_quant_ex(FAKE, 4, 256, FAKE, FAKE, MIS + 8, 1, None) == -6
+    assert lib.smoe_quantize_weight_blockwise_ex(FAKE, 0, 256, 256, FAKE, FAKE, 1, None) == -4
+    ld = lib.smoe_quant_cols_ld(256, 2)
+    assert lib.smoe_quant_cols_128x1(FAKE, None, 1, 256, 256, FAKE, 2, ld, FAKE, FAKE, FAKE, 2,
+                                     None) == -8
+    assert lib.smoe_quant_rows_cols(FAKE, 256, 256, FAKE, 2, ld, FAKE, FAKE, FAKE, FAKE, FAKE, 4,
+                                    None) == -8
+    assert lib.smoe_quant_rows_cols(None, 256, 256, FAKE, 2, ld, FAKE, FAKE, FAKE, FAKE, FAKE, 3,
+                                    None) == -1
+    assert lib.smoe_swiglu_bwd_quant(FAKE, FAKE, 256, 128, FAKE, 2, ld, FAKE, FAKE, FAKE, FAKE,
+                                     FAKE, None, 7, None) == -8
+    assert lib.smoe_unpermute_combine_bwd_quant(FAKE, FAKE, FAKE, FAKE, FAKE, 128, 2, 256, FAKE,
+                                                2, ld, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, -2,
+                                                None) == -8
+    g = lib.smoe_grouped_gemm_fp8_packed_e8m0
+    assert g(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 256, 128, 640, FAKE, None) == -3   # K % 512
+    assert g(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 256, 120, 1024, FAKE, None) == -3  # N % 16
+    assert g(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 256, 128, 65536 + 512, FAKE, None) == -2
+    assert g(FAKE, FAKE, FAKE, FAKE, FAKE, 0, 256, 128, 1024, FAKE, None) == -4
+    assert g(FAKE, None, FAKE, FAKE, FAKE, 2, 256, 128, 1024, FAKE, None) == -1
+    assert g(FAKE, FAKE + 2, FAKE, FAKE, FAKE, 2, 256, 128, 1024, FAKE, None) == -6

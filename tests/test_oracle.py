@@ -278,6 +278,29 @@ def test_group_scale_pow2_closed_forms():
     assert (sc >= s3).all() and (sc < 2 * s3).all()
 
 
+def test_pow2_weight_and_swiglu_quantisers():
+    """C10 on weight blocks and on SwiGLU's h: every scale a power of two in
+    [s_C3, 2 s_C3), the bytes torch's e4m3 cast of x * 2^-e (exact, no clamp
+    needed), and a short last block (C9) still the zero-padded block."""
+    rng = np.random.default_rng(12)
+    w = O.f32_to_bf16((rng.standard_normal((2, 200, 272)) * np.exp2(rng.integers(-9, 9, (2, 1, 1))))
+                      .astype(np.float32))
+    q, s = O.quantize_weight_blockwise(w, pow2=True)
+    _, s3 = O.quantize_weight_blockwise(w)
+    assert (np.frexp(s)[0] == 0.5).all() and (s >= s3).all() and (s < 2 * s3).all()
+    wf = np.pad(O.bf16_to_f32(w), ((0, 0), (0, 56), (0, 112)))
+    y = wf.reshape(2, 2, 128, 3, 128) / s[:, :, None, :, None]
+    assert np.abs(y).max() <= 448
+    assert np.array_equal(q, _torch_e4m3(y.reshape(2, 256, 384))[:, :200])
+    c1 = O.f32_to_bf16((rng.standard_normal((33, 2 * 144)) * 4).astype(np.float32))
+    hq, hs = O.swiglu_quant(c1, pow2=True)
+    cf = O.bf16_to_f32(c1)
+    h = (O.silu_f32(cf[:, :144]) * cf[:, 144:]).astype(np.float32)
+    rq, rs = O.quant_1x128(h, pow2=True)
+    assert np.array_equal(hq, rq) and np.array_equal(hs, rs)
+    assert (np.frexp(hs)[0] == 0.5).all()
+
+
 def test_pow2_wgrad_operands_as_accurate_as_c3():
     """The opt-in E8M0 recipe loses no accuracy: a weight gradient from
     power-of-two 128x1 operands is as close to the exact product of the bf16
