@@ -710,8 +710,9 @@ def _grouped_fc_fwd_bwd(dev, hid, steps, warmup, e8m0=False):
         dyv = (W.tokens(R, N, device=dev, seed=32).float() * 1e-2).to(torch.bfloat16)
         wq, ws = ops.quantize_weight_blockwise(W.weights(E, N, Kd, device=dev), scale=rs)
         wtq, wts = ops.transpose_blockwise(wq, ws, k=Kd)
-        wf = ops.pack_weight_fp8(wq) if ops.packed_gemm_ok(N, wq.shape[2]) else wq
-        wtf = ops.pack_weight_fp8(wtq) if ops.packed_gemm_ok(Kd, wtq.shape[2]) else wtq
+        ok = ops.packed_e8m0_ok if e8m0 else ops.packed_gemm_ok
+        wf = ops.pack_weight_fp8(wq) if ok(N, wq.shape[2]) else wq
+        wtf = ops.pack_weight_fp8(wtq) if ok(Kd, wtq.shape[2]) else wtq
         y = torch.empty((R, N), dtype=torch.bfloat16, device=dev)
         da = torch.empty((R, Kd), dtype=torch.bfloat16, device=dev)
         dw = torch.empty((E, N, Kd), dtype=torch.float32, device=dev)

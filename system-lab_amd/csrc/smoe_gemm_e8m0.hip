@@ -27,8 +27,8 @@
 // 1.53-1.58 ms against 1.77 ms for smoe_gemm_packed.hip, fc2 (N 7168, K 2048)
 // 0.92-0.96 against 1.03-1.05 ms; bytes identical.
 //
-// Scope: K a multiple of 512, every scale a power of two (or zero-exponent
-// data that is never read); the ops layer checks the recipe.
+// Scope: K a multiple of 128 from 512 to 65536 (K blocks 4 .. 512), every
+// scale a power of two; the ops layer checks the recipe.
 #include "smoe_mfma.h"
 
 namespace smoe {
@@ -178,39 +178,52 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_fp8_e8m0_kernel(
       oa[j] = (uint32_t)(min(row, rows - 1) * Kd + ((slot ^ (row & 7)) << 4));
     }
   }
-  // scale chunk DMA h of wave w: lane l moves 16 bytes (4 K steps) of tile
-  // row (w*2+h)*32 + l/2 (the second half of a chunk past ksb re-reads the first)
+  // Activation scales travel in chunks of 8 K steps, 32 bytes per tile row:
+  // scale DMA h of wave w moves tile rows (w*2+h)*32 + l/2, lane l the 16
+  // bytes of half l%2.  Chunk c holds the 8 steps from sc_win(c): 8c, except
+  // the last chunk, whose window ends at ksb (so no DMA reads past a row's
+  // ksb scales).  With 4 <= ksb < 8 the one chunk's halves hold steps 0..3
+  // and ksb-4..ksb-1.  sc_slot maps step kb to its position in its chunk.
   uint32_t osc[kSCDma];
 #pragma unroll
   for (int h = 0; h < kSCDma; ++h)
     osc[h] = (uint32_t)(min((wid * kSCDma + h) * 32 + (lane >> 1), rows - 1) * ksb) * 4u;
+  auto sc_win = [&](int chunk) { return ksb >= kSChunk ? min(chunk * kSChunk, ksb - kSChunk) : 0; };
+  auto sc_src = [&](int chunk) -> uint32_t {  // this lane's first step, in bytes
+    const int half = lane & 1;
+    const int st = ksb >= kSChunk ? sc_win(chunk) + 4 * half : (half ? ksb - 4 : 0);
+    return (uint32_t)st * 4u;
+  };
+  auto sc_slot = [&](int kb) {
+    return ksb >= kSChunk ? kb - sc_win(kb / kSChunk) : (kb < 4 ? kb : kb + kSChunk - ksb);
+  };
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_ptr_t)smem;
   const uint32_t a_lds = __builtin_amdgcn_readfirstlane(lds0 + wid * kSegs * 1024);
   const uint32_t sc_lds = __builtin_amdgcn_readfirstlane(lds0 + kSC0 + wid * kSCDma * 1024);
   auto issue_sc = [&](int chunk) __attribute__((always_inline)) {
-    const bool second = (lane & 1) && (chunk + 1) * kSChunk <= ksb;
+    const uint32_t src = sc_src(chunk);
 #pragma unroll
     for (int h = 0; h < kSCDma; ++h)
-      dma16(s_base + chunk * kSChunk, osc[h] + (second ? 16u : 0u),
-            sc_lds + (chunk & 1) * kSCBytes + h * 1024);
+      dma16(s_base, osc[h] + src, sc_lds + (chunk & 1) * kSCBytes + h * 1024);
   };
   // The same DMAs issued only when the wave-uniform go is nonzero, with the
   // branch inside one asm statement: a branch the compiler sees in the K loop
   // makes it split the accumulators' live ranges around it.
   auto issue_sc_if = [&](int chunk, int go) __attribute__((always_inline)) {
-    const bool second = (lane & 1) && (chunk + 1) * kSChunk <= ksb;
-    const float* src = s_base + chunk * kSChunk;
+    const uint32_t src = sc_src(chunk);
     const uint32_t dst = sc_lds + (chunk & 1) * kSCBytes;
+    // go is wave-uniform; compared per lane, so that it may sit in either
+    // register file
     asm volatile(
-        "s_cmp_eq_u32 %4, 0\n\t"
-        "s_cbranch_scc1 1f\n\t"
+        "v_cmp_eq_u32 vcc, 0, %4\n\t"
+        "s_cbranch_vccnz 1f\n\t"
         "s_mov_b32 m0, %0\n\t"
         "global_load_lds_dwordx4 %2, %3\n\t"
         "s_mov_b32 m0, %1\n\t"
         "global_load_lds_dwordx4 %5, %3\n\t"
-        "1:" ::"s"(dst), "s"(dst + 1024), "v"(osc[0] + (second ? 16u : 0u)), "s"(src),
-        "s"(go), "v"(osc[1] + (second ? 16u : 0u))
-        : "memory", "scc");
+        "1:" ::"s"(dst), "s"(dst + 1024), "v"(osc[0] + src), "s"(s_base), "v"(go),
+        "v"(osc[1] + src)
+        : "memory", "vcc");
   };
   // ---- packed weights: wave w's four 16-row blocks of weight rows
   const uint8_t* b_base = bp + (size_t)e * ((size_t)N * Kd);
@@ -286,8 +299,7 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_fp8_e8m0_kernel(
     const uint8_t* a_src = a_base + (size_t)ka * kBK;
     const uint8_t* b_src = b_base + (size_t)min(kb + 3, ksb - 1) * 2048;
     const uint8_t* sA = smem + (kb % kAS) * kABytes;
-    const float* sC = (const float*)(smem + kSC0 + ((kb / kSChunk) & 1) * kSCBytes) +
-                      (kb & (kSChunk - 1));
+    const float* sC = (const float*)(smem + kSC0 + ((kb / kSChunk) & 1) * kSCBytes) + sc_slot(kb);
     const int ew = e8m0_of(sb_row[kb]);
     v8i fw[kCB];
 #pragma unroll
@@ -296,8 +308,7 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_fp8_e8m0_kernel(
     asm volatile("" : "+v"(fw[0]), "+v"(fw[1]), "+v"(fw[2]), "+v"(fw[3]));
     // the next scale chunk, after the compiler's wait for cur (which does
     // not count it)
-    issue_sc_if(kb / kSChunk + 1,
-                __builtin_amdgcn_readfirstlane((kb & (kSChunk - 1)) == 0 && kb + kSChunk < ksb));
+    issue_sc_if(kb / kSChunk + 1, (kb & (kSChunk - 1)) == 0 && kb + kSChunk < ksb);
     v8i fx = lds_frag_p(sA, frow, fg);
     int ex = e8m0_of(sC[frow * kSChunk]);
 #pragma unroll
@@ -383,8 +394,8 @@ extern "C" int smoe_grouped_gemm_fp8_packed_e8m0(const uint8_t* a, const float* 
                                                  int Kdim, uint16_t* c, void* stream) {
   if (R <= 0 || N <= 0 || Kdim <= 0) return SMOE_EINVAL_DIM;
   if (E <= 0 || E > SMOE_MAX_EXPERTS) return SMOE_EINVAL_EXPERTS;
-  if (N % kLane || Kdim % (4 * kBK)) return SMOE_EINVAL_ALIGN128;
-  if (Kdim > 65536) return SMOE_EINVAL_DIM;
+  if (N % kLane || Kdim % kBK) return SMOE_EINVAL_ALIGN128;
+  if (Kdim < 4 * kBK || Kdim > 65536) return SMOE_EINVAL_DIM;  // 4 .. 512 K steps
   if ((long long)N * Kdim >= (1LL << 32)) return SMOE_EINVAL_DIM;
   SMOE_CHECK_PTR(a);
   SMOE_CHECK_PTR(wp);

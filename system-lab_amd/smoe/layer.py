@@ -175,13 +175,14 @@ class SimpleMoE(nn.Module):
         self._gemm_t = None
         return self._fp8
 
-    @staticmethod
-    def _for_gemm(wq):
+    def _for_gemm(self, wq):
         """The form the GEMM ops take: packed in MFMA fragment order where the
-        register-loaded kernel covers the shape (K a multiple of 512; the same
-        bytes out, faster), else the plain [E, N, K] weights."""
+        register-loaded kernel covers the shape (K a multiple of 512, or for
+        the E8M0 recipe of 128 from 512 up; the same bytes out, faster), else
+        the plain [E, N, K] weights."""
         E, N, Kd = wq.shape
-        return ops.pack_weight_fp8(wq) if ops.packed_gemm_ok(N, Kd) else wq
+        ok = ops.packed_e8m0_ok if self._pow2 else ops.packed_gemm_ok
+        return ops.pack_weight_fp8(wq) if ok(N, Kd) else wq
 
     def fp8_weights(self):
         """(w1q, w1s, w2q, w2s), re-quantised when w1 or w2 changed since the

@@ -329,14 +329,23 @@ def packed_gemm_ok(N: int, Kd: int) -> bool:
             and N * Kd < (1 << 32))
 
 
+def packed_e8m0_ok(N: int, Kd: int) -> bool:
+    """Whether the E8M0 GEMM (smoe_grouped_gemm_fp8_packed_e8m0) covers a
+    packed weight of N rows and K = Kd: K a multiple of 128 from 512 to
+    65536, N % 16 == 0 and N*K < 2^32 (the C entry point's checks)."""
+    return (Kd % GROUP == 0 and 4 * GROUP <= Kd <= PACKED_MAX_K and N % 16 == 0
+            and N * Kd < (1 << 32))
+
+
 def pack_weight_fp8(wq: torch.Tensor) -> PackedWeight:
     """[E, N, K] fp8 weights -> PackedWeight (smoe_pack_weight_fp8).  Raises
-    unless ``packed_gemm_ok(N, K)``."""
+    unless ``packed_gemm_ok(N, K)`` or ``packed_e8m0_ok(N, K)`` (a weight only
+    the E8M0 GEMM covers can only be used with ``e8m0=True``)."""
     _check(wq, "wq", (FP8, torch.uint8), 3)
     E, N, Kd = wq.shape
-    if not packed_gemm_ok(N, Kd):
-        raise ValueError(f"packed weights need K % 512 == 0, K <= {PACKED_MAX_K}, N % 16 == 0 "
-                         f"and N*K < 2^32 (N={N}, K={Kd})")
+    if not (packed_gemm_ok(N, Kd) or packed_e8m0_ok(N, Kd)):
+        raise ValueError(f"packed weights need K % 128 == 0, 512 <= K <= {PACKED_MAX_K}, "
+                         f"N % 16 == 0 and N*K < 2^32 (N={N}, K={Kd})")
     wp = torch.empty((E, N, Kd), dtype=torch.uint8, device=wq.device)
     _C.call("smoe_pack_weight_fp8", _ptr(_bytes(wq)), E, N, Kd, _ptr(wp), _stream())
     return PackedWeight(wp)
@@ -376,9 +385,9 @@ def grouped_gemm_fp8(xq: torch.Tensor, xs: torch.Tensor, wq: torch.Tensor, ws: t
     E, N, Kw = wt.shape
     if Kw != Kd:
         raise ValueError(f"K mismatch: xq has {Kd}, wq has {Kw}")
-    if packed and not packed_gemm_ok(N, Kd):
-        raise ValueError(f"packed weights need K % 512 == 0, K <= {PACKED_MAX_K} and N*K < 2^32 "
-                         f"(N={N}, K={Kd})")
+    if packed and not (packed_e8m0_ok(N, Kd) if e8m0 else packed_gemm_ok(N, Kd)):
+        raise ValueError(f"packed weights need K % 512 == 0 (K % 128 == 0 and K >= 512 with "
+                         f"e8m0), K <= {PACKED_MAX_K} and N*K < 2^32 (N={N}, K={Kd})")
     if offsets.numel() != E + 1:
         raise ValueError("offsets must have E+1 entries")
     if Kd % GROUP:

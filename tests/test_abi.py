@@ -203,8 +203,13 @@ def test_wgrad_ex_and_packed_bounds_reject():
 def test_scale_mode_entries_reject():
     """The _ex quantisers take SMOE_SCALE_AMAX (0) or SMOE_SCALE_POW2 (1) and
     nothing else; the column quantiser takes only the column bit, the fused
-    row-and-column quantisers also the row bit (2); the E8M0 GEMM has the
-    packed GEMM's shape checks.  All rejected before any launch."""
+    row-and-column quantisers also the row bit (2); the E8M0 GEMM takes K a
+    multiple of 128 from 512 to 65536 (ops.packed_e8m0_ok says the same).
+    All rejected before any launch."""
+    from smoe import ops
+    assert ops.packed_e8m0_ok(128, 640) and ops.packed_e8m0_ok(128, 65536)
+    assert not ops.packed_e8m0_ok(128, 384) and not ops.packed_e8m0_ok(128, 576)
+    assert not ops.packed_e8m0_ok(120, 1024) and not ops.packed_e8m0_ok(128, 65536 + 128)
     lib = _C.lib()
     for mode in (2, -1):
         assert lib.smoe_permute_quant_ex(FAKE, FAKE, 4, 256, 2, FAKE, FAKE, mode, None) == -8
@@ -229,7 +234,8 @@ def test_scale_mode_entries_reject():
                                                 2, ld, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, -2,
                                                 None) == -8
     g = lib.smoe_grouped_gemm_fp8_packed_e8m0
-    assert g(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 256, 128, 640, FAKE, None) == -3   # K % 512
+    assert g(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 256, 128, 576, FAKE, None) == -3   # K % 128
+    assert g(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 256, 128, 384, FAKE, None) == -2   # K < 512
     assert g(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 256, 120, 1024, FAKE, None) == -3  # N % 16
     assert g(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 256, 128, 65536 + 512, FAKE, None) == -2
     assert g(FAKE, FAKE, FAKE, FAKE, FAKE, 0, 256, 128, 1024, FAKE, None) == -4

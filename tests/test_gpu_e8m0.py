@@ -324,12 +324,13 @@ def _pow2_gemm_operands(dev, counts, N, Kd, seed):
 
 
 def _check_e8m0_gemm(dev, off, xq, xs, wq, ws, rows=None):
-    """E8M0 kernel against the packed kernel on the same operands (within
-    one bf16 ulp, nearly all equal) and against the float64 oracle on the
-    given rows (all rows by default) at the GEMM bar."""
+    """E8M0 kernel against the packed kernel on the same operands (the
+    plain kernel where K is not a multiple of 512), within one bf16 ulp and
+    nearly all equal, and against the float64 oracle on the given rows (all
+    rows by default) at the GEMM bar."""
     wp = ops.pack_weight_fp8(wq)
     got = ops.grouped_gemm_fp8(xq, xs, wp, ws, off, e8m0=True)
-    ref = ops.grouped_gemm_fp8(xq, xs, wp, ws, off)
+    ref = ops.grouped_gemm_fp8(xq, xs, wp if ops.packed_gemm_ok(*wq.shape[1:]) else wq, ws, off)
     torch.cuda.synchronize()
     lo, hi = int(off[0]), int(off[-1])
     d = _ulps_bf16(got[lo:hi], ref[lo:hi])
@@ -352,7 +353,15 @@ def _check_e8m0_gemm(dev, off, xq, xs, wq, ws, rows=None):
                                          ([0, 0, 1000], 512, 1024),
                                          ([700, 3], 784, 512),
                                          ([4096, 0, 0, 3], 2048, 2048),
-                                         ([1], 16, 65536)])
+                                         ([1], 16, 65536),
+                                         # K blocks not a multiple of 4: the last
+                                         # scale chunk's window ends at K
+                                         ([300, 7], 256, 640),
+                                         ([513, 0, 64], 512, 768),
+                                         ([257], 256, 896),
+                                         ([129, 400], 384, 1152),
+                                         ([1000, 5], 512, 1280),
+                                         ([600, 77], 2880, 2944)])
 def test_e8m0_gemm(dev, counts, N, Kd):
     say("e8m0 gemm", counts, N, Kd)
     off, xq, xs, wq, ws = _pow2_gemm_operands(dev, counts, N, Kd, sum(counts) + N)
@@ -403,7 +412,8 @@ def _close_bf16(got, ref, what, mx=1e-2, mn=1e-3):
 
 
 @pytest.mark.parametrize("T,H,I,E,K", [(256, 256, 256, 8, 2), (1024, 2048, 768, 128, 8),
-                                       (256, 2880, 2880, 8, 4), (512, 1024, 512, 16, 4)])
+                                       (256, 2880, 2880, 8, 4), (512, 1024, 512, 16, 4),
+                                       (512, 640, 768, 8, 2)])
 def test_layer_e8m0_recipe(dev, T, H, I, E, K):
     """SimpleMoE(recipe="e8m0") against the oracle with C10 everywhere.
     Forward stage by stage, each GPU stage fed the GPU's previous output:
