@@ -199,10 +199,15 @@ def test_packed_config4_oracle_samples(dev):
 
 def test_packed_validation(dev):
     say("validation")
-    off, xq, xs, wq, ws = _operands(dev, [100, 50], 256, 640)
+    off, xq, xs, wq, ws = _operands(dev, [100, 50], 256, 384)
     with pytest.raises(ValueError):
-        ops.pack_weight_fp8(wq)                       # K = 640 is not a multiple of 512
+        ops.pack_weight_fp8(wq)                       # K = 384: below 512, no packed kernel
+    off, xq, xs, wq, ws = _operands(dev, [100, 50], 256, 640)
+    # K = 640 packs for the E8M0 kernel only; the packed kernel refuses it
     assert not ops.packed_gemm_ok(256, 640) and ops.packed_gemm_ok(256, 512)
+    assert ops.packed_e8m0_ok(256, 640)
+    with pytest.raises(ValueError):
+        ops.grouped_gemm_fp8(xq, xs, ops.pack_weight_fp8(wq), ws, off)
     st = torch.cuda.current_stream().cuda_stream
     c = torch.empty((150, 256), dtype=torch.bfloat16, device=dev)
     rc = _C.lib().smoe_grouped_gemm_fp8_packed(xq.data_ptr(), xs.data_ptr(), wq.data_ptr(),
