@@ -413,7 +413,7 @@ def bench_fwd_bwd(dev, steps, warmup):
     return out
 
 
-def bench_fwd_bwd_one_stream(dev, steps, warmup):
+def bench_fwd_bwd_one_stream(dev, steps, warmup, recipe="blockwise"):
     """The config-5 step of ``bench_fwd_bwd`` (forward with saved
     intermediates + ``backward_from``) with the weight-gradient stream
     replaced by the caller's stream: every kernel runs alone, which gives
@@ -423,7 +423,7 @@ def bench_fwd_bwd_one_stream(dev, steps, warmup):
     import smoe
     from smoe import workloads as W
     c = W.CONFIGS["qwen3"]
-    m = smoe.SimpleMoE(c.H, c.I, c.E, c.K, device=dev)
+    m = smoe.SimpleMoE(c.H, c.I, c.E, c.K, device=dev, recipe=recipe)
     with torch.no_grad():
         m.w1.copy_(W.weights(c.E, 2 * c.I, c.H, device=dev))
         m.w2.copy_(W.weights(c.E, c.H, c.I, device=dev, seed=13))
@@ -442,7 +442,7 @@ def bench_fwd_bwd_one_stream(dev, steps, warmup):
     t1 = timed_median(step, steps, warmup)
     del m
     torch.cuda.empty_cache()
-    return {"workload": "qwen3 layer fwd+bwd T=16384 H=2048 I=768 E=128 top8",
+    return {"workload": "qwen3 layer fwd+bwd T=16384 H=2048 I=768 E=128 top8", "recipe": recipe,
             "ms_two_streams": round(t2, 4), "ms_one_stream": round(t1, 4)}
 
 
@@ -504,7 +504,7 @@ def run_only(args, dev, c):
     at the config-4 shapes, router = the fused router + sort at config 2,
     wgrad = the config-5 fc1 weight gradient, fwdbwd = the config-5 layer
     forward + backward, fwdbwd1 = the same with the weight gradients on the
-    caller's stream (every kernel alone), layer = the config-3 (Mixtral)
+    caller's stream (every kernel alone; --recipe picks its scale recipe), layer = the config-3 (Mixtral)
     layer forward."""
     import torch
     from smoe import ops, workloads as W
@@ -530,7 +530,8 @@ def run_only(args, dev, c):
     elif args.only == "fwdbwd":
         print(json.dumps({"only": "fwdbwd", **bench_fwd_bwd(dev, args.steps, args.warmup)}))
     elif args.only == "fwdbwd1":
-        print(json.dumps({"only": "fwdbwd1", **bench_fwd_bwd_one_stream(dev, args.steps, args.warmup)}))
+        print(json.dumps({"only": "fwdbwd1", **bench_fwd_bwd_one_stream(dev, args.steps, args.warmup,
+                                                                         args.recipe)}))
     elif args.only == "layer":
         print(json.dumps({"only": "layer", **bench_layer(dev, args.steps, args.warmup)}))
     elif args.only == "gemm":
@@ -796,6 +797,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-extra", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--recipe", choices=["blockwise", "e8m0"], default="blockwise",
+                    help="scale recipe of the --only fwdbwd1 layer step")
     ap.add_argument("--only", choices=["permute", "gemm", "combine", "copy", "fwdbwd", "ceiling",
                                        "blaslt", "router", "wgrad", "layer", "refshapes",
                                        "bwdparts", "fwdbwd1"],
