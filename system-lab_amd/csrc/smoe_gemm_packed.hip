@@ -37,7 +37,6 @@
 // Scope: K a multiple of 512 (the chunked activation scales); other K use the
 // plain kernel (the ops layer and SimpleMoE choose).
 #include "smoe_mfma.h"
-#include <cstdlib>
 
 namespace smoe {
 namespace packed {
@@ -97,7 +96,7 @@ __device__ __forceinline__ v8i lds_frag_p(const uint8_t* base, int row, int g) {
 // +128 (waves 0-3) with up columns I + nt*128 .. +128 (waves 4-7) and the
 // epilogue writes hq, hs (and c1 when c is not null) exactly as the fused
 // epilogue of smoe_gemm.hip does.
-template <bool kSwiGLU, bool kE8M0 = false>
+template <bool kSwiGLU>
 __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_fp8_packed_kernel(
     const uint8_t* __restrict__ a, const float* __restrict__ as, const uint8_t* __restrict__ bp,
     const float* __restrict__ bs, const int32_t* __restrict__ offsets, int E, int R, int N, int Kd,
@@ -292,18 +291,6 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_fp8_packed_kernel(
       }
       v8i fxn = fx;
       if (i + 1 < kRB) fxn = lds_frag_p(sA, (i + 1) * 16 + frow, fg);
-      if constexpr (kE8M0) {
-        const int ex = (__float_as_uint(sC[(i * 16 + frow) * kSChunk]) >> 23) & 0xff;
-        const int ew = (__float_as_uint(sb) >> 23) & 0xff;
-        asm volatile("" : "+v"(fx));
-#pragma unroll
-        for (int j = 0; j < kCB; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(fw[j], fx, acc[i][j], 0, 0,
-                                                                       0, ew, 0, ex);
-        asm volatile("" : "+v"(acc[i][0]), "+v"(acc[i][1]));
-        fx = fxn;
-        continue;
-      }
       const float sc = sC[(i * 16 + frow) * kSChunk] * sb;
       asm volatile("" : "+v"(fx));
       v4f p[kCB];
@@ -322,12 +309,10 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_fp8_packed_kernel(
       scp = sc;
       fx = fxn;
     }
-    if constexpr (!kE8M0) {
 #pragma unroll
-      for (int j = 0; j < kCB; ++j)
+    for (int j = 0; j < kCB; ++j)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) acc[kRB - 1][j][v] = __builtin_fmaf(pp[j][v], scp, acc[kRB - 1][j][v]);
-    }
+      for (int v = 0; v < 4; ++v) acc[kRB - 1][j][v] = __builtin_fmaf(pp[j][v], scp, acc[kRB - 1][j][v]);
     // Activation stage kb+1 was issued during step kb-2; at least the 8 loads
     // of step kb-1 (4 DMAs, and 4 weight loads the next step reads) came after
     // it, so vmcnt(8) covers it, and the scale chunks, which are older.  (The
@@ -451,9 +436,6 @@ extern "C" int smoe_grouped_gemm_fp8_packed(const uint8_t* a, const float* as, c
   long long mt_bound;
   const long long nblk = packed_grid(E, R, (N + packed::kBN - 1) / packed::kBN, &mt_bound);
   if (nblk > 0x7fffffffLL) return SMOE_EINVAL_DIM;
-  if (getenv("SMOE_PROTO_E8M0")) packed::grouped_gemm_fp8_packed_kernel<false, true>
-      <<<dim3((unsigned)nblk), dim3(packed::kThreads), 0, (hipStream_t)stream>>>(
-          a, as, wp, ws, offsets, E, R, N, Kdim, (int)mt_bound, c, nullptr, nullptr); else
   packed::grouped_gemm_fp8_packed_kernel<false>
       <<<dim3((unsigned)nblk), dim3(packed::kThreads), 0, (hipStream_t)stream>>>(
           a, as, wp, ws, offsets, E, R, N, Kdim, (int)mt_bound, c, nullptr, nullptr);
