@@ -241,6 +241,9 @@ def bench_gemm(dev, steps, warmup, skip_cpu=True):
                        steps, warmup)
     t2e = timed_median(lambda: ops.grouped_gemm_fp8(hq, hs, w2p, w2s, off, out=y, e8m0=True),
                        steps, warmup)
+    t1se = timed_median(lambda: ops.grouped_gemm_fp8_swiglu(xq, xs, w1p, w1s, off, scale="pow2"),
+                        steps, warmup)
+    t_swe = timed_median(lambda: ops.swiglu_quant(c1, scale="pow2"), steps, warmup)
     tfe = (fl1 + fl2) / ((t1e + t2e) * 1e-3) / 1e12
     tfu = (fl1 + fl2) / ((t1u + t2u) * 1e-3) / 1e12
     out = {"workload": "dsv3 local experts R=65536 H=7168 I=2048 E=32 zipf1.2",
@@ -252,6 +255,8 @@ def bench_gemm(dev, steps, warmup, skip_cpu=True):
            "plain_fc1_ms": round(t1u, 4), "plain_fc2_ms": round(t2u, 4),
            "plain_tflops": round(tfu, 1), "plain_roofline_frac": round(tfu / FP8_PEAK_TFLOPS, 4),
            "e8m0_fc1_ms": round(t1e, 4), "e8m0_fc2_ms": round(t2e, 4),
+           "e8m0_fc1_swiglu_fused_ms": round(t1se, 4),
+           "e8m0_fc1_then_swiglu_ms": round(t1e + t_swe, 4),
            "e8m0_tflops": round(tfe, 1), "e8m0_roofline_frac": round(tfe / FP8_PEAK_TFLOPS, 4),
            "e8m0_note": "power-of-two 1x128 / 128x128 scales (recipe e8m0), "
                         "smoe_grouped_gemm_fp8_packed_e8m0",

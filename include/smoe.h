@@ -303,7 +303,8 @@ int smoe_grouped_gemm_fp8_packed(const uint8_t* a, const float* as, const uint8_
  * accumulators kept in the accumulation registers, which lets a workgroup
  * of 4 waves (256 x 64 each) replace the 8 of the packed kernel.  Scales
  * that are not powers of two are read by their exponent only (wrong
- * results).  Same requirements as smoe_grouped_gemm_fp8_packed.  No
+ * results).  Requires Kdim % 128 == 0, 512 <= Kdim <= 65536, N % 16 == 0
+ * and N*Kdim < 2^32; wp from smoe_pack_weight_fp8.  No
  * counterpart of its own in the reference: the grouped GEMM it replaces is
  * that of smoe_grouped_gemm_fp8, under the MXFP8-style power-of-two scale
  * rule (moe/MegatronCore_MoE_reading_notes.md:503-504).
@@ -311,6 +312,23 @@ int smoe_grouped_gemm_fp8_packed(const uint8_t* a, const float* as, const uint8_
 int smoe_grouped_gemm_fp8_packed_e8m0(const uint8_t* a, const float* as, const uint8_t* wp,
                                       const float* ws, const int32_t* offsets, int E, int R,
                                       int N, int Kdim, uint16_t* c, void* stream);
+
+/*
+ * smoe_grouped_gemm_fp8_packed_e8m0 on packed W1 [E,2I,Kdim] with SwiGLU and
+ * the power-of-two 1x128 requantisation in its epilogue: hq, hs equal
+ * smoe_swiglu_quant_ex(c1, ..., SMOE_SCALE_POW2) of the c1 that
+ * smoe_grouped_gemm_fp8_packed_e8m0 writes, and c1 itself is written when
+ * not NULL.  Requires I % 128 == 0 and the Kdim range of
+ * smoe_grouped_gemm_fp8_packed_e8m0.  Replaces the same grouped GEMM +
+ * activation pair as smoe_grouped_gemm_fp8_swiglu
+ * (summary/fp8_expert_gemm_optimization.md:121-131) under the MXFP8-style
+ * scale rule (moe/MegatronCore_MoE_reading_notes.md:503-504).
+ */
+int smoe_grouped_gemm_fp8_packed_e8m0_swiglu(const uint8_t* a, const float* as,
+                                             const uint8_t* w1p, const float* w1s,
+                                             const int32_t* offsets, int E, int R, int I,
+                                             int Kdim, uint8_t* hq, float* hs, uint16_t* c1,
+                                             void* stream);
 
 /*
  * smoe_grouped_gemm_fp8_swiglu on packed W1 (smoe_pack_weight_fp8 of w1

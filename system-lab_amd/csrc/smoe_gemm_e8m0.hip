@@ -90,10 +90,16 @@ __device__ __forceinline__ void mfma_scale_acc(v4f& acc, const v8i& a, const v8i
                  : "v"(a), "v"(b), "v"(sa), "v"(sb));
 }
 
+// kSwiGLU: bp is W1 packed [E, 2I, K] (N = 2I); tile nt pairs gate columns
+// nt*128 .. +128 (waves 0-1) with up columns I + nt*128 .. +128 (waves 2-3),
+// and the epilogue writes h = silu(gate) * up requantised 1x128 with
+// power-of-two scales into hq [R, I], hs [R, I/128] (and c1 when c is not
+// null): the bytes of the SwiGLU quantiser run on this kernel's c.
+template <bool kSwiGLU>
 __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_fp8_e8m0_kernel(
     const uint8_t* __restrict__ a, const float* __restrict__ as, const uint8_t* __restrict__ bp,
     const float* __restrict__ bs, const int32_t* __restrict__ offsets, int E, int R, int N, int Kd,
-    int mt_bound, uint16_t* __restrict__ c) {
+    int mt_bound, uint16_t* __restrict__ c, uint8_t* __restrict__ hq, float* __restrict__ hs) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kSmem];
   __shared__ int mstart[SMOE_MAX_EXPERTS + 1];
   __shared__ int wsum[kWaves];
@@ -133,7 +139,8 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_fp8_e8m0_kernel(
 
   // ---- tile index: chip-wide m-groups, kChipM/8 m-tiles per XCD ---------
   const int bid = blockIdx.x;
-  const int NT = (N + kBN - 1) / kBN;
+  const int I = N / 2;
+  const int NT = kSwiGLU ? I / kGroup : (N + kBN - 1) / kBN;
   constexpr int kXM = kChipM / 8;
   const int xcd = bid & 7, kx = bid >> 3;
   const int m_all = min(total_mt, mt_bound);
@@ -164,7 +171,7 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_fp8_e8m0_kernel(
   if (row0 < 0 || rows <= 0) return;  // the whole workgroup leaves together
   const int n0 = nt * kBN;
   const int ksb = Kd / kBK;
-  const int ncols = min(kBN, N - n0);
+  const int ncols = kSwiGLU ? kBN : min(kBN, N - n0);
 
   // ---- activation DMA: wave w fills 1 KiB segments w*8 .. w*8+7 of a stage
   const uint8_t* a_base = a + (size_t)row0 * Kd;
@@ -230,7 +237,11 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_fp8_e8m0_kernel(
   uint32_t ob[kCB];
 #pragma unroll
   for (int j = 0; j < kCB; ++j) {
-    const int wr0 = min(n0 + wid * 64 + j * 16, N - 16);  // columns past N: clamped, never stored
+    int wr0;  // first weight row of this column block
+    if constexpr (kSwiGLU)
+      wr0 = (wid < 2 ? 0 : I) + nt * kGroup + (wid & 1) * 64 + j * 16;
+    else
+      wr0 = min(n0 + wid * 64 + j * 16, N - 16);  // columns past N: clamped, never stored
     ob[j] = (uint32_t)(wr0 / 16) * (uint32_t)ksb * 2048u + (uint32_t)lane * 16u;
   }
   auto load_b = [&](int kb, WBuf& f) __attribute__((always_inline)) {
@@ -270,7 +281,8 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_fp8_e8m0_kernel(
   __syncthreads();
   for (int i = tid; i < kNB128 * ksb; i += kThreads) {
     const int nb = i / ksb, kb = i - nb * ksb;
-    sbt[i] = bs[((size_t)e * NB + min(n0 / kGroup + nb, NB - 1)) * ksb + kb];
+    const int blk = kSwiGLU ? (nb == 0 ? nt : I / kGroup + nt) : min(n0 / kGroup + nb, NB - 1);
+    sbt[i] = bs[((size_t)e * NB + blk) * ksb + kb];
   }
   __syncthreads();
   const float* sb_row = sbt + ((wid * 64) / kGroup) * ksb;
@@ -278,11 +290,6 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_fp8_e8m0_kernel(
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 
-  // ---- one K step: weights of step kb in cur, step kb+1's in nx1, step
-  // kb+2's loaded into nx2.  Activation DMAs go out before the even row
-  // blocks and weight loads before the odd ones.  Past the last step the
-  // loads repeat step ksb-1's data into buffers and stages no later step
-  // reads, so the number of DMAs per step is fixed (the wait below counts on it).
   // ---- one K step: weights of step kb in cur, those of step kb+3 loaded
   // into nxt (the buffer step kb-1 used).  The activation DMAs of a step go
   // out before its first 8 row blocks and the weight loads before the last
@@ -373,13 +380,40 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_fp8_e8m0_kernel(
     }
   }
   __syncthreads();
-  constexpr int kChunks = kBN * 2 / 16;
-  const int nchunks = ncols * 2 / 16;
-  for (int idx = tid; idx < rows * kChunks; idx += kThreads) {
-    const int r = idx / kChunks, ch = idx - r * kChunks;
-    if (ch < nchunks)
-      *(uint4*)((uint8_t*)(c + (size_t)(row0 + r) * N + n0) + ch * 16) =
-          *(const uint4*)(ct + r * kCPitch + ch * 16);
+  if constexpr (kSwiGLU) {
+    // 8 lanes per row, 16 columns each: h = silu(g) * u from the staged bf16
+    // values, amax over the 8 lanes, 16 fp8 bytes per lane
+    for (int idx = tid; idx < rows * 8; idx += kThreads) {
+      const int r = idx >> 3, sub = idx & 7;
+      const uint8_t* rowp = ct + r * kCPitch;
+      float fgt[16], fu[16], h[16];
+      unpack_bf16x8(*(const uint4*)(rowp + sub * 32), fgt);
+      unpack_bf16x8(*(const uint4*)(rowp + sub * 32 + 16), fgt + 8);
+      unpack_bf16x8(*(const uint4*)(rowp + 256 + sub * 32), fu);
+      unpack_bf16x8(*(const uint4*)(rowp + 256 + sub * 32 + 16), fu + 8);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) h[i] = silu32(fgt[i]) * fu[i];
+      const Q16 q = quant16<true>(h);
+      const size_t gr = (size_t)(row0 + r);
+      *(uint4*)(hq + gr * I + nt * kGroup + sub * 16) = q.q;
+      if (sub == 0) hs[gr * (I / kGroup) + nt] = q.scale;
+      if (c) {
+        uint16_t* crow = c + gr * N + nt * kGroup + sub * 16;
+        *(uint4*)crow = *(const uint4*)(rowp + sub * 32);
+        *(uint4*)(crow + 8) = *(const uint4*)(rowp + sub * 32 + 16);
+        *(uint4*)(crow + I) = *(const uint4*)(rowp + 256 + sub * 32);
+        *(uint4*)(crow + I + 8) = *(const uint4*)(rowp + 256 + sub * 32 + 16);
+      }
+    }
+  } else {
+    constexpr int kChunks = kBN * 2 / 16;
+    const int nchunks = ncols * 2 / 16;
+    for (int idx = tid; idx < rows * kChunks; idx += kThreads) {
+      const int r = idx / kChunks, ch = idx - r * kChunks;
+      if (ch < nchunks)
+        *(uint4*)((uint8_t*)(c + (size_t)(row0 + r) * N + n0) + ch * 16) =
+            *(const uint4*)(ct + r * kCPitch + ch * 16);
+    }
   }
 }
 
@@ -388,10 +422,9 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_fp8_e8m0_kernel(
 
 using namespace smoe;
 
-extern "C" int smoe_grouped_gemm_fp8_packed_e8m0(const uint8_t* a, const float* as,
-                                                 const uint8_t* wp, const float* ws,
-                                                 const int32_t* offsets, int E, int R, int N,
-                                                 int Kdim, uint16_t* c, void* stream) {
+namespace {
+int e8m0_args(const uint8_t* a, const float* as, const uint8_t* wp, const float* ws,
+              const int32_t* offsets, int E, int R, int N, int Kdim) {
   if (R <= 0 || N <= 0 || Kdim <= 0) return SMOE_EINVAL_DIM;
   if (E <= 0 || E > SMOE_MAX_EXPERTS) return SMOE_EINVAL_EXPERTS;
   if (N % kLane || Kdim % kBK) return SMOE_EINVAL_ALIGN128;
@@ -399,15 +432,51 @@ extern "C" int smoe_grouped_gemm_fp8_packed_e8m0(const uint8_t* a, const float* 
   if ((long long)N * Kdim >= (1LL << 32)) return SMOE_EINVAL_DIM;
   SMOE_CHECK_PTR(a);
   SMOE_CHECK_PTR(wp);
-  SMOE_CHECK_PTR(c);
   if (!as || !ws || !offsets) return SMOE_EINVAL_NULL;
   if (((uintptr_t)as | (uintptr_t)ws | (uintptr_t)offsets) & 3u) return SMOE_EINVAL_PTRALIGN;
-  const long long mt_bound = (R + e8m0::kBM - 1) / e8m0::kBM + E;
-  const long long mt_pad = (mt_bound + e8m0::kChipM - 1) / e8m0::kChipM * e8m0::kChipM;
-  const long long nblk = (mt_pad * ((N + e8m0::kBN - 1) / e8m0::kBN) + 7) / 8 * 8;
+  return SMOE_OK;
+}
+long long e8m0_grid(int E, int R, int NT, long long* mt_bound) {
+  *mt_bound = (R + e8m0::kBM - 1) / e8m0::kBM + E;
+  const long long mt_pad = (*mt_bound + e8m0::kChipM - 1) / e8m0::kChipM * e8m0::kChipM;
+  return (mt_pad * NT + 7) / 8 * 8;
+}
+}  // namespace
+
+extern "C" int smoe_grouped_gemm_fp8_packed_e8m0(const uint8_t* a, const float* as,
+                                                 const uint8_t* wp, const float* ws,
+                                                 const int32_t* offsets, int E, int R, int N,
+                                                 int Kdim, uint16_t* c, void* stream) {
+  const int st = e8m0_args(a, as, wp, ws, offsets, E, R, N, Kdim);
+  if (st) return st;
+  SMOE_CHECK_PTR(c);
+  long long mt_bound;
+  const long long nblk = e8m0_grid(E, R, (N + e8m0::kBN - 1) / e8m0::kBN, &mt_bound);
   if (nblk > 0x7fffffffLL) return SMOE_EINVAL_DIM;
-  e8m0::grouped_gemm_fp8_e8m0_kernel<<<dim3((unsigned)nblk), dim3(e8m0::kThreads), 0,
-                                       (hipStream_t)stream>>>(a, as, wp, ws, offsets, E, R, N,
-                                                              Kdim, (int)mt_bound, c);
+  e8m0::grouped_gemm_fp8_e8m0_kernel<false>
+      <<<dim3((unsigned)nblk), dim3(e8m0::kThreads), 0, (hipStream_t)stream>>>(
+          a, as, wp, ws, offsets, E, R, N, Kdim, (int)mt_bound, c, nullptr, nullptr);
+  SMOE_RETURN_LAUNCH();
+}
+
+extern "C" int smoe_grouped_gemm_fp8_packed_e8m0_swiglu(const uint8_t* a, const float* as,
+                                                        const uint8_t* w1p, const float* w1s,
+                                                        const int32_t* offsets, int E, int R,
+                                                        int I, int Kdim, uint8_t* hq, float* hs,
+                                                        uint16_t* c1, void* stream) {
+  if (I <= 0) return SMOE_EINVAL_DIM;
+  if (I % kGroup) return SMOE_EINVAL_ALIGN128;
+  const int st = e8m0_args(a, as, w1p, w1s, offsets, E, R, 2 * I, Kdim);
+  if (st) return st;
+  SMOE_CHECK_PTR(hq);
+  if (c1 && ((uintptr_t)c1 & 15u)) return SMOE_EINVAL_PTRALIGN;
+  if (!hs) return SMOE_EINVAL_NULL;
+  if ((uintptr_t)hs & 3u) return SMOE_EINVAL_PTRALIGN;
+  long long mt_bound;
+  const long long nblk = e8m0_grid(E, R, I / kGroup, &mt_bound);
+  if (nblk > 0x7fffffffLL) return SMOE_EINVAL_DIM;
+  e8m0::grouped_gemm_fp8_e8m0_kernel<true>
+      <<<dim3((unsigned)nblk), dim3(e8m0::kThreads), 0, (hipStream_t)stream>>>(
+          a, as, w1p, w1s, offsets, E, R, 2 * I, Kdim, (int)mt_bound, c1, hq, hs);
   SMOE_RETURN_LAUNCH();
 }

@@ -44,6 +44,8 @@ SIGNATURES = {
     "smoe_pack_weight_fp8": (c_int, [P, c_int, c_int, c_int, P, P]),
     "smoe_grouped_gemm_fp8_packed": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int, P, P]),
     "smoe_grouped_gemm_fp8_packed_e8m0": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int, P, P]),
+    "smoe_grouped_gemm_fp8_packed_e8m0_swiglu": (c_int, [P, P, P, P, P, c_int, c_int, c_int,
+                                                         c_int, P, P, P, P]),
     "smoe_grouped_gemm_fp8_packed_swiglu": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int,
                                                     P, P, P, P]),
     "smoe_swiglu_quant": (c_int, [P, c_int, c_int, P, P, P]),

@@ -266,7 +266,6 @@ class SimpleMoE(nn.Module):
             hq, hs, h = ops.swiglu_quant(c1, save_h=True, scale=rs)
         else:
             # inference: SwiGLU + requantisation run in the fc1 epilogue
-            # (the e8m0 recipe runs its GEMM, then the SwiGLU kernel)
             hq, hs = ops.grouped_gemm_fp8_swiglu(xq, xs, w1q, w1s, offsets, scale=rs)
         y = ops.grouped_gemm_fp8(hq, hs, w2q, w2s, offsets, e8m0=e8)
         out = ops.unpermute_combine(y, inv_map, w)

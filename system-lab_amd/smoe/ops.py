@@ -419,13 +419,16 @@ def grouped_gemm_fp8_swiglu(xq: torch.Tensor, xs: torch.Tensor, w1q: torch.Tenso
     ``save_c1``.  Rows outside [offsets[0], offsets[E]) are not written.
     ``w1q`` may be a PackedWeight (see grouped_gemm_fp8).  ``scale="pow2"``
     (the E8M0 recipe: power-of-two operand scales in, power-of-two hs out)
-    runs ``grouped_gemm_fp8(..., e8m0=True)`` and then ``swiglu_quant``."""
-    if _scale(scale) != SCALES["amax"]:
+    gives the bytes of ``swiglu_quant(grouped_gemm_fp8(..., e8m0=True),
+    scale="pow2")``: fused (smoe_grouped_gemm_fp8_packed_e8m0_swiglu) for a
+    packed W1 with I % 128 == 0, else those two calls."""
+    pow2 = _scale(scale) != SCALES["amax"]
+    _check(xq, "xq", (FP8, torch.uint8))
+    wt, packed = _weight(w1q, "w1q")
+    if pow2 and not (packed and wt.shape[1] % (2 * GROUP) == 0):
         c1 = grouped_gemm_fp8(xq, xs, w1q, w1s, offsets, e8m0=True)
         hq, hs = swiglu_quant(c1, scale=scale)
         return (hq, hs, c1) if save_c1 else (hq, hs)
-    _check(xq, "xq", (FP8, torch.uint8))
-    wt, packed = _weight(w1q, "w1q")
     _check(xs, "xs", (torch.float32,), 2)
     _check(w1s, "w1s", (torch.float32,), 3)
     _check(offsets, "offsets", (torch.int32,), 1)
@@ -433,9 +436,9 @@ def grouped_gemm_fp8_swiglu(xq: torch.Tensor, xs: torch.Tensor, w1q: torch.Tenso
     E, N, Kw = wt.shape
     if Kw != Kd:
         raise ValueError(f"K mismatch: xq has {Kd}, w1q has {Kw}")
-    if packed and not packed_gemm_ok(N, Kd):
-        raise ValueError(f"packed weights need K % 512 == 0, K <= {PACKED_MAX_K} and N*K < 2^32 "
-                         f"(N={N}, K={Kd})")
+    if packed and not (packed_e8m0_ok(N, Kd) if pow2 else packed_gemm_ok(N, Kd)):
+        raise ValueError(f"packed weights need K % 512 == 0 (K % 128 == 0 and K >= 512 with "
+                         f"scale='pow2'), K <= {PACKED_MAX_K} and N*K < 2^32 (N={N}, K={Kd})")
     if N % 2 == 0 and (N // 2) % GROUP and (N // 2) % 16 == 0:
         # I not a multiple of 128: the fused epilogue pairs 128-column gate
         # and up blocks, which such an I does not have; the same bytes come
@@ -453,7 +456,10 @@ def grouped_gemm_fp8_swiglu(xq: torch.Tensor, xs: torch.Tensor, w1q: torch.Tenso
     hq = torch.empty((R, I), dtype=FP8, device=xq.device)
     hs = torch.empty((R, I // GROUP), dtype=torch.float32, device=xq.device)
     c1 = torch.empty((R, N), dtype=torch.bfloat16, device=xq.device) if save_c1 else None
-    fn = "smoe_grouped_gemm_fp8_packed_swiglu" if packed else "smoe_grouped_gemm_fp8_swiglu"
+    if pow2:
+        fn = "smoe_grouped_gemm_fp8_packed_e8m0_swiglu"
+    else:
+        fn = "smoe_grouped_gemm_fp8_packed_swiglu" if packed else "smoe_grouped_gemm_fp8_swiglu"
     _C.call(fn, _ptr(_bytes(xq)), _ptr(xs), _ptr(wt if packed else _bytes(wt)), _ptr(w1s),
             _ptr(offsets), E, R, I, Kd, _ptr(hq), _ptr(hs), _ptr(c1), _stream())
     return (hq, hs, c1) if save_c1 else (hq, hs)

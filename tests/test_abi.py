@@ -204,7 +204,8 @@ def test_scale_mode_entries_reject():
     """The _ex quantisers take SMOE_SCALE_AMAX (0) or SMOE_SCALE_POW2 (1) and
     nothing else; the column quantiser takes only the column bit, the fused
     row-and-column quantisers also the row bit (2); the E8M0 GEMM takes K a
-    multiple of 128 from 512 to 65536 (ops.packed_e8m0_ok says the same).
+    multiple of 128 from 512 to 65536 (ops.packed_e8m0_ok says the same),
+    its fused SwiGLU form also I a multiple of 128.
     All rejected before any launch."""
     from smoe import ops
     assert ops.packed_e8m0_ok(128, 640) and ops.packed_e8m0_ok(128, 65536)
@@ -238,6 +239,15 @@ def test_scale_mode_entries_reject():
     assert g(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 256, 128, 384, FAKE, None) == -2   # K < 512
     assert g(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 256, 120, 1024, FAKE, None) == -3  # N % 16
     assert g(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 256, 128, 65536 + 512, FAKE, None) == -2
+    # the fused SwiGLU form: I % 128, its K range, hs NULL, misaligned c1
+    f = lib.smoe_grouped_gemm_fp8_packed_e8m0_swiglu
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 256, 192, 1024, FAKE, FAKE, None, None) == -3
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 256, 0, 1024, FAKE, FAKE, None, None) == -2
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 256, 256, 384, FAKE, FAKE, None, None) == -2
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 256, 256, 576, FAKE, FAKE, None, None) == -3
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 256, 256, 640, FAKE, None, None, None) == -1
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 256, 256, 640, FAKE, FAKE, MIS, None) == -6
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 0, 256, 256, 640, FAKE, FAKE, None, None) == -4
     assert g(FAKE, FAKE, FAKE, FAKE, FAKE, 0, 256, 128, 1024, FAKE, None) == -4
     assert g(FAKE, None, FAKE, FAKE, FAKE, 2, 256, 128, 1024, FAKE, None) == -1
     assert g(FAKE, FAKE + 2, FAKE, FAKE, FAKE, 2, 256, 128, 1024, FAKE, None) == -6

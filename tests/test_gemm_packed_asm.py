@@ -1,8 +1,9 @@
-"""The packed grouped GEMM (system-lab_amd/csrc/smoe_gemm_packed.hip) mixes
-activation DMAs issued as inline asm, which the compiler does not count, with
-weight loads into registers whose waits the compiler places itself.  Both
-retire through one in-order counter, so the compiler's waits can only wait
-longer than needed; this compiles the kernel with the library's flags and
+"""The packed grouped GEMMs (system-lab_amd/csrc/smoe_gemm_packed.hip and
+smoe_gemm_e8m0.hip) mix activation DMAs issued as inline asm, which the
+compiler does not count, with weight loads into registers whose waits the
+compiler places itself.  Both retire through one in-order counter, so the
+compiler's waits can only wait longer than needed; this compiles each
+kernel source with the library's flags and
 checks, counting every memory instruction as the hardware does, that no
 register of a weight load is read, copied or overwritten before a wait that
 covers it (tests/asm_inflight.py).  The scanner is first held to snippets
@@ -56,10 +57,12 @@ def test_scanner_flags_hazards_and_passes_clean_code():
 
 
 @pytest.mark.skipif(not shutil.which(HIPCC) and not os.path.exists(HIPCC), reason="hipcc not found")
-def test_packed_gemm_has_no_inflight_register_access(tmp_path):
+@pytest.mark.parametrize("name", ["smoe_gemm_packed", "smoe_gemm_e8m0"])
+def test_packed_gemm_has_no_inflight_register_access(tmp_path, name):
+    """Both packed-weight GEMM sources, every kernel instantiation in them."""
     sys.path.insert(0, os.path.join(ROOT, "system-lab_amd"))
     from smoe import build
-    src = os.path.join(ROOT, "system-lab_amd", "csrc", "smoe_gemm_packed.hip")
+    src = os.path.join(ROOT, "system-lab_amd", "csrc", name + ".hip")
     out = tmp_path / "packed.s"
     flags = [f for f in build.HIP_FLAGS if not f.startswith("-W")]
     subprocess.run([HIPCC, *flags, "--cuda-device-only", "-S", src, "-o", str(out)], check=True,

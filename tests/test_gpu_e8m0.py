@@ -21,7 +21,7 @@ import torch
 
 from oracle import smoe_oracle as O
 import smoe
-from smoe import ops, workloads as W
+from smoe import _C, ops, workloads as W
 
 pytestmark = pytest.mark.gpu
 
@@ -385,7 +385,8 @@ def test_e8m0_gemm_dsv3_full_shape(dev):
     """Benchmark config 4's fc1 and fc2 (R=65536, 32 Zipf-loaded experts with
     zero-token ones, H=7168, I=2048) at full size with power-of-two scales:
     every row against the packed kernel, 8 sampled rows of every non-empty
-    expert (first and last included) against the float64 oracle."""
+    expert (first and last included) against the float64 oracle; fc1's
+    fused SwiGLU form against the GEMM and the SwiGLU quantiser, every row."""
     say("e8m0 gemm dsv3 full")
     c = W.CONFIGS["dsv3"]
     off = W.offsets_from_counts(W.zipf_counts()).to(dev)
@@ -402,8 +403,62 @@ def test_e8m0_gemm_dsv3_full_shape(dev):
         wq, ws = ops.quantize_weight_blockwise(W.weights(c.E, N, Kd, device=dev, seed=seed),
                                                scale="pow2")
         _check_e8m0_gemm(dev, off, xq, xs, wq, ws, rows=rows)
+        if N == 2 * c.I:
+            _check_e8m0_swiglu(dev, off, xq, xs, wq, ws)
         del xq, xs, wq, ws
         torch.cuda.empty_cache()
+
+
+def _check_e8m0_swiglu(dev, off, xq, xs, w1q, w1s):
+    """The fused entry (smoe_grouped_gemm_fp8_packed_e8m0_swiglu) against the
+    E8M0 GEMM followed by the SwiGLU quantiser on the rows in
+    [offsets[0], offsets[E]): hq, hs and c1 bit-exact; hs powers of two.
+    Then hq, hs against the oracle's SwiGLU quantiser of the GPU's c1,
+    bit-exact."""
+    w1p = ops.pack_weight_fp8(w1q)
+    hq, hs, c1 = ops.grouped_gemm_fp8_swiglu(xq, xs, w1p, w1s, off, save_c1=True, scale="pow2")
+    qhq, qhs = ops.grouped_gemm_fp8_swiglu(xq, xs, w1p, w1s, off, scale="pow2")
+    rc1 = ops.grouped_gemm_fp8(xq, xs, w1p, w1s, off, e8m0=True)
+    rhq, rhs = ops.swiglu_quant(rc1, scale="pow2")
+    torch.cuda.synchronize()
+    lo, hi = int(off[0]), int(off[-1])
+    assert torch.equal(c1[lo:hi].view(torch.int16), rc1[lo:hi].view(torch.int16))
+    for q, sc in ((hq, hs), (qhq, qhs)):
+        assert torch.equal(q[lo:hi].view(torch.uint8), rhq[lo:hi].view(torch.uint8))
+        assert torch.equal(sc[lo:hi], rhs[lo:hi])
+    assert bool((torch.frexp(hs[lo:hi])[0] == 0.5).all())
+    oq, os_ = O.swiglu_quant(u16(c1[lo:hi]), pow2=True)
+    assert np.array_equal(u8(hq[lo:hi]), oq) and np.array_equal(hs[lo:hi].cpu().numpy(), os_)
+    return c1
+
+
+@pytest.mark.parametrize("counts,I,Kd", [([200, 0, 333], 256, 1024), ([513, 64], 768, 2048),
+                                         ([300, 0, 77], 128, 512), ([1000], 1408, 1024),
+                                         ([257, 3], 384, 640), ([129, 0, 400], 256, 2944)])
+def test_e8m0_swiglu_fused(dev, counts, I, Kd):
+    say("e8m0 swiglu fused", counts, I, Kd)
+    off, xq, xs, w1q, w1s = _pow2_gemm_operands(dev, counts, 2 * I, Kd, sum(counts) + I)
+    _check_e8m0_swiglu(dev, off, xq, xs, w1q, w1s)
+
+
+def test_e8m0_swiglu_fused_row_window(dev):
+    """Rows outside [offsets[0], offsets[E]) of hq, hs and c1 are not written."""
+    say("e8m0 swiglu fused row window")
+    _, xq, xs, w1q, w1s = _pow2_gemm_operands(dev, [600], 512, 512, 9)
+    off = torch.tensor([40, 300, 300, 555], dtype=torch.int32, device=dev)
+    w1q, w1s = w1q.repeat(3, 1, 1).contiguous(), w1s.repeat(3, 1, 1).contiguous()
+    hq = torch.full((600, 256), 7, dtype=torch.uint8, device=dev)
+    hs = torch.full((600, 2), 3.0, dtype=torch.float32, device=dev)
+    c1 = torch.full((600, 512), 3.0, dtype=torch.bfloat16, device=dev)
+    w1p = ops.pack_weight_fp8(w1q)
+    _C.call("smoe_grouped_gemm_fp8_packed_e8m0_swiglu", xq.data_ptr(), xs.data_ptr(),
+            w1p.data.data_ptr(), w1s.data_ptr(), off.data_ptr(), 3, 600, 256, 512, hq.data_ptr(),
+            hs.data_ptr(), c1.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    for lo, hi in ((0, 40), (555, 600)):
+        assert bool((hq[lo:hi] == 7).all()) and bool((hs[lo:hi] == 3.0).all())
+        assert bool((c1[lo:hi] == 3.0).all())
+    _check_e8m0_swiglu(dev, off, xq, xs, w1q, w1s)
 
 
 def _close_bf16(got, ref, what, mx=1e-2, mn=1e-3):
@@ -443,7 +498,7 @@ def test_layer_e8m0_recipe(dev, T, H, I, E, K):
     _close_bf16(st["y"], O.f32_to_bf16(y.astype(np.float32)), "y")
     ro = O.unpermute_combine(u16(st["y"]), st["inv_map"].cpu().numpy(), st["topk_w"].cpu().numpy(), K)
     assert np.array_equal(u16(out), ro)
-    # the inference path (GEMM, then the SwiGLU kernel) gives the same output
+    # the inference path (SwiGLU fused into the fc1 epilogue) gives the same output
     with torch.no_grad():
         out_inf = m(x.to(dev), lg.to(dev))
     assert torch.equal(out_inf.view(torch.int16), out.view(torch.int16))
