@@ -11,8 +11,9 @@
 //
 // A workgroup of 8 waves owns a 256 (n) x 256 (k) tile of one expert; each
 // wave owns 64 n x 128 k, i.e. 4 x 8 blocks of v_mfma_f32_16x16x128_f8f6f4,
-// one MFMA per 128-row group.  aT rows feed the MFMA's A operand and bT rows its B
-// operand, so an output lane holds one k (lane % 16) and four consecutive n.
+// one MFMA per 128-row group.  bT rows feed the MFMA's A operand and aT rows
+// its B operand, so an output lane holds one n (lane % 16) and four
+// consecutive k, which leave for LDS as one 16-byte write.
 // Both scales vary per row and group, so each partial is multiplied by
 // sa[n,g]*sb[k,g] before accumulation (the product is formed before the
 // MFMA result arrives, leaving one FMA per output after it).  Operands are
@@ -164,32 +165,38 @@ __device__ __forceinline__ void wgrad_tile(const uint8_t* __restrict__ aT,
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(fa[j], fb, acc[i][j], 0, 0,
-                                                                       0, ea[j], 0, eb);
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(fb, fa[j], acc[i][j], 0, 0,
+                                                                       0, eb, 0, ea[j]);
         fb = fbn;
         eb = ebn;
       }
     } else {
       v8i fa[4];
-      v4f sa[4];
+      float sa[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         fa[j] = lds_frag(sA, wn * 64 + j * 16 + frow, fch);
-        const int r = wn * 64 + j * 16 + (lane >> 4) * 4;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) sa[j][v] = sSa[(r + v) * kWChunk];
+        sa[j] = sSa[(wn * 64 + j * 16 + frow) * kWChunk];
       }
-      // the next row block's fragment and scale are read before this block's
-      // MFMAs are issued, so their LDS latency hides behind them
+      // the next row block's fragment and scales are read before this
+      // block's MFMAs are issued, so their LDS latency hides behind them;
+      // a lane's 4 outputs are 4 consecutive k, each with its own bT scale
+      const int kq0 = wk * 128 + (lane >> 4) * 4;
+      auto sb_of = [&](int i) {
+        v4f r;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) r[v] = sSb[(kq0 + i * 16 + v) * kWChunk];
+        return r;
+      };
       v8i fb = lds_frag(sB, kr0, fch);
-      float sb = sSb[kr0 * kWChunk];
+      v4f sb = sb_of(0);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         v8i fbn = fb;
-        float sbn = sb;
+        v4f sbn = sb;
         if (i + 1 < 8) {
           fbn = lds_frag(sB, kr0 + (i + 1) * 16, fch);
-          sbn = sSb[(kr0 + (i + 1) * 16) * kWChunk];
+          sbn = sb_of(i + 1);
         }
         // the scale products do not depend on the MFMA results: computing
         // them first leaves one FMA per output after each MFMA
@@ -198,7 +205,7 @@ __device__ __forceinline__ void wgrad_tile(const uint8_t* __restrict__ aT,
         for (int j = 0; j < 4; ++j) sab[j] = sa[j] * sb;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const v4f p = mfma16(fa[j], fb, v4f{0.0f, 0.0f, 0.0f, 0.0f});
+          const v4f p = mfma16(fb, fa[j], v4f{0.0f, 0.0f, 0.0f, 0.0f});
 #pragma unroll
           for (int v = 0; v < 4; ++v) acc[i][j][v] = __builtin_fmaf(p[v], sab[j][v], acc[i][j][v]);
         }
@@ -215,10 +222,11 @@ __device__ __forceinline__ void wgrad_tile(const uint8_t* __restrict__ aT,
   if ((kOut == kOutF32Acc || kOut == kOutBF16Acc) && steps == 0) return;
 
   // Epilogue: the fp32 tile leaves through LDS in two 128-row halves (the
-  // stage buffers are free after the K loop's last barrier).  Lane (i, j, v)
-  // holds dW row n = wn*64 + j*16 + (lane/16)*4 + v, column k = wk*128 +
-  // i*16 + lane%16; with a row pitch of 260 floats the 4 lane groups of a
-  // write land 16 banks apart, so the writes are conflict-free.  Then each
+  // stage buffers are free after the K loop's last barrier).  Lane (i, j)
+  // holds dW row n = wn*64 + j*16 + lane%16, columns k = wk*128 + i*16 +
+  // (lane/16)*4 .. +3, written as one 16-byte word; with a row pitch of 260
+  // floats the 16 rows of a lane group start 4 banks apart, so each group's
+  // 16-byte writes cover all 64 banks once (conflict-free).  Then each
   // wave writes whole rows, 4 columns per lane: fp32 as 16-byte stores,
   // non-temporal (dW is written once here and read by a later kernel), bf16
   // rounded to nearest even as 8-byte stores.  The accumulating modes read
@@ -234,12 +242,10 @@ __device__ __forceinline__ void wgrad_tile(const uint8_t* __restrict__ aT,
 #pragma unroll
       for (int i = 0; i < 8; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const int row = (wn & 1) * 64 + j * 16 + (lane >> 4) * 4 + v;
-            ct[row * kPitch + wk * 128 + i * 16 + frow] = acc[i][j][v];
-          }
+        for (int j = 0; j < 4; ++j) {
+          const int row = (wn & 1) * 64 + j * 16 + frow;
+          *(v4f*)(ct + row * kPitch + wk * 128 + i * 16 + (lane >> 4) * 4) = acc[i][j];
+        }
     }
     __syncthreads();
     for (int r = wid; r < 128; r += 8) {
