@@ -554,8 +554,10 @@ int smoe_unpermute_combine_bwd(const uint16_t* dout, const uint16_t* y, const in
  * row r of dy is rebuilt inside the quantiser as bf16(w[p]*dout[p/K]) with
  * p = row_map[r] (row_map and inv_map inverse permutations of [0, T*K),
  * as smoe_route_sort writes them).  Same bytes as smoe_unpermute_combine_bwd
- * followed by smoe_quant_rows_cols.  Replaces dmerge and the requantisation
- * of its gradient (moe/MoE_detailed_computation_dataflow.md:209-226;
+ * followed by smoe_quant_rows_cols.  With dyTq and dyTs both NULL the
+ * column pass is skipped (pad is still written); smoe_combine_bwd_quant_cols
+ * then gives it, e.g. on another stream.  Replaces dmerge and the
+ * requantisation of its gradient (moe/MoE_detailed_computation_dataflow.md:209-226;
  * moe/MegatronCore_MoE_reading_notes.md:498-501).
  */
 int smoe_unpermute_combine_bwd_quant(const uint16_t* dout, const uint16_t* y,
@@ -564,6 +566,18 @@ int smoe_unpermute_combine_bwd_quant(const uint16_t* dout, const uint16_t* y,
                                      int E, int ld, uint8_t* dyq, float* dys, uint8_t* dyTq,
                                      float* dyTs, int32_t* pad, float* dw, int col_scale,
                                      void* stream);
+
+/*
+ * The column pass of smoe_unpermute_combine_bwd_quant alone: dyTq, dyTs and
+ * pad, the same bytes, from dout, row_map and w (it does not read y or the
+ * row outputs, so it may run beside the row pass).  col_scale is
+ * SMOE_COLSCALE_FP32 or SMOE_COLSCALE_POW2.  Replaces the wgrad half of the
+ * same requantisation (moe/MegatronCore_MoE_reading_notes.md:498-501).
+ */
+int smoe_combine_bwd_quant_cols(const uint16_t* dout, const int32_t* row_map, const float* w,
+                                int T, int K, int H, const int32_t* offsets, int E, int ld,
+                                uint8_t* dyTq, float* dyTs, int32_t* pad, int col_scale,
+                                void* stream);
 
 #ifdef __cplusplus
 }

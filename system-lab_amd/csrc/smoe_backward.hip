@@ -639,6 +639,23 @@ extern "C" int smoe_unpermute_combine_bwd(const uint16_t* dout, const uint16_t* 
   SMOE_RETURN_LAUNCH();
 }
 
+namespace {
+// The 128x1 columns of dy: row r of dy is rebuilt as bf16(w[p] * dout[p / K])
+// with p = row_map[r].
+void combine_bwd_cols_launch(const uint16_t* dout, const int32_t* row_map, const float* w, int K,
+                             int R, int H, const int32_t* offsets, int E, int ld, uint8_t* dyTq,
+                             float* dyTs, int32_t* pad, bool p2, hipStream_t s) {
+#define SMOE_CQ(P2)                                                                          \
+  quant_cols_kernel<false, false, P2><<<dim3((H + kQcCols - 1) / kQcCols, ld / kGroup), dim3(256), \
+                                        0, s>>>(dout, row_map, K, w, R, H, offsets, pad, E, ld,  \
+                                                dyTq, dyTs, nullptr, nullptr, nullptr, nullptr,  \
+                                                nullptr)
+  if (p2) SMOE_CQ(true);
+  else SMOE_CQ(false);
+#undef SMOE_CQ
+}
+}  // namespace
+
 extern "C" int smoe_unpermute_combine_bwd_quant(const uint16_t* dout, const uint16_t* y,
                                                 const int32_t* inv_map, const int32_t* row_map,
                                                 const float* w, int T, int K, int H,
@@ -658,8 +675,11 @@ extern "C" int smoe_unpermute_combine_bwd_quant(const uint16_t* dout, const uint
   if (ld / kGroup > 65535) return SMOE_EINVAL_DIM;
   SMOE_CHECK_PTR(dout);
   SMOE_CHECK_PTR(y);
-  SMOE_CHECK_PTR(dyTq);
-  if (!inv_map || !row_map || !w || !dw || !offsets || !dys || !dyTs || !pad || !dyq)
+  // dyTq and dyTs both NULL: no column pass (smoe_combine_bwd_quant_cols
+  // runs it separately)
+  const bool cols = dyTq || dyTs;
+  if (cols) SMOE_CHECK_PTR(dyTq);
+  if (!inv_map || !row_map || !w || !dw || !offsets || !dys || (cols && !dyTs) || !pad || !dyq)
     return SMOE_EINVAL_NULL;
   if (((uintptr_t)inv_map | (uintptr_t)row_map | (uintptr_t)w | (uintptr_t)dw |
        (uintptr_t)offsets | (uintptr_t)dys | (uintptr_t)dyTs | (uintptr_t)pad) & 3u)
@@ -682,14 +702,33 @@ extern "C" int smoe_unpermute_combine_bwd_quant(const uint16_t* dout, const uint
   }
 #undef SMOE_CBB
   pad_offsets_kernel<<<1, 1024, 0, s>>>(offsets, E, pad);
-  // 128x1 columns: row r of dy is rebuilt as bf16(w[p] * dout[p / K]) with
-  // p = row_map[r]
-#define SMOE_CQ(P2)                                                                    \
-  quant_cols_kernel<false, false, P2><<<dim3((H + kQcCols - 1) / kQcCols, ld / kGroup), dim3(256), 0, \
-                                        s>>>(dout, row_map, K, w, R, H, offsets, pad, E, ld, dyTq,   \
-                                             dyTs, nullptr, nullptr, nullptr, nullptr, nullptr)
-  if (cp2) SMOE_CQ(true);
-  else SMOE_CQ(false);
-#undef SMOE_CQ
+  if (cols) combine_bwd_cols_launch(dout, row_map, w, K, R, H, offsets, E, ld, dyTq, dyTs, pad, cp2, s);
+  SMOE_RETURN_LAUNCH();
+}
+
+extern "C" int smoe_combine_bwd_quant_cols(const uint16_t* dout, const int32_t* row_map,
+                                           const float* w, int T, int K, int H,
+                                           const int32_t* offsets, int E, int ld, uint8_t* dyTq,
+                                           float* dyTs, int32_t* pad, int col_scale,
+                                           void* stream) {
+  if (T <= 0 || H <= 0) return SMOE_EINVAL_DIM;
+  if (col_scale & ~SMOE_COLSCALE_POW2) return SMOE_EINVAL_MODE;
+  if (H % kLane) return SMOE_EINVAL_ALIGN128;
+  if (K <= 0 || K > 32) return SMOE_EINVAL_TOPK;
+  if ((long long)T * K > 0x7fffffffLL) return SMOE_EINVAL_DIM;
+  if (E <= 0 || E > SMOE_MAX_EXPERTS) return SMOE_EINVAL_EXPERTS;
+  const int R = T * K;
+  if (ld < smoe_quant_cols_ld(R, E) || ld % kGroup) return SMOE_EINVAL_DIM;
+  if (ld / kGroup > 65535) return SMOE_EINVAL_DIM;
+  SMOE_CHECK_PTR(dout);
+  SMOE_CHECK_PTR(dyTq);
+  if (!row_map || !w || !offsets || !dyTs || !pad) return SMOE_EINVAL_NULL;
+  if (((uintptr_t)row_map | (uintptr_t)w | (uintptr_t)offsets | (uintptr_t)dyTs |
+       (uintptr_t)pad) & 3u)
+    return SMOE_EINVAL_PTRALIGN;
+  hipStream_t s = (hipStream_t)stream;
+  pad_offsets_kernel<<<1, 1024, 0, s>>>(offsets, E, pad);
+  combine_bwd_cols_launch(dout, row_map, w, K, R, H, offsets, E, ld, dyTq, dyTs, pad,
+                          col_scale & SMOE_COLSCALE_POW2, s);
   SMOE_RETURN_LAUNCH();
 }

@@ -68,6 +68,8 @@ SIGNATURES = {
     "smoe_unpermute_combine_bwd": (c_int, [P, P, P, P, c_int, c_int, c_int, P, P, P]),
     "smoe_unpermute_combine_bwd_quant": (c_int, [P, P, P, P, P, c_int, c_int, c_int, P, c_int,
                                                  c_int, P, P, P, P, P, P, c_int, P]),
+    "smoe_combine_bwd_quant_cols": (c_int, [P, P, P, c_int, c_int, c_int, P, c_int, c_int, P, P,
+                                            P, c_int, P]),
 }
 
 

@@ -376,6 +376,7 @@ class SimpleMoE(nn.Module):
                                                                 device=dout.device)
         dw2 = dw2_into if dw2_into is not None else torch.empty((E, H, I), dtype=wgrad_dtype,
                                                                 device=dout.device)
+        dout = dout.contiguous()
         side.wait_stream(main)
         with torch.cuda.stream(side):
             # the wgrad activation operands depend on the forward only: h, and
@@ -383,15 +384,17 @@ class SimpleMoE(nn.Module):
             hTq, hTs, _, _ = ops.quant_cols(inter["h"], off, col_scale=cs)
             xTq, xTs, _, _ = ops.quant_cols(inter["x"], off, gather=inter["row_map"], gather_div=K,
                                             col_scale=cs)
-        # combine backward fused with both quantisations of dy (1x128 rows for
-        # dgrad, 128x1 columns for wgrad); dy itself is never stored
-        dyq, dys, dyTq, dyTs, pad, ld, dw = ops.unpermute_combine_bwd_quant(
-            dout.contiguous(), inter["y"], inv, inter["row_map"], inter["topk_w"], off, col_scale=cs,
-            row_scale=rs)
-        side.wait_stream(main)
+        # combine backward fused with dy's 1x128 row quantisation for the
+        # dgrad; the 128x1 columns for the wgrad (rebuilt from dout, not from
+        # the row pass) on the side stream; dy itself is never stored
         with torch.cuda.stream(side):
+            dyTq, dyTs, pad, ld = ops.combine_bwd_quant_cols(dout, inter["row_map"],
+                                                             inter["topk_w"], off, col_scale=cs)
             ops.grouped_gemm_fp8_wgrad(dyTq, dyTs, hTq, hTs, pad, ld, out=dw2,
                                        accumulate=dw2_into is not None, e8m0=e8m0)
+        dyq, dys, _, _, _, _, dw = ops.unpermute_combine_bwd_quant(
+            dout, inter["y"], inv, inter["row_map"], inter["topk_w"], off, col_scale=cs,
+            row_scale=rs, cols=False)
         dh = ops.grouped_gemm_fp8(dyq, dys, w2tq, w2ts, off, e8m0=e8)
         # SwiGLU backward fused with both quantisations of dc1 (dc1 itself is
         # never stored)

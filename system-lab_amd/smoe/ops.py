@@ -722,11 +722,13 @@ def unpermute_combine_bwd(dout: torch.Tensor, y: torch.Tensor, inv_map: torch.Te
 def unpermute_combine_bwd_quant(dout: torch.Tensor, y: torch.Tensor, inv_map: torch.Tensor,
                                 row_map: torch.Tensor, topk_w: torch.Tensor,
                                 offsets: torch.Tensor, col_scale: str = "fp32",
-                                row_scale: str = "amax"):
+                                row_scale: str = "amax", cols: bool = True):
     """Combine backward fused with both quantisations of dy: the bytes of
     ``quant_rows_cols(unpermute_combine_bwd(...)[0], offsets, col_scale,
     row_scale)`` and dw, without storing dy.  -> (dyq [T*K,pad128(H)] fp8,
-    dys, dyTq [H,ld] fp8, dyTs, pad, ld, dw [T,K] f32)."""
+    dys, dyTq [H,ld] fp8, dyTs, pad, ld, dw [T,K] f32).  ``cols=False``
+    skips the column pass (dyTq, dyTs are None); ``combine_bwd_quant_cols``
+    gives it on its own."""
     mode = _fused_scale(col_scale, row_scale)
     _check(dout, "dout", (torch.bfloat16,), 2)
     _check(y, "y", (torch.bfloat16,), 2)
@@ -746,11 +748,39 @@ def unpermute_combine_bwd_quant(dout: torch.Tensor, y: torch.Tensor, inv_map: to
     dev = dout.device
     dyq = torch.empty((R, pad128(H)), dtype=FP8, device=dev)
     dys = torch.empty((R, nblocks(H)), dtype=torch.float32, device=dev)
-    dyTq = torch.empty((H, ld), dtype=FP8, device=dev)
-    dyTs = torch.empty((H, ld // GROUP), dtype=torch.float32, device=dev)
+    dyTq = torch.empty((H, ld), dtype=FP8, device=dev) if cols else None
+    dyTs = torch.empty((H, ld // GROUP), dtype=torch.float32, device=dev) if cols else None
     pad = torch.empty(E + 1, dtype=torch.int32, device=dev)
     dw = torch.empty((T, K), dtype=torch.float32, device=dev)
     _C.call("smoe_unpermute_combine_bwd_quant", _ptr(dout), _ptr(y), _ptr(inv_map),
             _ptr(row_map), _ptr(topk_w), T, K, H, _ptr(offsets), E, ld, _ptr(dyq), _ptr(dys),
             _ptr(dyTq), _ptr(dyTs), _ptr(pad), _ptr(dw), mode, _stream())
     return dyq, dys, dyTq, dyTs, pad, ld, dw
+
+
+def combine_bwd_quant_cols(dout: torch.Tensor, row_map: torch.Tensor, topk_w: torch.Tensor,
+                           offsets: torch.Tensor, col_scale: str = "fp32"):
+    """The column pass of ``unpermute_combine_bwd_quant`` alone (dy's 128x1
+    columns rebuilt from dout, row_map and topk_w; y is not read):
+    -> (dyTq [H,ld] fp8, dyTs, pad, ld), the same bytes."""
+    mode = _col_scale(col_scale)
+    _check(dout, "dout", (torch.bfloat16,), 2)
+    _check(row_map, "row_map", (torch.int32,))
+    _check(topk_w, "topk_w", (torch.float32,), 2)
+    _check(offsets, "offsets", (torch.int32,), 1)
+    T, K = topk_w.shape
+    H = dout.shape[1]
+    R = T * K
+    if dout.shape[0] != T:
+        raise ValueError("dout must be [T, H] for topk_w [T, K]")
+    if row_map.numel() != R:
+        raise ValueError("row_map must hold T*K entries")
+    E = offsets.numel() - 1
+    ld = int(_C.lib().smoe_quant_cols_ld(R, E))
+    dev = dout.device
+    dyTq = torch.empty((H, ld), dtype=FP8, device=dev)
+    dyTs = torch.empty((H, ld // GROUP), dtype=torch.float32, device=dev)
+    pad = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    _C.call("smoe_combine_bwd_quant_cols", _ptr(dout), _ptr(row_map), _ptr(topk_w), T, K, H,
+            _ptr(offsets), E, ld, _ptr(dyTq), _ptr(dyTs), _ptr(pad), mode, _stream())
+    return dyTq, dyTs, pad, ld

@@ -168,6 +168,19 @@ def test_remaining_entry_points_reject():
     assert cq(*args(E=0)) == -4
     assert cq(*args(ld=ld2 - 128)) == -2
     assert cq(*args(rm=None)) == -1
+    # dyTq and dyTs both NULL skip the column pass; only one of them NULL is an error
+    one_null = list(args()); one_null[13] = None
+    assert cq(*one_null) == -1
+    # its column pass alone: the same checks, the column bit only
+    cc = lib.smoe_combine_bwd_quant_cols
+    cargs = lambda T=500, K=2, H=128, E=4, ld=ld2, rm=FAKE, mode=0: (
+        FAKE, rm, FAKE, T, K, H, FAKE, E, ld, FAKE, FAKE, FAKE, mode, None)
+    assert cc(*cargs(H=130)) == -3
+    assert cc(*cargs(K=33)) == -7
+    assert cc(*cargs(E=0)) == -4
+    assert cc(*cargs(ld=ld2 - 128)) == -2
+    assert cc(*cargs(rm=None)) == -1
+    assert cc(*cargs(mode=2)) == -8 and cc(*cargs(mode=-1)) == -8
     # a column-scale rule other than SMOE_COLSCALE_FP32 / _POW2
     assert q(FAKE, None, 1, 1000, 128, FAKE, 4, ld, FAKE, FAKE, FAKE, 2, None) == -8
     assert rc(FAKE, 1000, 128, FAKE, 4, ld, FAKE, FAKE, FAKE, FAKE, FAKE, -1, None) == -8

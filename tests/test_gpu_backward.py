@@ -209,6 +209,18 @@ def test_combine_bwd_quant_equals_two_kernels(dev, T, K, H, E):
     assert torch.equal(got[3][:, :Rp // 128].view(torch.int32), ref[3][:, :Rp // 128].view(torch.int32))
     assert torch.equal(got[4], ref[4]) and got[5] == ref[5]
     assert torch.equal(got[6].view(torch.int32), dw.view(torch.int32))
+    # the row pass alone (cols=False) and the column pass alone give the same bytes
+    rows = ops.unpermute_combine_bwd_quant(dv, yv, im, rm, wv, off_t, cols=False)
+    assert rows[2] is None and rows[3] is None
+    for a_, b_ in ((rows[0], got[0]), (rows[1], got[1]), (rows[4], got[4]), (rows[6], got[6])):
+        assert torch.equal(a_.view(torch.uint8), b_.view(torch.uint8))
+    for cs in ("fp32", "pow2"):
+        full = ops.unpermute_combine_bwd_quant(dv, yv, im, rm, wv, off_t, col_scale=cs)
+        cq, cs_, cpad, cld = ops.combine_bwd_quant_cols(dv, rm, wv, off_t, col_scale=cs)
+        assert cld == full[5] and torch.equal(cpad, full[4])
+        assert torch.equal(cq.view(torch.uint8)[:, :Rp], full[2].view(torch.uint8)[:, :Rp])
+        assert torch.equal(cs_[:, :Rp // 128].view(torch.int32),
+                           full[3][:, :Rp // 128].view(torch.int32))
     # dy rows from the oracle's combine backward, quantised by the oracle
     ody, odw = O.combine_bwd(u16(dout), u16(y), inv_map, w.numpy(), K)
     rq, rs = O.quant_1x128(O.bf16_to_f32(ody))
