@@ -49,22 +49,26 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def timed(fn, iters, warmup):
+def timed(fn, iters, warmup, blocks=3):
     """Mean ms per call over ``iters`` back-to-back calls on the current
     stream, bracketed by HIP events recorded on that stream (the stream the
-    kernels use).  Inputs may stay in L2 / the last-level cache between
-    calls: reported as the warm figure only."""
+    kernels use); the median over ``blocks`` such runs, so that a one-off
+    host stall in one run does not set the figure.  Inputs may stay in L2 /
+    the last-level cache between calls: reported as the warm figure only."""
     import torch
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s.record()
-    for _ in range(iters):
-        fn()
-    e.record()
-    torch.cuda.synchronize()
-    return s.elapsed_time(e) / iters
+    means = []
+    for _ in range(blocks):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(iters):
+            fn()
+        e.record()
+        torch.cuda.synchronize()
+        means.append(s.elapsed_time(e) / iters)
+    return sorted(means)[len(means) // 2]
 
 
 class Flush:
