@@ -21,6 +21,9 @@
 // grouped GEMM; both scale vectors are staged 8 row groups at a time.
 #include "smoe_mfma.h"
 
+#include <algorithm>
+#include <atomic>
+
 namespace smoe {
 
 // Tile: 256 (n, aT rows) x 256 (k, bT rows) per workgroup of 8 waves in a
@@ -355,9 +358,9 @@ __global__ __launch_bounds__(kWThreads, 1) void grouped_gemm_fp8_wgrad_kernel(
   const int xcd = blockIdx.x & 7, j = blockIdx.x >> 3;
   // XCD x's range [T_x, T_x+1) starts at the tile where its cost share
   // starts; every workgroup computes it the same way.  Workgroup j of the
-  // XCD takes tiles T_x + j, T_x + j + per_xcd, ... (a range with more
-  // tiles than workgroups, i.e. cheap tiles, loops).  Scalar registers keep
-  // the loop off the tile body's VGPRs.
+  // XCD takes tiles T_x + j, T_x + j + per_xcd, ... (the launch gives each
+  // XCD one workgroup per CU, so every workgroup walks its share of the
+  // range).  Scalar registers keep the loop off the tile body's VGPRs.
   const int t_begin = __builtin_amdgcn_readfirstlane(xcd == 0 ? 0 : (int)first_tile(W * xcd / 8));
   const int t_end =
       __builtin_amdgcn_readfirstlane(xcd == 7 ? E * TE : (int)first_tile(W * (xcd + 1) / 8));
@@ -369,6 +372,29 @@ __global__ __launch_bounds__(kWThreads, 1) void grouped_gemm_fp8_wgrad_kernel(
                      dW);
     __syncthreads();  // the next tile reuses the LDS
   }
+}
+
+// Compute units per XCD of the current device, looked up once per device.
+constexpr int kMaxDevices = 64;
+static std::atomic<int> g_cus_per_xcd[kMaxDevices];
+
+static int cus_per_xcd(hipError_t* err) {
+  int dev = 0;
+  *err = hipGetDevice(&dev);
+  if (*err != hipSuccess) return 0;
+  if (dev < 0 || dev >= kMaxDevices) {
+    *err = hipErrorInvalidDevice;
+    return 0;
+  }
+  int n = g_cus_per_xcd[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    int cus = 0;
+    *err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (*err != hipSuccess) return 0;
+    n = cus / 8 > 0 ? cus / 8 : 1;
+    g_cus_per_xcd[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
 }
 
 }  // namespace smoe
@@ -393,11 +419,15 @@ extern "C" int smoe_grouped_gemm_fp8_wgrad_ex(const uint8_t* aT, const float* aT
   SMOE_CHECK_PTR(dW);
   if (!aTs || !bTs || !pad) return SMOE_EINVAL_NULL;
   if (((uintptr_t)aTs | (uintptr_t)bTs | (uintptr_t)pad) & 3u) return SMOE_EINVAL_PTRALIGN;
-  // per_xcd workgroups per XCD, one tile each on average; a range with
-  // more tiles (cheap tiles) loops
+  // One workgroup per CU (the kernel's LDS allows one), per_xcd of them on
+  // each XCD, each walking its XCD's tile range with stride per_xcd: the
+  // cost table is built once per workgroup instead of once per tile, and
+  // no workgroup is launched per tile.
+  hipError_t herr = hipSuccess;
+  const int cus = cus_per_xcd(&herr);
+  if (herr != hipSuccess) return (int)herr;
   const long long tiles = (long long)E * ((Kdim + kWK - 1) / kWK) * ((N + kWN - 1) / kWN);
-  const long long per_xcd = (tiles + 7) / 8;
-  if (per_xcd * 8 > 0x7fffffffLL) return SMOE_EINVAL_DIM;
+  const long long per_xcd = std::min<long long>((tiles + 7) / 8, cus);
   const dim3 grid((unsigned)(per_xcd * 8)), block(kWThreads);
   hipStream_t s = (hipStream_t)stream;
 #define SMOE_WG(M, P2)                                                                   \
