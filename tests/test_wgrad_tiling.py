@@ -4,7 +4,8 @@
 steps(e) + 4 row-group steps; the sequence is cut into 8 contiguous ranges
 of about equal cost; workgroup b (XCD b%8, index j = b//8) runs tiles
 T_x + j, T_x + j + per_xcd, ... of its XCD's range, per_xcd =
-ceil(tiles / 8).  Checked without a GPU: every (expert, n-tile, k-tile) is
+min(ceil(tiles / 8), CUs per XCD) (the launch: one workgroup per CU).
+Checked without a GPU: every (expert, n-tile, k-tile) is
 produced exactly once for valid and malformed pad[], each XCD's tiles are a
 contiguous run (so an expert's tiles stay together), and under Zipf loads
 the most loaded XCD carries close to 1/8 of the work where the earlier
@@ -23,9 +24,9 @@ def _costs(pad, E, ld, TE):
     return TE * (steps + FIXED), steps
 
 
-def wgrad_tiles(pad, N, Kd, ld):
+def wgrad_tiles(pad, N, Kd, ld, cus_per_xcd=32):
     """-> list of (block, xcd, e, n0, k0) and per-XCD cost, following the
-    kernel's integer arithmetic."""
+    kernel's integer arithmetic and the launch's grid."""
     E = len(pad) - 1
     KT, NT = -(-Kd // WK), -(-N // WN)
     TE = KT * NT
@@ -33,7 +34,7 @@ def wgrad_tiles(pad, N, Kd, ld):
     cpre = np.concatenate([[0], np.cumsum(cost)])
     W = int(cpre[-1])
     total = E * TE
-    per_xcd = -(-total // 8)
+    per_xcd = min(-(-total // 8), cus_per_xcd)
 
     def first_tile(c):
         lo = int(np.searchsorted(cpre, c, side="right") - 1)
@@ -63,11 +64,12 @@ CASES = [([130, 0, 5, 256, 1], 128, 128), ([1000] * 11, 384, 640), ([1024] * 128
          ([0] * 4, 256, 256), ([50000, 10, 0, 7000, 0, 0, 3], 512, 768)]
 
 
+@pytest.mark.parametrize("cus", [32, 1, 5, 1 << 20])
 @pytest.mark.parametrize("counts,N,Kd", CASES)
-def test_every_wgrad_tile_once(counts, N, Kd):
+def test_every_wgrad_tile_once(counts, N, Kd, cus):
     pad = _pad_from_counts(counts)
     E = len(counts)
-    tiles, _, bounds = wgrad_tiles(pad, N, Kd, int(pad[-1]) or 128)
+    tiles, _, bounds = wgrad_tiles(pad, N, Kd, int(pad[-1]) or 128, cus)
     KT, NT = -(-Kd // WK), -(-N // WN)
     assert bounds[-1] == E * NT * KT and all(b1 >= b0 for b0, b1 in zip(bounds, bounds[1:]))
     seen = [(e, n0, k0) for _, _, e, n0, k0 in tiles]
@@ -81,7 +83,7 @@ def test_malformed_pad_still_covers_every_tile(seed):
     E = int(rng.integers(1, 40))
     pad = np.sort(rng.integers(-500, 5000, E + 1)) if seed % 2 else rng.integers(-500, 5000, E + 1)
     ld = 4096
-    tiles, _, _ = wgrad_tiles(pad, 512, 384, ld)
+    tiles, _, _ = wgrad_tiles(pad, 512, 384, ld, 1 + seed % 4)
     seen = [(e, n0, k0) for _, _, e, n0, k0 in tiles]
     assert len(set(seen)) == len(seen) == E * 2 * 2
 
