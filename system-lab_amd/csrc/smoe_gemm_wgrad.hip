@@ -423,10 +423,11 @@ extern "C" int smoe_grouped_gemm_fp8_wgrad_ex(const uint8_t* aT, const float* aT
   // each XCD, each walking its XCD's tile range with stride per_xcd: the
   // cost table is built once per workgroup instead of once per tile, and
   // no workgroup is launched per tile.
+  const long long tiles = (long long)E * ((Kdim + kWK - 1) / kWK) * ((N + kWN - 1) / kWN);
+  if (tiles > 0x7fffffffLL) return SMOE_EINVAL_DIM;  // the kernel numbers tiles in int
   hipError_t herr = hipSuccess;
   const int cus = cus_per_xcd(&herr);
   if (herr != hipSuccess) return (int)herr;
-  const long long tiles = (long long)E * ((Kdim + kWK - 1) / kWK) * ((N + kWN - 1) / kWN);
   const long long per_xcd = std::min<long long>((tiles + 7) / 8, cus);
   const dim3 grid((unsigned)(per_xcd * 8)), block(kWThreads);
   hipStream_t s = (hipStream_t)stream;
