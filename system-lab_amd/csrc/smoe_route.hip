@@ -13,11 +13,15 @@
 //   2. route_rowscan — one wave per expert: exclusive scan of hist[e][:] in
 //                    place (the expert's rows that earlier segments own) and
 //                    counts[e]
-//   3. route_rank  — every workgroup scans counts into offsets in LDS; each
-//                    wave then walks its segment in pair order, 64 pairs at a
-//                    time (ids prefetched into registers); lanes with equal
-//                    expert ids are found with one ballot per id bit, so the
-//                    rank inside a chunk is a popcount of lower matching lanes.
+//   3. route_rank  — every workgroup scans counts into offsets in LDS; a
+//                    wave then walks pairs in order, 64 at a time (ids
+//                    prefetched into registers); lanes with equal expert ids
+//                    are found with one ballot per id bit, so the rank inside
+//                    a chunk is a popcount of lower matching lanes.  The
+//                    stand-alone sort gives each 512-pair segment a workgroup
+//                    (route_rank_wg: a wave per quarter, combined through
+//                    per-wave expert counts in LDS); the fused router path
+//                    gives each 128-pair segment a wave (route_rank).
 //                    Order is stable and no global atomics are used.
 // A pair whose id lies outside [0, E) gets no row: inv_map[p] = -1, and the
 // number of such pairs is written to the status word at the head of the
@@ -546,6 +550,102 @@ __global__ __launch_bounds__(256) void route_rank_kernel(const int32_t* __restri
   }
 }
 
+// The rank pass with one workgroup per segment: wave w ranks pairs
+// w*kSegT/4 .. +kSegT/4 of the segment in 64-pair chunks as
+// route_rank_kernel does, counting per expert in LDS; after a barrier a
+// pair's row is offs[e] + rowpre[e][seg] + the counts of expert e in the
+// waves before it + its rank inside its wave.  Same rows as
+// route_rank_kernel<kSegT> (order by pair index), four times the
+// workgroups.
+template <int kSegT>
+__global__ __launch_bounds__(256) void route_rank_wg_kernel(const int32_t* __restrict__ idx,
+                                                            const int32_t* __restrict__ rowpre,
+                                                            const int32_t* __restrict__ counts,
+                                                            int R, int E, int nseg, int nbits,
+                                                            int32_t* __restrict__ offsets,
+                                                            int32_t* __restrict__ row_map,
+                                                            int32_t* __restrict__ inv_map,
+                                                            int32_t* __restrict__ status) {
+  extern __shared__ int32_t c_lds[];  // base[E] then cnt[4][E]
+  __shared__ int32_t wtot[4];
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int seg = blockIdx.x;
+  int32_t* base = c_lds;
+  int32_t* cnt = c_lds + E;
+  constexpr int kPW = kSegT / 4;      // pairs per wave
+  constexpr int kPL = kPW / kWave;    // 64-pair chunks per wave
+  const int p0 = seg * kSegT + w * kPW;
+  // every load issued first: this wave's ids, this thread's experts' counts
+  // and segment prefixes
+  int v[kPL];
+#pragma unroll
+  for (int i = 0; i < kPL; ++i) {
+    const int p = p0 + i * kWave + lane;
+    v[i] = p < R ? idx[p] : E;  // E is a sentinel id no valid lane has
+  }
+  const int per = (E + 255) / 256;
+  int loc[4], pre[4], run = 0;
+  for (int i = 0; i < per; ++i) {
+    const int e = tid * per + i;
+    run += e < E ? counts[e] : 0;
+    loc[i] = run;
+    pre[i] = e < E ? rowpre[(size_t)e * nseg + seg] : 0;
+  }
+  for (int e = tid; e < 4 * E; e += 256) cnt[e] = 0;
+  // offsets = exclusive scan of counts; base[e] = offsets[e] + rowpre[e][seg]
+  const int inc = wave_incl_scan(run, lane);
+  if (lane == kWave - 1) wtot[w] = inc;
+  __syncthreads();
+  int b0 = inc - run;
+  for (int j = 0; j < w; ++j) b0 += wtot[j];
+  for (int i = 0; i < per; ++i) {
+    const int e = tid * per + i;
+    if (e < E) {
+      const int ex = b0 + (i ? loc[i - 1] : 0);
+      base[e] = ex + pre[i];
+      if (blockIdx.x == 0) offsets[e] = ex;
+    }
+  }
+  if (blockIdx.x == 0 && tid == 0) {
+    const int total = wtot[0] + wtot[1] + wtot[2] + wtot[3];
+    offsets[E] = total;
+    *status = R - total;  // pairs dropped for an id outside [0, E)
+  }
+  // ranks inside this wave's pairs
+  int32_t* mycnt = cnt + w * E;
+  const uint64_t lt = (1ull << lane) - 1ull;
+  int rl[kPL];
+#pragma unroll
+  for (int i = 0; i < kPL; ++i) {
+    const bool valid = (unsigned)v[i] < (unsigned)E;
+    const int e = valid ? v[i] : E;
+    uint64_t m = ~0ull;
+    for (int b = 0; b < nbits; ++b) {
+      const bool bit = (e >> b) & 1;
+      const uint64_t bal = __ballot(bit);
+      m &= bit ? bal : ~bal;
+    }
+    rl[i] = valid ? mycnt[e] + __popcll(m & lt) : 0;
+    __builtin_amdgcn_wave_barrier();
+    if (valid && (m & lt) == 0) mycnt[e] += __popcll(m);
+    __builtin_amdgcn_wave_barrier();
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kPL; ++i) {
+    const int p = p0 + i * kWave + lane;
+    if ((unsigned)v[i] < (unsigned)E) {
+      const int e = v[i];
+      int r = base[e] + rl[i];
+      for (int j = 0; j < w; ++j) r += cnt[j * E + e];
+      row_map[r] = p;
+      inv_map[p] = r;
+    } else if (p < R) {
+      inv_map[p] = -1;
+    }
+  }
+}
+
 static inline int seg_count(int R, int seg = kSeg) { return (R + seg - 1) / seg; }
 
 }  // namespace smoe
@@ -673,7 +773,11 @@ extern "C" int smoe_route_sort(const int32_t* topk_idx, int T, int K, int E, int
   hipStream_t s = (hipStream_t)stream;
   route_hist_kernel<<<dim3((nseg + 3) / 4), dim3(256), (size_t)4 * E * sizeof(int32_t), s>>>(
       topk_idx, R, E, nseg, hist);
-  sort_tail<kSeg>(topk_idx, R, E, nseg, row_map, inv_map, counts, offsets, ws, s);
+  int nbits = 1;
+  while ((1 << nbits) <= E) ++nbits;  // ids 0..E (E is the sentinel)
+  route_rowscan_kernel<<<dim3((E + 3) / 4), dim3(256), 0, s>>>(hist, E, nseg, counts);
+  route_rank_wg_kernel<kSeg><<<dim3(nseg), dim3(256), (size_t)5 * E * sizeof(int32_t), s>>>(
+      topk_idx, hist, counts, R, E, nseg, nbits, offsets, row_map, inv_map, (int32_t*)ws);
   SMOE_RETURN_LAUNCH();
 }
 
