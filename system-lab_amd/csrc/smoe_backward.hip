@@ -178,7 +178,7 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(
 #pragma unroll
         for (int i = 1; i < 8; ++i) am = (j == i) ? rmax[i] : am;
         const float sc = scale_of<kRowPow2>(am);
-        const QDiv qd = qdiv_setup(sc);
+        const QDiv qd = qdiv_setup_t<kRowPow2>(sc);
         const int r = rg * 8 + j;
         row_m[r] = qd.m;
         row_r[r] = qd.r;
@@ -193,7 +193,7 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(
     if (t < kQcCols) {
       const float am = fmaxf(fmaxf(wmax[0][t], wmax[1][t]), fmaxf(wmax[2][t], wmax[3][t]));
       const float sc = scale_of<kPow2>(am);
-      const QDiv qd = qdiv_setup(sc);
+      const QDiv qd = qdiv_setup_t<kPow2>(sc);
       col_m[t] = qd.m;
       col_r[t] = qd.r;
       col_e[t] = qd.e;
@@ -217,7 +217,7 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const uint32_t wd = (i & 1) ? (v[j][i >> 1] & 0xffff0000u) : (v[j][i >> 1] << 16);
-        qv[j] = quot_bf16(__uint_as_float(wd), d[i]);
+        qv[j] = quot_t<kPow2>(__uint_as_float(wd), d[i]);
       }
       const uint32_t b[2] = {e4m3_pack4(qv[0], qv[1], qv[2], qv[3]),
                              e4m3_pack4(qv[4], qv[5], qv[6], qv[7])};
@@ -237,8 +237,8 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(
         const uint32_t wd[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          qv[2 * i] = quot_bf16(__uint_as_float(wd[i] << 16), rd);
-          qv[2 * i + 1] = quot_bf16(__uint_as_float(wd[i] & 0xffff0000u), rd);
+          qv[2 * i] = quot_t<kRowPow2>(__uint_as_float(wd[i] << 16), rd);
+          qv[2 * i + 1] = quot_t<kRowPow2>(__uint_as_float(wd[i] & 0xffff0000u), rd);
         }
         *(uint2*)(qr + (size_t)(row0 + r) * pad128(C) + c0 + cc) =
             make_uint2(e4m3_pack4(qv[0], qv[1], qv[2], qv[3]), e4m3_pack4(qv[4], qv[5], qv[6], qv[7]));
@@ -464,12 +464,12 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(
           m = fmaxf(m, fabsf(__uint_as_float(o[i] & 0xffff0000u)));
         }
         const float sc = scale_of<kRowPow2>(row16_max(m));
-        const QDiv qd = qdiv_setup(sc);
+        const QDiv qd = qdiv_setup_t<kRowPow2>(sc);
         float qv[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          qv[2 * i] = quot_bf16(__uint_as_float(o[i] << 16), qd);
-          qv[2 * i + 1] = quot_bf16(__uint_as_float(o[i] & 0xffff0000u), qd);
+          qv[2 * i] = quot_t<kRowPow2>(__uint_as_float(o[i] << 16), qd);
+          qv[2 * i + 1] = quot_t<kRowPow2>(__uint_as_float(o[i] & 0xffff0000u), qd);
         }
         *(uint2*)(dyq + (size_t)r[k] * Hp + col) =
             make_uint2(e4m3_pack4(qv[0], qv[1], qv[2], qv[3]), e4m3_pack4(qv[4], qv[5], qv[6], qv[7]));

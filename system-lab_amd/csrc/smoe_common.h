@@ -132,6 +132,29 @@ __device__ __forceinline__ float quot_bf16(float x, const QDiv& d) {
   return __uint_as_float((__float_as_uint(y) & 0x7fffffffu) | (__float_as_uint(x) & 0x80000000u));
 }
 
+// The same set-up and quotient by scale rule.  A power-of-two scale s
+// (kPow2, the E8M0 recipe) has an exact reciprocal 1/s (s in [2^-127,
+// 2^127]), so x * (1/s) is the IEEE quotient x / s itself: one multiply.
+// Quotients in fp32's subnormal range are far below e4m3's smallest step
+// and encode as a signed zero either way.
+template <bool kPow2>
+__device__ __forceinline__ QDiv qdiv_setup_t(float s) {
+  if constexpr (kPow2) {
+    QDiv d;
+    d.m = 0.0f;
+    d.r = 1.0f / s;
+    d.e = 0;
+    return d;
+  } else {
+    return qdiv_setup(s);
+  }
+}
+template <bool kPow2>
+__device__ __forceinline__ float quot_t(float x, const QDiv& d) {
+  if constexpr (kPow2) return x * d.r;
+  else return quot_bf16(x, d);
+}
+
 // ---------------------------------------------------------------- exp -----
 // exp in fp32: Cody-Waite reduction n = rint(x*log2e),
 // r = fma(-n, LN2_LO, fma(-n, LN2_HI, x)) with LN2_HI holding 16 significant
@@ -283,10 +306,20 @@ __device__ __forceinline__ Q16 quant16(const float (&f)[16]) {
   amax = group_max<8>(amax);
   const float s = scale_of<kPow2>(amax);
   uint32_t w[4];
+  if constexpr (kPow2) {
+    // x * (1/s) is the IEEE quotient for a power-of-two s; the clamp keeps
+    // quot_ieee's handling of NaN
+    const float r = 1.0f / s;
+    auto q = [&](float x) { return fminf(fmaxf(x * r, -kE4M3Max), kE4M3Max); };
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    w[i] = e4m3_pack4(quot_ieee(f[4 * i], s), quot_ieee(f[4 * i + 1], s),
-                      quot_ieee(f[4 * i + 2], s), quot_ieee(f[4 * i + 3], s));
+    for (int i = 0; i < 4; ++i)
+      w[i] = e4m3_pack4(q(f[4 * i]), q(f[4 * i + 1]), q(f[4 * i + 2]), q(f[4 * i + 3]));
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = e4m3_pack4(quot_ieee(f[4 * i], s), quot_ieee(f[4 * i + 1], s),
+                        quot_ieee(f[4 * i + 2], s), quot_ieee(f[4 * i + 3], s));
+  }
   Q16 r;
   r.q = make_uint4(w[0], w[1], w[2], w[3]);
   r.scale = s;
@@ -302,12 +335,12 @@ __device__ __forceinline__ Q16 quant16_bf16(const float (&f)[16]) {
   for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(f[i]));
   amax = group_max<8>(amax);
   const float s = scale_of<kPow2>(amax);
-  const QDiv d = qdiv_setup(s);
+  const QDiv d = qdiv_setup_t<kPow2>(s);
   uint32_t w[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
-    w[i] = e4m3_pack4(quot_bf16(f[4 * i], d), quot_bf16(f[4 * i + 1], d),
-                      quot_bf16(f[4 * i + 2], d), quot_bf16(f[4 * i + 3], d));
+    w[i] = e4m3_pack4(quot_t<kPow2>(f[4 * i], d), quot_t<kPow2>(f[4 * i + 1], d),
+                      quot_t<kPow2>(f[4 * i + 2], d), quot_t<kPow2>(f[4 * i + 3], d));
   Q16 r;
   r.q = make_uint4(w[0], w[1], w[2], w[3]);
   r.scale = s;

@@ -252,15 +252,15 @@ __global__ __launch_bounds__(256) void quant_weight_kernel(const uint16_t* __res
   __syncthreads();
   amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
   const float s = scale_of<kPow2>(amax);
-  const QDiv d = qdiv_setup(s);
+  const QDiv d = qdiv_setup_t<kPow2>(s);
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int ch = j * 256 + threadIdx.x;
     const int row = ch >> 4, col = (ch & 15) * 8;
-    const uint32_t lo = e4m3_pack4(quot_bf16(f[j][0], d), quot_bf16(f[j][1], d),
-                                   quot_bf16(f[j][2], d), quot_bf16(f[j][3], d));
-    const uint32_t hi = e4m3_pack4(quot_bf16(f[j][4], d), quot_bf16(f[j][5], d),
-                                   quot_bf16(f[j][6], d), quot_bf16(f[j][7], d));
+    const uint32_t lo = e4m3_pack4(quot_t<kPow2>(f[j][0], d), quot_t<kPow2>(f[j][1], d),
+                                   quot_t<kPow2>(f[j][2], d), quot_t<kPow2>(f[j][3], d));
+    const uint32_t hi = e4m3_pack4(quot_t<kPow2>(f[j][4], d), quot_t<kPow2>(f[j][5], d),
+                                   quot_t<kPow2>(f[j][6], d), quot_t<kPow2>(f[j][7], d));
     if (r0 + row < N)
       *(uint2*)(wq + ((size_t)e * N + r0 + row) * Kp + k0 + col) = make_uint2(lo, hi);
   }
