@@ -406,14 +406,7 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_fp8_e8m0_kernel(
       }
     }
   } else {
-    constexpr int kChunks = kBN * 2 / 16;
-    const int nchunks = ncols * 2 / 16;
-    for (int idx = tid; idx < rows * kChunks; idx += kThreads) {
-      const int r = idx / kChunks, ch = idx - r * kChunks;
-      if (ch < nchunks)
-        *(uint4*)((uint8_t*)(c + (size_t)(row0 + r) * N + n0) + ch * 16) =
-            *(const uint4*)(ct + r * kCPitch + ch * 16);
-    }
+    store_staged_tile<kThreads, kBM, kBN, kCPitch>(ct, c, row0, rows, N, n0, ncols, tid);
   }
 }
 

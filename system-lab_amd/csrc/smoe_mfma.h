@@ -80,5 +80,32 @@ __device__ __forceinline__ v8i lds_frag(const uint8_t* base, int row, int c0) {
   return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
+// Write a bf16 output tile staged in LDS (kBM rows of kBN values, row pitch
+// kCPitch bytes) to c[row0 + r][n0 ..] (row length N), its first `rows`
+// rows and `ncols` columns.  Thread t copies 16-byte chunk t % (kBN/8) of
+// rows t / (kBN/8), then every (kThreads / (kBN/8))-th row after it, eight
+// LDS reads in flight before their eight stores (a loop of read, wait,
+// store leaves each store behind a full LDS round trip).
+template <int kThreads, int kBM, int kBN, int kCPitch>
+__device__ __forceinline__ void store_staged_tile(const uint8_t* ct, uint16_t* c, int row0,
+                                                  int rows, int N, int n0, int ncols, int tid) {
+  constexpr int kChunks = kBN * 2 / 16;
+  constexpr int kRowStep = kThreads / kChunks;
+  static_assert(kThreads % kChunks == 0 && (kBM / kRowStep) % 8 == 0, "store_staged_tile shape");
+  const int ch = tid % kChunks, rt = tid / kChunks;
+  const bool ch_ok = ch * 8 < ncols;
+  uint8_t* dst = (uint8_t*)(c + (size_t)(row0 + rt) * N + n0) + ch * 16;
+  const size_t dstep = (size_t)kRowStep * N * 2;
+  const uint8_t* src = ct + rt * kCPitch + ch * 16;
+#pragma unroll
+  for (int i0 = 0; i0 < kBM / kRowStep; i0 += 8) {
+    uint4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = *(const uint4*)(src + (i0 + u) * kRowStep * kCPitch);
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (ch_ok && rt + (i0 + u) * kRowStep < rows) *(uint4*)(dst + (size_t)(i0 + u) * dstep) = v[u];
+  }
+}
 
 }  // namespace smoe
