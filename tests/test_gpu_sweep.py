@@ -9,7 +9,9 @@ float64 oracle to finish in well under a second:
 - the grouped GEMM, plain, packed and E8M0 (where the shape allows each):
   within the GEMM bar of the oracle on every row;
 - the variable-K weight-gradient GEMM, C3 and E8M0 operands: within the GEMM
-  bar, and zero for experts with no rows.
+  bar, and zero for experts with no rows;
+- the byte-moving stages (permute + quantise, SwiGLU + quantise, the column
+  quantiser, the combine and both halves of its backward): bit-exact.
 """
 import numpy as np
 import pytest
@@ -151,3 +153,59 @@ def test_sweep_wgrad(dev, seed):
             if counts[e] == 0:
                 assert not got[e].any(), f"expert {e} has no rows but a non-zero gradient"
         close(got, ref, f"wgrad seed {seed} pow2={pow2}")
+
+
+DATA_SEEDS = list(range(8))
+
+
+@pytest.mark.parametrize("seed", DATA_SEEDS)
+def test_sweep_data_path(dev, seed):
+    """Permute + quantise, SwiGLU + quantise, the combine, the column
+    quantiser and the combine backward (both halves), all bit-exact, on a
+    random routing of random sizes (widths a multiple of 16, so the short
+    last 128-group of the C9 rule shows up too), C3 and C10 scales."""
+    rng = np.random.default_rng(800 + seed)
+    E = int(rng.choice([1, 3, 8, 33, 128]))
+    K = int(rng.integers(1, min(E, 8) + 1))
+    T = int(rng.integers(1, 900))
+    H = 16 * int(rng.integers(1, 97))
+    I = 16 * int(rng.integers(1, 49))
+    say("data path", seed, T, E, K, H, I)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    idx, w = ops.router_topk(torch.from_numpy(logits).to(dev), K)
+    row_map, inv_map, _, offsets = ops.route_sort(idx, E)
+    inv = inv_map.cpu().numpy()
+    off = offsets.cpu().numpy()
+    w_np = w.cpu().numpy()
+    R = T * K
+    x = W.tokens(T, H, device=dev, seed=900 + seed)
+    y = W.tokens(R, H, device=dev, seed=1000 + seed)
+    c1 = W.tokens(R, 2 * I, device=dev, seed=1100 + seed)
+    dout = W.tokens(T, H, device=dev, seed=1200 + seed)
+    for pow2 in (False, True):
+        scale = "pow2" if pow2 else "amax"
+        xq, xs = ops.permute_quant_rows(x, inv_map, K, scale=scale)
+        rq, rs = O.permute_quant(u16(x), inv, K, pow2=pow2)
+        assert np.array_equal(u8(xq), rq) and np.array_equal(xs.cpu().numpy(), rs), "permute"
+        hq, hs = ops.swiglu_quant(c1, scale=scale)
+        rq, rs = O.swiglu_quant(u16(c1), pow2=pow2)
+        assert np.array_equal(u8(hq), rq) and np.array_equal(hs.cpu().numpy(), rs), "swiglu"
+        cq, cs, pad, _ = ops.quant_cols(y, offsets, col_scale="pow2" if pow2 else "fp32")
+        rq, rs, rpad = O.quant_cols_128x1(O.bf16_to_f32(u16(y)), off, pow2=pow2)
+        Rp = int(rpad[-1])
+        assert np.array_equal(pad.cpu().numpy(), rpad)
+        assert np.array_equal(u8(cq)[:, :Rp], rq), "columns"
+        assert np.array_equal(cs.cpu().numpy()[:, :Rp // 128], rs), "column scales"
+    out = ops.unpermute_combine(y, inv_map, w)
+    assert np.array_equal(u16(out), O.unpermute_combine(u16(y), inv, w_np, K)), "combine"
+    dy, dw = ops.unpermute_combine_bwd(dout, y, inv_map, w)
+    rdy, rdw = O.combine_bwd(u16(dout), u16(y), inv, w_np, K)
+    assert np.array_equal(u16(dy), rdy), "combine backward dy"
+    close(dw.cpu().numpy(), rdw, "combine backward dw")
+    for cs_name, pow2 in (("fp32", False), ("pow2", True)):
+        tq, ts, tpad, _ = ops.combine_bwd_quant_cols(dout, row_map, w, offsets, col_scale=cs_name)
+        rq, rs, rpad = O.quant_cols_128x1(O.bf16_to_f32(rdy), off, pow2=pow2)
+        Rp = int(rpad[-1])
+        assert np.array_equal(tpad.cpu().numpy(), rpad)
+        assert np.array_equal(u8(tq)[:, :Rp], rq), "dy columns"
+        assert np.array_equal(ts.cpu().numpy()[:, :Rp // 128], rs), "dy column scales"
